@@ -1,0 +1,282 @@
+"""numpy front end of the CPU oracle (oracle/wafer_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker (or the timed CPU lane),
+never as the product path.  Raw 16-bit floats travel as numpy uint16 arrays
+holding their storage bits.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+import subprocess
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = HERE / "_build" / "liboracle.so"
+
+I8, I16, F16, BF16, I32, F32 = 0, 1, 2, 3, 4, 5
+TENSOR, NTENSOR, CX, NCX = 0, 1, 2, 3
+
+_lib = None
+
+
+def build() -> pathlib.Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        _lib = ctypes.CDLL(str(LIB_PATH))
+        _declare(_lib)
+    return _lib
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+    L.oracle_f32_to_bf16.restype = ctypes.c_uint16
+    L.oracle_f32_to_bf16.argtypes = [f32]
+    L.oracle_explp.restype = f32
+    L.oracle_explp.argtypes = [f32]
+    L.oracle_gemm_fma.restype = f32
+    L.oracle_gemm_fma.argtypes = [f32, f32, f32]
+    L.oracle_f16_to_f32.restype = f32
+    L.oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+    L.oracle_f32_to_f16.restype = i32
+    L.oracle_f32_to_f16.argtypes = [f32, ctypes.POINTER(ctypes.c_uint16)]
+    L.oracle_format_bits.argtypes = [i32]
+    L.oracle_geometry_compute.argtypes = [i32, i32, vp, i32, vp]
+    L.oracle_bit_offset.restype = i64
+    L.oracle_bit_offset.argtypes = [i32, i32, vp, i32, vp]
+    L.oracle_pack.argtypes = [i32, i32, vp, i32, vp, vp, i64]
+    L.oracle_unpack.argtypes = [i32, i32, vp, i32, vp, i64, vp]
+    L.oracle_gemm_formal.argtypes = [i32, i32, vp, vp, vp, vp, i64, i64, i64, i64, i32, i32, i32]
+    L.oracle_gemm_i8.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i32, i32]
+    L.oracle_elementwise.argtypes = [i32, i32, vp, vp, vp, i64]
+    L.oracle_convert.argtypes = [i32, i32, vp, vp, i64]
+    L.oracle_reduce.argtypes = [i32, i32, i32, vp, i32, vp, vp]
+    L.oracle_attention_prefill.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, i32, i32, i32]
+    L.oracle_attention_decode.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, i32, i32, i32]
+    L.oracle_rmsnorm.argtypes = [i32, vp, vp, vp, i64, i64, f32]
+    L.oracle_softmax.argtypes = [i32, vp, vp, i64, i64]
+    L.oracle_silu_mul.argtypes = [i32, vp, vp, vp, i64]
+    L.oracle_gelu_tanh.argtypes = [i32, vp, vp, i64]
+    L.oracle_rope.argtypes = [i32, vp, vp, i64, i64, i64, vp, f32]
+    L.oracle_bias_add.argtypes = [i32, vp, vp, vp, i64, i64]
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"oracle {what} failed with status {rc}")
+
+
+def threads() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        return os.cpu_count() or 1
+
+
+# ---- scalar helpers ---------------------------------------------------------
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """Vectorised RNE float32 -> bf16 bits (same rule as oracle_f32_to_bf16)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = 0x7FC0
+    return r
+
+
+def bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def storage_dtype(fmt: int):
+    return {I8: np.int8, I16: np.int16, F16: np.uint16, BF16: np.uint16, I32: np.int32, F32: np.float32,
+            6: np.uint32, 8: np.uint8, 9: np.uint16, 10: np.uint32, 11: np.int64, 12: np.uint64}[fmt]
+
+
+def to_float(fmt: int, a: np.ndarray) -> np.ndarray:
+    if fmt == F32:
+        return np.asarray(a, dtype=np.float32)
+    if fmt == BF16:
+        return bf16_to_f32(a)
+    if fmt == F16:
+        return np.asarray(a, dtype=np.uint16).view(np.float16).astype(np.float32)
+    raise ValueError(fmt)
+
+
+# ---- codec ------------------------------------------------------------------
+def geometry(fmt: int, layout: int, shape) -> dict:
+    shp = np.ascontiguousarray(shape, dtype=np.int64)
+    g = np.zeros(11, dtype=np.int64)
+    _check(lib().oracle_geometry_compute(fmt, layout, _p(shp), len(shp), _p(g)), "geometry")
+    keys = ["physical_elements", "physical_bytes", "element_bits", "c_block", "cx_blocks", "c0",
+            "aligned_c", "outer_elements", "block_outer_elements", "outer_slice_stride",
+            "bank_align_elements"]
+    return dict(zip(keys, (int(v) for v in g)))
+
+
+def bit_offset(fmt: int, layout: int, shape, index) -> int:
+    shp = np.ascontiguousarray(shape, dtype=np.int64)
+    idx = np.ascontiguousarray(index, dtype=np.int64)
+    return int(lib().oracle_bit_offset(fmt, layout, _p(shp), len(shp), _p(idx)))
+
+
+def pack(fmt: int, layout: int, shape, logical: np.ndarray, template: np.ndarray) -> np.ndarray:
+    shp = np.ascontiguousarray(shape, dtype=np.int64)
+    out = np.array(template, dtype=np.uint8, copy=True)
+    src = np.ascontiguousarray(logical)
+    _check(lib().oracle_pack(fmt, layout, _p(shp), len(shp), _p(src), _p(out), out.size), "pack")
+    return out
+
+
+def unpack(fmt: int, layout: int, shape, storage: np.ndarray) -> np.ndarray:
+    shp = np.ascontiguousarray(shape, dtype=np.int64)
+    st = np.ascontiguousarray(storage, dtype=np.uint8)
+    count = int(np.prod(shp)) if len(shp) else 1
+    dt = np.uint8 if fmt == 7 else storage_dtype(fmt)
+    out = np.zeros(count, dtype=dt)
+    _check(lib().oracle_unpack(fmt, layout, _p(shp), len(shp), _p(st), st.size, _p(out)), "unpack")
+    return out.reshape(tuple(shape))
+
+
+# ---- GEMMs ------------------------------------------------------------------
+def gemm_formal(in_fmt, out_fmt, lhs, rhs, m, k, n, batch=1, psum=None, lhs_t=False, rhs_t=False, nthreads=None):
+    dst = np.zeros(batch * m * n, dtype=storage_dtype(out_fmt))
+    lhs = np.ascontiguousarray(lhs)
+    rhs = np.ascontiguousarray(rhs)
+    ps = None if psum is None else np.ascontiguousarray(psum, dtype=np.float32)
+    _check(lib().oracle_gemm_formal(in_fmt, out_fmt, _p(lhs), _p(rhs), _p(ps), _p(dst), m, k, n, batch,
+                                    int(lhs_t), int(rhs_t), nthreads or threads()), "gemm")
+    return dst
+
+
+def gemm_i8(a, b, scale, m, k, n, rhs_t=False, nthreads=None, want_acc=True):
+    a = np.ascontiguousarray(a, dtype=np.int8)
+    b = np.ascontiguousarray(b, dtype=np.int8)
+    scale = np.ascontiguousarray(scale, dtype=np.float32)
+    acc = np.zeros((m, n), dtype=np.int32) if want_acc else None
+    y = np.zeros((m, n), dtype=np.uint16)
+    _check(lib().oracle_gemm_i8(_p(a), _p(b), _p(scale), _p(acc), _p(y), m, k, n, int(rhs_t),
+                                nthreads or threads()), "gemm_i8")
+    return acc, y
+
+
+# ---- managed lane -----------------------------------------------------------
+def elementwise(op: int, fmt: int, a, b=None):
+    a = np.ascontiguousarray(a)
+    b = None if b is None else np.ascontiguousarray(b)
+    out = np.zeros(a.size, dtype=storage_dtype(fmt))
+    _check(lib().oracle_elementwise(op, fmt, _p(a), _p(b), _p(out), a.size), "elementwise")
+    return out.reshape(a.shape)
+
+
+def convert(opcode: int, src, dst_fmt: int):
+    src = np.ascontiguousarray(src)
+    out = np.zeros(src.size, dtype=storage_dtype(dst_fmt))
+    _check(lib().oracle_convert(opcode, 0, _p(src), _p(out), src.size), "convert")
+    return out.reshape(src.shape)
+
+
+def reduce(op: int, dim: int, fmt: int, shape, src):
+    shp = np.ascontiguousarray(shape, dtype=np.int64)
+    rank = len(shp)
+    mask = np.zeros(rank, dtype=bool)
+    if dim <= 3:
+        mask[rank - 1 - dim] = True
+    elif dim == 4:
+        mask[rank - 3] = mask[rank - 2] = True
+    else:
+        mask[rank - 3:] = True
+    out_shape = [1 if mask[i] else int(shp[i]) for i in range(rank)]
+    src = np.ascontiguousarray(src)
+    out = np.zeros(int(np.prod(out_shape)), dtype=storage_dtype(fmt))
+    _check(lib().oracle_reduce(op, dim, fmt, _p(shp), rank, _p(src), _p(out)), "reduce")
+    return out.reshape(out_shape)
+
+
+# ---- attention ----------------------------------------------------------------
+def attention_prefill(q, k, v, scale, causal=True, block_k=64, fmt=BF16, nthreads=None):
+    B, Hq, Sq, D = q.shape
+    _, Hkv, Skv, _ = k.shape
+    q, k, v = (np.ascontiguousarray(t, dtype=np.uint16) for t in (q, k, v))
+    o = np.zeros((B, Hq, Sq, D), dtype=np.uint16)
+    _check(lib().oracle_attention_prefill(fmt, _p(q), _p(k), _p(v), _p(o), B, Hq, Hkv, Sq, Skv, D,
+                                          float(scale), int(causal), block_k, nthreads or threads()),
+           "attention_prefill")
+    return o
+
+
+def attention_decode(q, k, v, scale, chunks=16, kv_len=None, block_k=64, fmt=BF16, nthreads=None):
+    B, Hq, _, D = q.shape
+    _, Hkv, cap, _ = k.shape
+    kv_len = cap if kv_len is None else kv_len
+    q, k, v = (np.ascontiguousarray(t, dtype=np.uint16) for t in (q, k, v))
+    o = np.zeros((B, Hq, 1, D), dtype=np.uint16)
+    _check(lib().oracle_attention_decode(fmt, _p(q), _p(k), _p(v), _p(o), B, Hq, Hkv, kv_len, cap, D,
+                                         float(scale), chunks, block_k, nthreads or threads()),
+           "attention_decode")
+    return o
+
+
+# ---- fused regions ----------------------------------------------------------
+def rmsnorm(x, w, eps, fmt=BF16):
+    x = np.ascontiguousarray(x)
+    w = np.ascontiguousarray(w)
+    rows, cols = int(np.prod(x.shape[:-1])), x.shape[-1]
+    y = np.zeros_like(x)
+    _check(lib().oracle_rmsnorm(fmt, _p(x), _p(w), _p(y), rows, cols, float(eps)), "rmsnorm")
+    return y
+
+
+def softmax(x, fmt=BF16):
+    x = np.ascontiguousarray(x)
+    rows, cols = int(np.prod(x.shape[:-1])), x.shape[-1]
+    y = np.zeros_like(x)
+    _check(lib().oracle_softmax(fmt, _p(x), _p(y), rows, cols), "softmax")
+    return y
+
+
+def silu_mul(g, u, fmt=BF16):
+    g = np.ascontiguousarray(g)
+    u = np.ascontiguousarray(u)
+    y = np.zeros_like(g)
+    _check(lib().oracle_silu_mul(fmt, _p(g), _p(u), _p(y), g.size), "silu_mul")
+    return y
+
+
+def gelu_tanh(x, fmt=BF16):
+    x = np.ascontiguousarray(x)
+    y = np.zeros_like(x)
+    _check(lib().oracle_gelu_tanh(fmt, _p(x), _p(y), x.size), "gelu_tanh")
+    return y
+
+
+def rope(x, positions, theta, fmt=BF16):
+    """x: [tokens, heads, D] storage array."""
+    x = np.ascontiguousarray(x)
+    pos = np.ascontiguousarray(positions, dtype=np.int32)
+    T, H, D = x.shape
+    y = np.zeros_like(x)
+    _check(lib().oracle_rope(fmt, _p(x), _p(y), T, H, D, _p(pos), float(theta)), "rope")
+    return y
+
+
+def bias_add(x, bias, fmt=F32):
+    x = np.ascontiguousarray(x)
+    b = np.ascontiguousarray(bias, dtype=np.float32)
+    rows, cols = int(np.prod(x.shape[:-1])), x.shape[-1]
+    y = np.zeros_like(x)
+    _check(lib().oracle_bias_add(fmt, _p(x), _p(b), _p(y), rows, cols), "bias_add")
+    return y
