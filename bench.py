@@ -1,0 +1,263 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 numeric backend on BASELINE.json's headline metric.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fa,fd,i8,mlp]
+
+One step = one launch of the hot path over one batch of synthetic, seeded
+input already resident in HBM.  The headline (`value`) is the FA prefill
+config (bf16 Q,K,V [1,16,2048,128], causal) in TFLOP/s of
+algorithmic (causal, visible-pair) work; FD decode (config 2), the int8 GEMM
+(config 3) and the fp32 MLP block (config 0) are reported in `secondary`,
+each with its own roofline fraction and CPU baseline.  Timing: W untimed
+launches, then exactly K launches between two HIP events recorded on the
+stream the kernels run on (torch's current stream, which the backend binds).
+
+cpu_baseline: the CPU oracle (oracle/, a C restatement of the Reference
+backend's semantics, test infrastructure) timed on this host's cores over a
+bounded sample of the same workload, scaled to the metric's unit.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK = {"bf16": 2500.0, "i8": 5000.0, "f32": 157.3, "hbm": 8000.0}  # TFLOP/s, TOP/s, GB/s
+
+FA_SHAPE = (1, 16, 2048, 128)
+FA_FLOPS = 4 * 16 * 128 * (2048 * 2049 // 2)           # 17,188,257,792
+FA_BYTES = 4 * 1 * 16 * 2048 * 128 * 2                  # Q, K, V, O
+FD_B, FD_HQ, FD_HKV, FD_L, FD_D, FD_CHUNKS = 32, 32, 8, 8192, 128, 16
+FD_BYTES = 2 * FD_B * FD_HKV * FD_L * FD_D * 2 + 2 * FD_B * FD_HQ * FD_D * 2  # 1,074,266,112
+FD_FLOPS = 4 * FD_B * FD_HQ * FD_L * FD_D
+I8_N = 4096
+I8_OPS = 2 * I8_N ** 3
+MLP_FLOPS = 2 * 128 * 512 * 2048 * 2
+SEED = 20260803
+
+
+def cores() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        return os.cpu_count() or 1
+
+
+def traffic_for(kernel: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, calibrated against a copy kernel), if committed."""
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        return json.loads(f.read_text()).get(kernel, {}).get("bytes_per_launch")
+    except (ValueError, OSError):
+        return None
+
+
+def timed(torch, fn, steps: int, warmup: int) -> float:
+    """Average milliseconds per launch over exactly `steps` launches."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def rnd_bf16(torch, gen, shape):
+    return torch.randn(shape, device="cuda", generator=gen).to(torch.bfloat16)
+
+
+# ---------------------------------------------------------------- workloads
+def bench_fa(torch, hip, steps, warmup, with_cpu=True):
+    gen = torch.Generator(device="cuda").manual_seed(SEED)
+    q, k, v = (rnd_bf16(torch, gen, FA_SHAPE) for _ in range(3))
+    o = torch.empty(FA_SHAPE, dtype=torch.bfloat16, device="cuda")
+    scale = 1.0 / math.sqrt(FA_SHAPE[3])
+    ms = timed(torch, lambda: hip.attention_prefill(q, k, v, o, scale, causal=True), steps, warmup)
+    achieved = FA_FLOPS / (ms * 1e-3) / 1e12
+    res = {
+        "ms": ms, "value": achieved,
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK["bf16"], "unit": "TFLOP/s",
+                     "frac": achieved / PEAK["bf16"], "traffic": traffic_for("fa_prefill")},
+    }
+    if with_cpu:
+        from oracle import oracle as orc
+        heads = 4
+        qs, ks, vs = (t[:, :heads].contiguous().cpu().view(torch.int16).numpy().view("uint16") for t in (q, k, v))
+        t0 = time.perf_counter()
+        orc.attention_prefill(qs, ks, vs, scale, causal=True, block_k=64, nthreads=cores())
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": (FA_FLOPS * heads / 16) / dt / 1e12, "unit": "TFLOP/s", "cores": cores(),
+                               "kind": "port",
+                               "sample": f"{heads} of 16 heads of the same causal [2048,128] bf16 prefill "
+                                         f"(block_k 64), {dt:.2f} s wall"}
+    return res
+
+
+def bench_fd(torch, hip, steps, warmup, with_cpu=True):
+    gen = torch.Generator(device="cuda").manual_seed(SEED)
+    q = rnd_bf16(torch, gen, (FD_B, FD_HQ, 1, FD_D))
+    k = rnd_bf16(torch, gen, (FD_B, FD_HKV, FD_L, FD_D))
+    v = rnd_bf16(torch, gen, (FD_B, FD_HKV, FD_L, FD_D))
+    o = torch.empty((FD_B, FD_HQ, 1, FD_D), dtype=torch.bfloat16, device="cuda")
+    scale = 1.0 / math.sqrt(FD_D)
+    ms = timed(torch, lambda: hip.attention_decode(q, k, v, o, scale, chunks=FD_CHUNKS), steps, warmup)
+    gbs = FD_BYTES / (ms * 1e-3) / 1e9
+    res = {
+        "workload": "FD decode bf16 Q[32,32,1,128] KV[32,8,8192,128] GQA 32/8, 16 chunks, LSE fold",
+        "metric": "HBM GB/s", "ms": ms, "value": gbs, "unit": "GB/s", "tflops": FD_FLOPS / (ms * 1e-3) / 1e12,
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK["hbm"], "unit": "GB/s",
+                     "frac": gbs / PEAK["hbm"], "traffic": traffic_for("fd_decode")},
+    }
+    if with_cpu:
+        from oracle import oracle as orc
+        nb = 8
+        qs, ks, vs = (t[:nb].contiguous().cpu().view(torch.int16).numpy().view("uint16") for t in (q, k, v))
+        t0 = time.perf_counter()
+        orc.attention_decode(qs, ks, vs, scale, chunks=FD_CHUNKS, block_k=64, nthreads=cores())
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": (FD_BYTES * nb / FD_B) / dt / 1e9, "unit": "GB/s", "cores": cores(),
+                               "kind": "port",
+                               "sample": f"{nb} of 32 sequences of the same decode, {dt:.2f} s wall"}
+    return res
+
+
+def bench_i8(torch, hip, steps, warmup, with_cpu=True):
+    gen = torch.Generator(device="cuda").manual_seed(SEED)
+    n = I8_N
+    a = torch.randint(-127, 128, (n, n), device="cuda", generator=gen, dtype=torch.int8)
+    b = torch.randint(-127, 128, (n, n), device="cuda", generator=gen, dtype=torch.int8)
+    scale = torch.rand(n, device="cuda", generator=gen) * 0.009 + 0.001
+    y = torch.empty((n, n), dtype=torch.bfloat16, device="cuda")
+    ms = timed(torch, lambda: hip.gemm_i8(a, b, scale, y, n, n, n), steps, warmup)
+    tops = I8_OPS / (ms * 1e-3) / 1e12
+    res = {
+        "workload": "int8 GEMM 4096^3 (rhs [K,N]), exact int32 accumulate, per-column f32 dequant, bf16 out",
+        "metric": "TOP/s", "ms": ms, "value": tops, "unit": "TOP/s",
+        "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK["i8"], "unit": "TOP/s",
+                     "frac": tops / PEAK["i8"], "traffic": traffic_for("gemm_i8")},
+    }
+    if with_cpu:
+        from oracle import oracle as orc
+        rows = 256
+        an, bn, sn = a[:rows].cpu().numpy(), b.cpu().numpy(), scale.cpu().numpy()
+        t0 = time.perf_counter()
+        orc.gemm_i8(an, bn, sn, rows, n, n, nthreads=cores(), want_acc=False)
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": (2 * rows * n * n) / dt / 1e12, "unit": "TOP/s", "cores": cores(),
+                               "kind": "port", "sample": f"{rows} of 4096 output rows, {dt:.2f} s wall"}
+    return res
+
+
+def bench_mlp(torch, hip, B, steps, warmup, with_cpu=True):
+    gen = torch.Generator(device="cuda").manual_seed(SEED)
+    x = torch.randn((128, 512), device="cuda", generator=gen)
+    w1 = torch.randn((512, 2048), device="cuda", generator=gen) / math.sqrt(512)
+    b1 = torch.randn(2048, device="cuda", generator=gen) * 0.02
+    w2 = torch.randn((2048, 512), device="cuda", generator=gen) / math.sqrt(2048)
+    b2 = torch.randn(512, device="cuda", generator=gen) * 0.02
+    hbuf = torch.empty((128, 2048), device="cuda")
+    y = torch.empty((128, 512), device="cuda")
+
+    def step():
+        hip.gemm(x, w1, hbuf, 128, 512, 2048)
+        hip.bias_add(hbuf, b1, hbuf, fmt=B.F32)
+        hip.gelu_tanh(hbuf, hbuf, fmt=B.F32)
+        hip.gemm(hbuf, w2, y, 128, 2048, 512)
+        hip.bias_add(y, b2, y, fmt=B.F32)
+
+    ms = timed(torch, step, steps, warmup)
+    tf = MLP_FLOPS / (ms * 1e-3) / 1e12
+    res = {
+        "workload": "fp32 MLP block x[128,512] W1[512,2048] W2[2048,512] tanh-GELU, formal (bit-exact) GEMM order",
+        "metric": "TFLOP/s", "ms": ms, "value": tf, "unit": "TFLOP/s",
+        "roofline": {"bound": "valu-f32", "achieved": tf, "peak": PEAK["f32"], "unit": "TFLOP/s",
+                     "frac": tf / PEAK["f32"], "traffic": None},
+    }
+    if with_cpu:
+        from oracle import oracle as orc
+        xn, w1n, w2n, b1n, b2n = (t.cpu().numpy() for t in (x, w1, w2, b1, b2))
+        t0 = time.perf_counter()
+        h1 = orc.gemm_formal(5, 5, xn, w1n, 128, 512, 2048, nthreads=cores()).reshape(128, 2048)
+        h1 = orc.gelu_tanh(orc.bias_add(h1, b1n), fmt=5)
+        orc.bias_add(orc.gemm_formal(5, 5, h1, w2n, 128, 2048, 512, nthreads=cores()).reshape(128, 512), b2n)
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": MLP_FLOPS / dt / 1e12, "unit": "TFLOP/s", "cores": cores(),
+                               "kind": "port", "sample": f"the whole block, {dt:.2f} s wall"}
+    return res
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--only", default="fa,fd,i8,mlp", help="comma list of fa, fd, i8, mlp")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this backend runs on one GPU; --gpus {args.gpus} is not a configuration it "
+              "measures (the multi-GPU sharding is a design note only)", file=sys.stderr)
+        return 2
+
+    import torch
+    from vibe_compiler_amd import backend as B
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    hip = B.Context(0)
+    only = set(args.only.split(","))
+    with_cpu = not args.no_cpu
+    secondary = []
+    fa = None
+    if "fa" in only:
+        fa = bench_fa(torch, hip, args.steps, args.warmup, with_cpu)
+    if "fd" in only:
+        secondary.append(dict(name="fd_decode", **bench_fd(torch, hip, args.steps, args.warmup, with_cpu)))
+    if "i8" in only:
+        secondary.append(dict(name="gemm_i8", **bench_i8(torch, hip, args.steps, args.warmup, with_cpu)))
+    if "mlp" in only:
+        secondary.append(dict(name="mlp_fp32", **bench_mlp(torch, hip, B, args.steps, args.warmup, with_cpu)))
+    hip.close()
+
+    line = {
+        "metric": "FA prefill TFLOP/s + FD decode HBM GB/s (% of roofline), 1\u00d7MI355X",
+        "value": fa["value"] if fa else None,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": fa["ms"] if fa else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 inputs resident in HBM)",
+        "config": {"workload": "FA prefill bf16 Q,K,V [1,16,2048,128] causal, scale 1/sqrt(128), "
+                               "fp32 online softmax, bf16 out",
+                   "batch": 1, "heads": 16, "seq_len": 2048, "head_dim": 128, "causal": True},
+        "roofline": fa["roofline"] if fa else None,
+        "cpu_baseline": fa.get("cpu_baseline") if fa else None,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

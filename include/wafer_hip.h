@@ -1,0 +1,230 @@
+/*
+ * wafer_hip.h -- C ABI of the MI355X (gfx950) numeric execution backend for
+ * the kernels the Wafer compiler emits.
+ *
+ * The backend sits beside the reference's Reference (formal / managed) and
+ * oneDNN CPU lanes.  Every entry point is `extern "C"`, takes plain device
+ * pointers and sizes, and returns an int status (WAFER_HIP_OK == 0, negative
+ * on failure; wafer_hip_last_error() then holds a message for the calling
+ * thread).  No entry point falls back to a CPU path: a request the HIP
+ * kernels cannot serve fails with WAFER_HIP_E_UNSUPPORTED.
+ *
+ * Memory: all tensor pointers are device pointers owned by the caller.  Work
+ * is enqueued on the context's stream (wafer_hip_set_stream) and is
+ * stream-ordered; wafer_hip_synchronize() waits for it.  Logical tensors are
+ * dense row-major; raw 16-bit floats are passed as their storage bits.
+ *
+ * Format codes are the reference's Data_Format table
+ * (lib/Wafer/Target/TargetFormat.cpp:62-63): I8=0 I16=1 F16=2 BF16=3 I32=4
+ * F32=5 TF32=6 Bool=7 U8=8 U16=9 U32=10 I64=11 U64=12.
+ */
+#ifndef WAFER_HIP_H
+#define WAFER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes --------------------------------------------------------
+ * Negative images of TargetModelKernelErrorCode
+ * (include/Wafer/Simulator/Kernel/TargetModelKernel.h:21-32) plus the HIP
+ * runtime failure this backend adds. */
+enum {
+  WAFER_HIP_OK = 0,
+  WAFER_HIP_E_INVALID_FIELD = -1,     /* InvalidCommandField */
+  WAFER_HIP_E_BUDGET = -2,            /* WorkBudgetExceeded */
+  WAFER_HIP_E_UNSUPPORTED = -3,       /* UnsupportedCommand */
+  WAFER_HIP_E_MEMORY = -4,            /* MemoryReadFailure */
+  WAFER_HIP_E_NUMERIC = -5,           /* FormalNumericFailure */
+  WAFER_HIP_E_CODEC = -6,             /* PhysicalCodecFailure */
+  WAFER_HIP_E_UNAVAILABLE = -7,       /* ...BackendUnavailable */
+  WAFER_HIP_E_RUNTIME = -8            /* a HIP runtime call failed */
+};
+
+/* Format codes (TargetFormat.cpp:62-63). */
+enum {
+  WAFER_FMT_I8 = 0, WAFER_FMT_I16 = 1, WAFER_FMT_F16 = 2, WAFER_FMT_BF16 = 3,
+  WAFER_FMT_I32 = 4, WAFER_FMT_F32 = 5, WAFER_FMT_TF32 = 6, WAFER_FMT_BOOL = 7,
+  WAFER_FMT_U8 = 8, WAFER_FMT_U16 = 9, WAFER_FMT_U32 = 10, WAFER_FMT_I64 = 11,
+  WAFER_FMT_U64 = 12
+};
+
+/* Physical layouts (PhysicalTensorDescriptor layout kinds,
+ * lib/Wafer/Target/PhysicalTensor/PhysicalLayout.cpp:111-200). */
+enum { WAFER_LAYOUT_TENSOR = 0, WAFER_LAYOUT_NTENSOR = 1, WAFER_LAYOUT_CX = 2,
+       WAFER_LAYOUT_NCX = 3 };
+
+/* TargetGemmOrientation (include/Wafer/Target/TargetFormat.h:92). */
+enum { WAFER_GEMM_NORMAL = 0, WAFER_GEMM_TRANSPOSE = 1 };
+
+/* kDisabledGemmPartialFormat (include/Wafer/Target/TargetCall.h:72). */
+#define WAFER_GEMM_PSUM_DISABLED 13u
+
+typedef struct wafer_hip_context wafer_hip_context;
+
+/* ---- context ------------------------------------------------------------
+ * Replaces the construction of a numeric backend object once per run
+ * (tools/wafer-compile/wafer-compile.cpp:477-506).  A context binds one HIP
+ * device and one stream (the null stream until set).  Calls on one context
+ * are serialised by the caller, as SystemCTargetModel::issue serialises
+ * backend calls (lib/Wafer/Simulator/SystemC/SystemCTargetModel.cpp:156-185). */
+int wafer_hip_context_create(int device, wafer_hip_context **out);
+int wafer_hip_context_destroy(wafer_hip_context *ctx);
+int wafer_hip_set_stream(wafer_hip_context *ctx, void *hip_stream);
+int wafer_hip_synchronize(wafer_hip_context *ctx);
+const char *wafer_hip_last_error(void);
+/* Implementation string, the analogue of the evidence `implementation`
+ * field (include/Wafer/Simulator/Kernel/TargetModelKernel.h:144-182). */
+const char *wafer_hip_implementation(void);
+
+/* ---- per-command GEMM (formal semantics, bit-exact) ----------------------
+ * Replaces wafer_tx81_gemm_oriented (runtime/crt/include/wafer_tx81_crt.h:44-49)
+ * as executed by the formal lane, executeGemm
+ * (lib/Wafer/Simulator/Reference/Numeric/FormalTensorNumeric.cpp:272-361):
+ * for each output, acc = +0; for k in order acc = fma(widen(lhs), widen(rhs),
+ * acc) with one RNE rounding; acc += psum (F32 add) when psum_format != 13;
+ * dst = RNE(acc -> out_format).  lhs is [batch, m, k] (Transpose: [batch, k, m]),
+ * rhs is [batch, k, n] (Transpose: [batch, n, k]), dst/psum [batch, m, n].
+ * in_format/out_format in {F16, BF16, F32}; psum_format F32 or 13. */
+int wafer_hip_gemm(wafer_hip_context *ctx, const void *lhs, const void *rhs,
+                   void *dst, const void *psum, uint32_t m, uint32_t k,
+                   uint32_t n, uint32_t batch, uint32_t in_format,
+                   uint32_t out_format, uint32_t psum_format,
+                   uint32_t lhs_orientation, uint32_t rhs_orientation);
+
+/* ---- MFMA GEMM (bf16/f16 in, f32 accumulate; tolerance parity) ------------
+ * The throughput path for large region-level GEMMs.  Same operand meaning as
+ * wafer_hip_gemm with lhs Normal; the MFMA accumulation order differs from
+ * the formal k-order, so results match the formal lane within tolerance.
+ * out_format F32 or the input format.  m, n multiples of 256 / 128 and k a
+ * multiple of 64 are served; other shapes return WAFER_HIP_E_UNSUPPORTED. */
+int wafer_hip_gemm_mfma(wafer_hip_context *ctx, const void *lhs,
+                        const void *rhs, void *dst, uint32_t m, uint32_t k,
+                        uint32_t n, uint32_t in_format, uint32_t out_format,
+                        uint32_t rhs_orientation);
+
+/* ---- int8 GEMM -------------------------------------------------------------
+ * No reference implementation exists (the formal and oneDNN lanes reject I8:
+ * lib/Wafer/Simulator/Reference/Formal/FormalNumericValidation.cpp:78-83,
+ * lib/Wafer/Simulator/OneDNN/OneDNNGemmAdapter.cpp:42-52); this follows the
+ * closed form on the reference's routes: acc = sum_k int32(a)*int32(b) exactly,
+ * y = bf16_RNE(f32_RNE(f32_RNE(acc) * scale[n])) (int32_fp32 route, CT Mul,
+ * fp32_bf16 route; lib/Wafer/Target/TargetFormat.cpp:174,192).
+ * a [m,k] i8, b [k,n] i8 (Transpose: [n,k]), scale [n] f32, y [m,n] bf16;
+ * acc_out [m,n] i32 may be NULL.  k <= 133152 keeps |acc| < 2^31. */
+int wafer_hip_gemm_i8(wafer_hip_context *ctx, const int8_t *a, const int8_t *b,
+                      const float *scale, int32_t *acc_out, uint16_t *y,
+                      uint32_t m, uint32_t k, uint32_t n,
+                      uint32_t rhs_orientation);
+
+/* ---- managed-reference elementwise / convert / reduce ---------------------
+ * Replace TargetModelManagedReferenceBackend::execute
+ * (include/Wafer/Simulator/Kernel/TargetModelKernel.h:187-200) on logical
+ * (unpacked) tensors.  op is TargetElementwiseOperation
+ * (include/Wafer/Target/TargetOperation.h:58-93); the float expressions follow
+ * evaluateElementwise (lib/Wafer/Simulator/Reference/ManagedReferenceTargetModel.cpp:230-299).
+ * in1 is ignored for unary ops. */
+int wafer_hip_elementwise(wafer_hip_context *ctx, uint32_t op, uint32_t format,
+                          const void *in0, const void *in1, void *dst,
+                          uint64_t count);
+/* opcode is a convert route of the Data_Format route table
+ * (lib/Wafer/Target/TargetFormat.cpp:164-196), rounding TargetRoundingMode
+ * (include/Wafer/Target/TargetOperation.h:175-181); NearestEven only. */
+int wafer_hip_convert(wafer_hip_context *ctx, uint32_t opcode,
+                      uint32_t rounding, const void *src, void *dst,
+                      uint64_t count);
+/* op TargetReduceOperation {Sum, Max, Min} and dim TargetReduceDimension
+ * (TargetOperation.h:102-113); shape is the logical shape (rank <= 8) and dst
+ * holds the shape with reduced dimensions set to 1. */
+int wafer_hip_reduce(wafer_hip_context *ctx, uint32_t op, uint32_t dim,
+                     uint32_t format, const int64_t *shape, uint32_t rank,
+                     const void *src, void *dst);
+
+/* ---- physical codec (bit-exact) --------------------------------------------
+ * Replace packPhysicalTensorLogicalValues / unpackPhysicalTensorLogicalValues
+ * (lib/Wafer/Target/PhysicalTensor/PhysicalTensorCodec.cpp:156-226) with the
+ * geometry of computePhysicalTensorGeometry (PhysicalLayout.cpp:111-200).
+ * pack writes only the bytes logical elements own: the caller preloads
+ * storage with the destination template. */
+int wafer_hip_physical_bytes(uint32_t format, uint32_t layout,
+                             const int64_t *shape, uint32_t rank,
+                             int64_t *bytes);
+int wafer_hip_pack(wafer_hip_context *ctx, uint32_t format, uint32_t layout,
+                   const int64_t *shape, uint32_t rank, const void *logical,
+                   void *storage, int64_t storage_bytes);
+int wafer_hip_unpack(wafer_hip_context *ctx, uint32_t format, uint32_t layout,
+                     const int64_t *shape, uint32_t rank, const void *storage,
+                     int64_t storage_bytes, void *logical);
+
+/* ---- region entries: online attention ---------------------------------------
+ * FA prefill.  Semantics of the compiler's online-attention decomposition
+ * (lib/Wafer/Transforms/Linalg/OnlineAttentionDecomposition.cpp:568-597,
+ * finalize OnlineAttentionMaterialization.cpp:197-262): per KV block,
+ * S = f32(q).f32(k) * scale (+ 0/-inf causal bias), m' = max(m, rowmax S),
+ * alpha = ExpLp(m - m'), P = ExpLp(S - m'), l = l*alpha + rowsum(P),
+ * acc = acc*alpha + bf16(P).V, out = narrow(acc * (1/l)).
+ * q [batch, q_heads, q_len, head_dim], k/v [batch, kv_heads, kv_len, head_dim],
+ * o like q; q_heads % kv_heads == 0 (GQA: q head h reads kv head
+ * h / (q_heads/kv_heads)).  Causal: query i sees key j iff j <= i.
+ * format BF16; head_dim 128; q_len a multiple of 128, kv_len of 64. */
+int wafer_hip_attention_prefill(wafer_hip_context *ctx, uint32_t format,
+                                const void *q, const void *k, const void *v,
+                                void *o, uint32_t batch, uint32_t q_heads,
+                                uint32_t kv_heads, uint32_t q_len,
+                                uint32_t kv_len, uint32_t head_dim,
+                                float scale, uint32_t causal);
+
+/* FD decode: one query token per sequence.  Each of `chunks` KV chunks gets
+ * its own online state, then the states are folded left to right
+ * (lib/Wafer/Transforms/Linalg/SpatialRegionMaterialization.cpp:2391-2430,
+ * merge OnlineAttentionMaterialization.cpp:264-373) and finalised as FA.
+ * q [batch, q_heads, 1, head_dim]; k/v caches [batch, kv_heads, kv_capacity,
+ * head_dim] of which the first kv_len tokens are valid; o like q.
+ * format BF16; head_dim 128; q_heads/kv_heads in {1, 2, 4, 8}.
+ * The context owns the partial-state workspace. */
+int wafer_hip_attention_decode(wafer_hip_context *ctx, uint32_t format,
+                               const void *q, const void *k_cache,
+                               const void *v_cache, void *o, uint32_t batch,
+                               uint32_t q_heads, uint32_t kv_heads,
+                               uint32_t kv_len, uint32_t kv_capacity,
+                               uint32_t head_dim, float scale,
+                               uint32_t chunks);
+
+/* ---- region entries: fused TileRegions ----------------------------------------
+ * Compositions of the managed elementwise / reduce commands with the op
+ * mapping of getInstrElementwiseKindAttr
+ * (lib/Wafer/Conversion/TileToInstr/ComputeLowering.cpp:2555-2606: Exp ->
+ * ExpLp, Div -> Recip then Mul, no tile-level Sigmoid).  F32 intermediates,
+ * one narrowing at the region output.  format F32, BF16 or F16. */
+/* y = x * Rsqrt(Sum(x*x) * (1/cols) + eps) * w, per row. */
+int wafer_hip_rmsnorm(wafer_hip_context *ctx, uint32_t format, const void *x,
+                      const void *w, void *y, uint64_t rows, uint64_t cols,
+                      float eps);
+/* e = ExpLp(x - rowmax); y = e * Recip(Sum(e)). */
+int wafer_hip_softmax(wafer_hip_context *ctx, uint32_t format, const void *x,
+                      void *y, uint64_t rows, uint64_t cols);
+/* y = g * Recip(1 + ExpLp(-g)) * u. */
+int wafer_hip_silu_mul(wafer_hip_context *ctx, uint32_t format,
+                       const void *gate, const void *up, void *y,
+                       uint64_t count);
+/* y = 0.5*x*(1 + Tanh(sqrt(2/pi)*(x + 0.044715*x^3))). */
+int wafer_hip_gelu_tanh(wafer_hip_context *ctx, uint32_t format, const void *x,
+                        void *y, uint64_t count);
+/* Rotate-half RoPE over x [tokens, heads, head_dim] with positions [tokens]
+ * (int32, device) and inv_freq[i] = 1/theta^(2i/head_dim). */
+int wafer_hip_rope(wafer_hip_context *ctx, uint32_t format, const void *x,
+                   void *y, uint64_t tokens, uint64_t heads,
+                   uint64_t head_dim, const int32_t *positions, float theta);
+/* y = x + bias (bias F32 [cols], broadcast over rows). */
+int wafer_hip_bias_add(wafer_hip_context *ctx, uint32_t format, const void *x,
+                       const float *bias, void *y, uint64_t rows,
+                       uint64_t cols);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WAFER_HIP_H */

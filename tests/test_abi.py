@@ -1,0 +1,63 @@
+"""CPU checks of the C ABI: the library loads without a GPU, exports every
+function include/wafer_hip.h declares, rejects bad arguments before any HIP
+call, and its host-side geometry matches the oracle."""
+import ctypes
+import pathlib
+import re
+
+import numpy as np
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+
+
+def declared_functions():
+    text = (ROOT / "include" / "wafer_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(wafer_hip_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_exports():
+    from vibe_compiler_amd import backend
+
+    assert declared_functions() == sorted(backend.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    from vibe_compiler_amd import backend
+
+    lib = backend.load()
+    for name in declared_functions():
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
+    assert "gfx950" in backend.implementation()
+
+
+def test_no_gpu_means_a_loud_error():
+    import torch
+
+    from vibe_compiler_amd import backend
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(backend.WaferHipError) as e:
+        backend.Context(0)
+    assert e.value.status in (-7, -8)
+
+
+def test_null_context_and_fields_are_rejected():
+    from vibe_compiler_amd import backend
+
+    L = backend.load()
+    assert L.wafer_hip_gemm(None, None, None, None, None, 1, 1, 1, 1, 5, 5, 13, 0, 0) == -1
+    assert L.wafer_hip_synchronize(None) == -1
+    assert b"null context" in L.wafer_hip_last_error()
+
+
+@pytest.mark.parametrize("fmt", [0, 2, 3, 5, 11])
+@pytest.mark.parametrize("layout", [0, 1, 2, 3])
+@pytest.mark.parametrize("shape", [[5], [3, 1], [2, 3, 33], [1, 2, 3, 1025], [2, 2, 130], [3, 96], [2, 1, 129],
+                                   [3, 160], [3, 200], [0, 7]])
+def test_physical_bytes_matches_oracle(oracle, fmt, layout, shape):
+    from vibe_compiler_amd import backend
+
+    assert backend.physical_bytes(fmt, layout, shape) == oracle.geometry(fmt, layout, shape)["physical_bytes"]

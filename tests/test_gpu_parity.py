@@ -1,0 +1,542 @@
+"""GPU parity: the HIP kernels, called through the C ABI, against the CPU
+oracle on identical seeded inputs (bit-exact where the semantics are
+order-free or order-preserving, the reference's attention gate otherwise),
+and at BASELINE sizes through size-independent properties.
+
+Tolerances stated here:
+  * formal GEMM, int8 GEMM, exact elementwise ops, convert, ordered reduce,
+    codec: bit-exact;
+  * FA / FD / RMSNorm / softmax (bf16): rtol 0.006, atol 0.008,
+    cosine >= 0.9999, relative L2 <= 0.01
+    (test/Board/PyTorch/wafer_pytorch_board_cases.py:31-33);
+  * MFMA bf16 GEMM vs the formal lane: relative L2 <= 2e-3 (bf16 output
+    rounding), max |d| <= 2e-2 * max|ref|;
+  * transcendental elementwise ops (device math library vs host libm):
+    relative 2e-6 + 1e-30 absolute;
+  * fp32 MLP block: |gpu - ref| <= 1e-4 * |ref| + 1e-6.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+
+from tests.similarity import attention_gate
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def say(*a):
+    print("[gpu-case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def hip():
+    from vibe_compiler_amd import backend
+
+    ctx = backend.Context(0)
+    yield ctx
+    ctx.close()
+
+
+@pytest.fixture(scope="module")
+def B():
+    from vibe_compiler_amd import backend
+
+    return backend
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def h(s):
+    return int(s, 16)
+
+
+def f32(bits):
+    return np.array([bits], dtype=np.uint32).view(np.float32)[0]
+
+
+def u16(a):
+    """numpy uint16 -> torch int16 device tensor with the same bits."""
+    return dev(np.ascontiguousarray(a, dtype=np.uint16).view(np.int16))
+
+
+def from_u16(t):
+    return host(t).view(np.uint16)
+
+
+# ------------------------------------------------------------------ formal GEMM
+def test_formal_gemm_reference_goldens(hip, B, oracle, goldens):
+    say("formal gemm goldens")
+    for case in goldens["gemm_fma"]:
+        # k = 2 with lhs [acc, a] and rhs [1, b]: the first step widens acc
+        # exactly, the second is the single fused multiply-add under test.
+        if "a_f32" in case:
+            lhs = np.array([h(case["acc_f32"]), h(case["a_f32"])], np.uint32).view(np.float32)
+            rhs = np.array([0x3F800000, h(case["b_f32"])], np.uint32).view(np.float32)
+            fmt, ld, rd = B.F32, dev(lhs), dev(rhs)
+        else:
+            acc16 = np.array([h(case["acc_f32"])], np.uint32).view(np.float32).astype(np.float16).view(np.uint16)[0]
+            lhs = np.array([acc16, h(case["a_f16"])], np.uint16)
+            rhs = np.array([0x3C00, h(case["b_f16"])], np.uint16)
+            fmt, ld, rd = B.F16, u16(lhs), u16(rhs)
+        out = torch.zeros(1, dtype=torch.float32, device="cuda")
+        hip.gemm(ld, rd, out, 1, 2, 1, in_fmt=fmt, out_fmt=B.F32)
+        assert int(host(out).view(np.uint32)[0]) == h(case["expect_f32"]), case["cite"]
+    for case in goldens["gemm_finalize_f16"]:
+        out = torch.zeros(1, dtype=torch.int16, device="cuda")
+        hip.gemm(dev(np.array([f32(h(case["acc_f32"]))], np.float32)), dev(np.array([1.0], np.float32)), out,
+                 1, 1, 1, in_fmt=B.F32, out_fmt=B.F16)
+        assert int(from_u16(out)[0]) == h(case["expect_f16"]), case["cite"]
+    g = goldens["gemm_2x2_f16"]
+    out = torch.zeros(4, dtype=torch.int16, device="cuda")
+    hip.gemm(u16([h(x) for x in g["lhs"]]), u16([h(x) for x in g["rhs"]]), out, 2, 2, 2, in_fmt=B.F16, out_fmt=B.F16)
+    assert [int(x) for x in from_u16(out)] == [h(x) for x in g["expect"]]
+    for case in goldens["gemm_sub_ulp_partial"]["cases"]:
+        fmt = B.F16 if case["format"] == "f16" else B.BF16
+        one, eps = h(case["one"]), h(case["epsilon"])
+        out = torch.zeros(2, dtype=torch.float32, device="cuda")
+        hip.gemm(u16([one, eps, one, eps]), u16([one] * 4), out, 1, 2, 1, batch=2, in_fmt=fmt, out_fmt=B.F32)
+        assert [int(x) for x in host(out).view(np.uint32)] == [h(case["expect_f32"])] * 2
+    gp = goldens["gemm_psum_cancellation"]
+    for case in gp["cases"]:
+        fmt = B.F16 if case["format"] == "f16" else B.BF16
+        one, eps = h(case["one"]), h(case["epsilon"])
+        out = torch.zeros(2, dtype=torch.int16, device="cuda")
+        psum = dev(np.array([f32(h(gp["psum_f32"]))] * 2, np.float32))
+        hip.gemm(u16([one, eps, one, eps]), u16([one] * 4), out, 1, 2, 1, batch=2, in_fmt=fmt, out_fmt=fmt, psum=psum)
+        assert [int(x) for x in from_u16(out)] == [eps, eps]
+    g = goldens["gemm_batched_ncx_f32"]
+    out = torch.zeros(8, dtype=torch.float32, device="cuda")
+    lhs = np.array([h(x) for x in g["lhs"]], np.uint32).view(np.float32)
+    rhs = np.array([h(x) for x in g["rhs"]], np.uint32).view(np.float32)
+    hip.gemm(dev(lhs), dev(rhs), out, 2, 2, 2, batch=2)
+    assert [int(x) for x in host(out).view(np.uint32)] == [h(x) for x in g["expect"]]
+
+
+@pytest.mark.parametrize("fmt_in,fmt_out", [(5, 5), (3, 3), (2, 2), (3, 5), (2, 5), (5, 3)])
+@pytest.mark.parametrize("lt,rt", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_formal_gemm_bit_exact_random(hip, B, oracle, fmt_in, fmt_out, lt, rt):
+    say("formal gemm random", fmt_in, fmt_out, lt, rt)
+    rng = np.random.default_rng(100 + fmt_in * 10 + fmt_out + 4 * lt + 2 * rt)
+    for (m, k, n, batch, with_psum) in [(37, 70, 65, 2, True), (128, 129, 3, 1, False), (1, 300, 1, 3, True)]:
+        a = rng.standard_normal((batch, m, k)).astype(np.float32)
+        b = rng.standard_normal((batch, k, n)).astype(np.float32)
+        if lt:
+            a = np.ascontiguousarray(np.swapaxes(a, 1, 2))
+        if rt:
+            b = np.ascontiguousarray(np.swapaxes(b, 1, 2))
+        if fmt_in == B.F32:
+            ah, bh = a, b
+            ad, bd = dev(a), dev(b)
+        elif fmt_in == B.BF16:
+            ah, bh = oracle.f32_to_bf16(a).reshape(a.shape), oracle.f32_to_bf16(b).reshape(b.shape)
+            ad, bd = u16(ah), u16(bh)
+        else:
+            ah, bh = a.astype(np.float16).view(np.uint16), b.astype(np.float16).view(np.uint16)
+            ad, bd = u16(ah), u16(bh)
+        ps = rng.standard_normal((batch, m, n)).astype(np.float32) if with_psum else None
+        ref = oracle.gemm_formal(fmt_in, fmt_out, ah, bh, m, k, n, batch=batch, psum=ps, lhs_t=bool(lt), rhs_t=bool(rt))
+        if fmt_out == B.F32:
+            out = torch.zeros(batch * m * n, dtype=torch.float32, device="cuda")
+        else:
+            out = torch.zeros(batch * m * n, dtype=torch.int16, device="cuda")
+        hip.gemm(ad, bd, out, m, k, n, batch=batch, in_fmt=fmt_in, out_fmt=fmt_out,
+                 psum=None if ps is None else dev(ps), lhs_t=bool(lt), rhs_t=bool(rt))
+        got = host(out)
+        assert np.array_equal(got.view(np.uint8), ref.view(np.uint8)), (m, k, n, batch)
+
+
+def test_fp32_mlp_block_config0(hip, B, oracle):
+    """x[128,512] @ W1 + b1, tanh-GELU, @ W2 + b2 (f32)."""
+    say("fp32 mlp block")
+    rng = np.random.default_rng(20260803)
+    x = rng.standard_normal((128, 512)).astype(np.float32)
+    w1 = (rng.standard_normal((512, 2048)) / math.sqrt(512)).astype(np.float32)
+    b1 = (rng.standard_normal(2048) * 0.02).astype(np.float32)
+    w2 = (rng.standard_normal((2048, 512)) / math.sqrt(2048)).astype(np.float32)
+    b2 = (rng.standard_normal(512) * 0.02).astype(np.float32)
+    # CPU lane: formal GEMM, bias add, GELU region, formal GEMM, bias add
+    h1 = oracle.gemm_formal(oracle.F32, oracle.F32, x, w1, 128, 512, 2048).reshape(128, 2048)
+    h1 = oracle.bias_add(h1, b1)
+    h1 = oracle.gelu_tanh(h1, fmt=oracle.F32)
+    y = oracle.gemm_formal(oracle.F32, oracle.F32, h1, w2, 128, 2048, 512).reshape(128, 512)
+    y = oracle.bias_add(y, b2)
+    xd, w1d, w2d = dev(x), dev(w1), dev(w2)
+    hd = torch.empty((128, 2048), dtype=torch.float32, device="cuda")
+    yd = torch.empty((128, 512), dtype=torch.float32, device="cuda")
+    hip.gemm(xd, w1d, hd, 128, 512, 2048)
+    hip.bias_add(hd, dev(b1), hd, fmt=B.F32)
+    hip.gelu_tanh(hd, hd, fmt=B.F32)
+    hip.gemm(hd, w2d, yd, 128, 2048, 512)
+    hip.bias_add(yd, dev(b2), yd, fmt=B.F32)
+    got = host(yd)
+    # GEMMs and bias adds are bit-exact; only tanh differs by device ulps.
+    assert np.all(np.abs(got - y) <= 1e-4 * np.abs(y) + 1e-6)
+    gh = host(hd)
+    assert np.abs(gh - h1).max() <= 1e-5
+
+
+# ------------------------------------------------------------------ int8 GEMM
+@pytest.mark.parametrize("m,k,n", [(256, 256, 256), (128, 640, 384), (512, 4096, 256)])
+@pytest.mark.parametrize("rt", [0, 1])
+def test_i8_gemm_bit_exact(hip, B, oracle, m, k, n, rt):
+    say("i8 gemm", m, k, n, rt)
+    rng = np.random.default_rng(m + k + n + rt)
+    a = rng.integers(-127, 128, size=(m, k), dtype=np.int64).astype(np.int8)
+    b = rng.integers(-127, 128, size=(k, n), dtype=np.int64).astype(np.int8)
+    bb = np.ascontiguousarray(b.T) if rt else b
+    scale = rng.uniform(0.001, 0.01, size=n).astype(np.float32)
+    acc_ref, y_ref = oracle.gemm_i8(a, bb, scale, m, k, n, rhs_t=bool(rt))
+    acc = torch.zeros((m, n), dtype=torch.int32, device="cuda")
+    y = torch.zeros((m, n), dtype=torch.int16, device="cuda")
+    hip.gemm_i8(dev(a), dev(bb), dev(scale), y, m, k, n, acc_out=acc, rhs_t=bool(rt))
+    assert np.array_equal(host(acc), acc_ref)
+    assert np.array_equal(host(y).view(np.uint16), y_ref)
+
+
+def test_i8_gemm_extremes(hip, B, oracle):
+    """|acc| at its maximum (k * 127 * 127 and k * 127 * -128) stays exact."""
+    say("i8 gemm extremes")
+    m = n = 128
+    k = 4096
+    a = np.full((m, k), 127, np.int8)
+    a[1::2] = -128
+    b = np.full((k, n), -127, np.int8)
+    b[:, ::3] = -128
+    scale = np.full(n, 0.0078125, np.float32)
+    acc_ref, y_ref = oracle.gemm_i8(a, b, scale, m, k, n)
+    acc = torch.zeros((m, n), dtype=torch.int32, device="cuda")
+    y = torch.zeros((m, n), dtype=torch.int16, device="cuda")
+    hip.gemm_i8(dev(a), dev(b), dev(scale), y, m, k, n, acc_out=acc)
+    assert np.array_equal(host(acc), acc_ref)
+    assert np.array_equal(host(y).view(np.uint16), y_ref)
+    assert int(host(acc)[1, 0]) == 4096 * 128 * 128
+
+
+def test_i8_gemm_baseline_size_rows(hip, B, oracle):
+    """BASELINE config 3 (4096^3, Normal rhs): exact int64 closed form on a
+    sample of 24 full rows and the dequant chain bit-exact on them."""
+    say("i8 gemm 4096^3")
+    rng = np.random.default_rng(20260803)
+    M = N = K = 4096
+    a = rng.integers(-127, 128, size=(M, K), dtype=np.int64).astype(np.int8)
+    b = rng.integers(-127, 128, size=(K, N), dtype=np.int64).astype(np.int8)
+    scale = rng.uniform(0.001, 0.01, size=N).astype(np.float32)
+    acc = torch.zeros((M, N), dtype=torch.int32, device="cuda")
+    y = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    hip.gemm_i8(dev(a), dev(b), dev(scale), y, M, K, N, acc_out=acc)
+    accg, yg = host(acc), host(y).view(np.uint16)
+    rows = np.concatenate([[0, 1, 255, 256, 2047, 4095], rng.choice(M, 18, replace=False)])
+    exact = a[rows].astype(np.int64) @ b.astype(np.int64)
+    assert np.array_equal(accg[rows], exact.astype(np.int32))
+    yr = oracle.f32_to_bf16((exact.astype(np.float32) * scale).astype(np.float32)).reshape(exact.shape)
+    assert np.array_equal(yg[rows], yr)
+    # checksum of checksums over the whole output: column sums of the
+    # accumulator equal (colsum of A) @ B exactly.
+    colsum = a.astype(np.int64).sum(0) @ b.astype(np.int64)
+    assert np.array_equal(accg.astype(np.int64).sum(0), colsum)
+
+
+# ------------------------------------------------------------------ MFMA bf16 GEMM
+@pytest.mark.parametrize("m,k,n,rt,fmt", [(256, 512, 256, 0, 3), (128, 256, 384, 1, 3), (512, 1024, 512, 0, 2),
+                                          (1024, 4096, 1024, 1, 3)])
+def test_mfma_gemm_vs_formal(hip, B, oracle, m, k, n, rt, fmt):
+    say("mfma gemm", m, k, n, rt, fmt)
+    rng = np.random.default_rng(m + n + k)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = (rng.standard_normal((k, n)) / math.sqrt(k)).astype(np.float32)
+    if fmt == B.BF16:
+        ah, bh = oracle.f32_to_bf16(a).reshape(a.shape), oracle.f32_to_bf16(b).reshape(b.shape)
+    else:
+        ah, bh = a.astype(np.float16).view(np.uint16), b.astype(np.float16).view(np.uint16)
+    bt = np.ascontiguousarray(bh.T) if rt else bh
+    ref = oracle.gemm_formal(fmt, oracle.F32, ah, bt, m, k, n, rhs_t=bool(rt)).reshape(m, n)
+    out = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    hip.gemm_mfma(u16(ah), u16(bt), out, m, k, n, in_fmt=fmt, out_fmt=B.F32, rhs_t=bool(rt))
+    got = host(out)
+    rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert rel <= 1e-5 and np.abs(got - ref).max() <= 1e-4 * np.abs(ref).max()
+    outn = torch.zeros((m, n), dtype=torch.int16, device="cuda")
+    hip.gemm_mfma(u16(ah), u16(bt), outn, m, k, n, in_fmt=fmt, out_fmt=fmt, rhs_t=bool(rt))
+    gn = from_u16(outn)
+    gf = oracle.to_float(fmt, gn).reshape(m, n)
+    rel = np.linalg.norm(gf - ref) / np.linalg.norm(ref)
+    assert rel <= 2e-3 and np.abs(gf - ref).max() <= 2e-2 * np.abs(ref).max()
+
+
+# ------------------------------------------------------------------ attention
+def _bf16_randn(oracle, rng, shape):
+    return oracle.f32_to_bf16(rng.standard_normal(shape).astype(np.float32)).reshape(shape)
+
+
+@pytest.mark.parametrize("Bn,Hq,Hkv,S,causal", [(1, 2, 2, 256, True), (1, 2, 2, 256, False), (2, 4, 1, 384, True),
+                                               (1, 8, 2, 128, True), (1, 1, 1, 640, False)])
+def test_fa_prefill_vs_oracle(hip, B, oracle, Bn, Hq, Hkv, S, causal):
+    say("fa prefill", Bn, Hq, Hkv, S, causal)
+    rng = np.random.default_rng(S + Hq + causal)
+    D = 128
+    q, k, v = (_bf16_randn(oracle, rng, (Bn, hh, S, D)) for hh in (Hq, Hkv, Hkv))
+    scale = 1.0 / math.sqrt(D)
+    ref = oracle.attention_prefill(q, k, v, scale, causal=causal, block_k=64)
+    o = torch.zeros((Bn, Hq, S, D), dtype=torch.int16, device="cuda")
+    hip.attention_prefill(u16(q), u16(k), u16(v), o, scale, causal=causal)
+    got = oracle.bf16_to_f32(from_u16(o)).reshape(o.shape)
+    attention_gate(got, oracle.bf16_to_f32(ref).reshape(ref.shape), what="FA vs oracle")
+
+
+def test_fa_prefill_baseline_config(hip, B, oracle):
+    """[1,16,2048,128] bf16 causal.  All heads against a
+    torch float32 attention on the GPU (independent check); two heads
+    against the CPU oracle."""
+    say("fa prefill baseline config")
+    rng = np.random.default_rng(20260803)
+    Bn, H, S, D = 1, 16, 2048, 128
+    q, k, v = (_bf16_randn(oracle, rng, (Bn, H, S, D)) for _ in range(3))
+    scale = 1.0 / math.sqrt(D)
+    o = torch.zeros((Bn, H, S, D), dtype=torch.int16, device="cuda")
+    qd, kd, vd = u16(q), u16(k), u16(v)
+    hip.attention_prefill(qd, kd, vd, o, scale, causal=True)
+    got = oracle.bf16_to_f32(from_u16(o)).reshape(o.shape)
+    qf, kf, vf = (torch.from_numpy(oracle.bf16_to_f32(t).reshape(t.shape)).cuda() for t in (q, k, v))
+    s = torch.matmul(qf, kf.transpose(-1, -2).contiguous()) * scale
+    s = s.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool, device="cuda"), 1), float("-inf"))
+    ref = torch.matmul(torch.softmax(s, -1), vf)
+    attention_gate(got, host(ref), what="FA vs torch f32")
+    heads = [0, 11]
+    ro = oracle.attention_prefill(q[:, heads], k[:, heads], v[:, heads], scale, causal=True, block_k=64)
+    attention_gate(got[:, heads], oracle.bf16_to_f32(ro).reshape(ro.shape), what="FA vs oracle (2 heads)")
+
+
+def test_fa_prefill_gqa_equals_repeated_kv(hip, B, oracle):
+    say("fa gqa == mha")
+    rng = np.random.default_rng(9)
+    q = _bf16_randn(oracle, rng, (1, 8, 256, 128))
+    k = _bf16_randn(oracle, rng, (1, 2, 256, 128))
+    v = _bf16_randn(oracle, rng, (1, 2, 256, 128))
+    o1 = torch.zeros((1, 8, 256, 128), dtype=torch.int16, device="cuda")
+    o2 = torch.zeros_like(o1)
+    hip.attention_prefill(u16(q), u16(k), u16(v), o1, 0.088, causal=True)
+    hip.attention_prefill(u16(q), u16(np.repeat(k, 4, 1)), u16(np.repeat(v, 4, 1)), o2, 0.088, causal=True)
+    assert np.array_equal(host(o1), host(o2))
+
+
+@pytest.mark.parametrize("Bn,Hq,Hkv,L,cap,chunks", [(2, 8, 2, 1024, 1024, 16), (1, 4, 4, 777, 1000, 16),
+                                                   (3, 8, 1, 100, 128, 16), (1, 16, 2, 4096, 4096, 4),
+                                                   (2, 4, 2, 513, 600, 1)])
+def test_fd_decode_vs_oracle(hip, B, oracle, Bn, Hq, Hkv, L, cap, chunks):
+    say("fd decode", Bn, Hq, Hkv, L, cap, chunks)
+    rng = np.random.default_rng(L + chunks)
+    D = 128
+    q = _bf16_randn(oracle, rng, (Bn, Hq, 1, D))
+    k = _bf16_randn(oracle, rng, (Bn, Hkv, cap, D))
+    v = _bf16_randn(oracle, rng, (Bn, Hkv, cap, D))
+    scale = 1.0 / math.sqrt(D)
+    ref = oracle.attention_decode(q, k, v, scale, chunks=chunks, kv_len=L, block_k=64)
+    o = torch.zeros((Bn, Hq, 1, D), dtype=torch.int16, device="cuda")
+    hip.attention_decode(u16(q), u16(k), u16(v), o, scale, chunks=chunks, kv_len=L)
+    got = oracle.bf16_to_f32(from_u16(o)).reshape(o.shape)
+    attention_gate(got, oracle.bf16_to_f32(ref).reshape(ref.shape), what="FD vs oracle")
+
+
+def test_fd_decode_baseline_config(hip, B, oracle):
+    """Q [32,32,1,128], K/V [32,8,8192,128], 16 chunks.
+    Four batches against the oracle, all batches against FA on the same
+    single query (FD == FA within tolerance)."""
+    say("fd decode baseline config")
+    Bn, Hq, Hkv, L, D = 32, 32, 8, 8192, 128
+    gen = torch.Generator(device="cuda").manual_seed(20260803)
+    q = torch.randn((Bn, Hq, 1, D), device="cuda", generator=gen).to(torch.bfloat16)
+    k = torch.randn((Bn, Hkv, L, D), device="cuda", generator=gen).to(torch.bfloat16)
+    v = torch.randn((Bn, Hkv, L, D), device="cuda", generator=gen).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(D)
+    o = torch.zeros((Bn, Hq, 1, D), dtype=torch.bfloat16, device="cuda")
+    hip.attention_decode(q, k, v, o, scale, chunks=16)
+    got = host(o.float())
+    sel = [0, 7, 19, 31]
+    qs, ks, vs = (host(t[sel].contiguous().view(torch.int16)).view(np.uint16) for t in (q, k, v))
+    ref = oracle.attention_decode(qs, ks, vs, scale, chunks=16, block_k=64)
+    attention_gate(got[sel], oracle.bf16_to_f32(ref).reshape(ref.shape), what="FD vs oracle (4 batches)")
+    # all batches: float32 softmax attention on the GPU with GQA expansion
+    kf = k.float().repeat_interleave(Hq // Hkv, dim=1)
+    vf = v.float().repeat_interleave(Hq // Hkv, dim=1)
+    s = torch.matmul(q.float(), kf.transpose(-1, -2).contiguous()) * scale
+    ref_all = torch.matmul(torch.softmax(s, -1), vf)
+    attention_gate(got, host(ref_all), what="FD vs torch f32 (all)")
+
+
+# ------------------------------------------------------------------ managed lane
+EXACT_OPS = ["Abs", "Neg", "Recip", "Square", "Max", "Min", "Add", "Sub", "Mul", "Relu", "Sqrt", "Rsqrt"]
+TRANS_OPS = ["Log2", "Ln", "Pow2", "Exp", "ExpLp", "Sin", "Cos", "Tanh", "Sigmoid", "Softplus"]
+
+
+@pytest.mark.parametrize("fmt", [5, 3, 2])
+def test_elementwise_vs_oracle(hip, B, oracle, fmt):
+    say("elementwise", fmt)
+    rng = np.random.default_rng(fmt)
+    n = 4099
+    a = (rng.standard_normal(n) * 3).astype(np.float32)
+    b = (rng.standard_normal(n) * 3).astype(np.float32)
+    pos = (np.abs(a) + 0.05).astype(np.float32)
+    enc = (lambda x: x) if fmt == B.F32 else (
+        (lambda x: oracle.f32_to_bf16(x)) if fmt == B.BF16 else (lambda x: x.astype(np.float16).view(np.uint16)))
+    todev = dev if fmt == B.F32 else u16
+    for name in EXACT_OPS + TRANS_OPS:
+        op = B.EW[name]
+        src = pos if name in ("Sqrt", "Rsqrt", "Log2", "Ln") else a
+        ea, eb = enc(src), enc(b)
+        binary = name in ("Max", "Min", "Add", "Sub", "Mul")
+        ref = oracle.elementwise(op, fmt, ea, eb if binary else None)
+        out = torch.zeros(n, dtype=torch.float32 if fmt == B.F32 else torch.int16, device="cuda")
+        hip.elementwise(op, fmt, todev(ea), out, in1=todev(eb) if binary else None)
+        got = host(out)
+        if fmt != B.F32:
+            got = got.view(np.uint16)
+        if name in EXACT_OPS:
+            assert np.array_equal(got, ref), name
+        else:
+            gf, rf = oracle.to_float(fmt, got), oracle.to_float(fmt, ref)
+            tol = 2e-6 if fmt == B.F32 else (8e-3 if fmt == B.BF16 else 1e-3)
+            close = np.abs(gf - rf) <= tol * np.abs(rf) + 1e-30 + (tol if name in ("Sin", "Cos") else 0)
+            assert np.all((gf == rf) | close), name
+
+
+def test_elementwise_rejects_outside_managed_domain(hip, B):
+    t = torch.zeros(8, dtype=torch.float32, device="cuda")
+    for name in ("Eq", "LogicAnd", "SatRelu", "LeakyRelu"):
+        with pytest.raises(B.WaferHipError) as e:
+            hip.elementwise(B.EW[name], B.F32, t, t, in1=t)
+        assert e.value.status == -3
+
+
+def test_convert_routes_vs_oracle(hip, B, oracle, goldens):
+    say("convert")
+    rng = np.random.default_rng(12)
+    f = (rng.standard_normal(5000) * 1000).astype(np.float32)
+    f[:10] = [0.0, -0.0, 1.5, 2.5, -2.5, 65504.0, 65520.0, 1e-8, 3.4e38, -1e-40]
+    bits = [h(x) for x in goldens["bf16_samples"]["input_f32"]]
+    f[10:10 + len(bits)] = np.array(bits, np.uint32).view(np.float32)
+    i32 = rng.integers(-2**31, 2**31, size=5000, dtype=np.int64).astype(np.int32)
+    i32[:6] = [0, 1, -1, 16777217, 2**31 - 1, -2**31]
+    i16 = rng.integers(-32768, 32768, size=5000, dtype=np.int64).astype(np.int16)
+    cases = [(167, f, B.BF16), (166, f, B.F16), (149, i32, B.F32), (148, i32, B.BF16), (147, i32, B.F16),
+             (145, i16, B.F32), (144, i16, B.BF16), (143, i16, B.F16),
+             (155, oracle.f32_to_bf16(f), B.F32), (161, np.abs(f).astype(np.float16).view(np.uint16), B.F32),
+             (154, oracle.f32_to_bf16(f), B.F16), (160, f.astype(np.float16).view(np.uint16), B.BF16),
+             (165, np.clip(f, -1e9, 1e9), B.I32), (164, np.clip(f, -3e4, 3e4), B.I16)]
+    for opcode, src, dfmt in cases:
+        ref = oracle.convert(opcode, src, dfmt)
+        sd = dev(src.view(np.int16)) if src.dtype == np.uint16 else dev(src)
+        odt = {B.F32: torch.float32, B.BF16: torch.int16, B.F16: torch.int16, B.I32: torch.int32, B.I16: torch.int16}[dfmt]
+        out = torch.zeros(src.size, dtype=odt, device="cuda")
+        hip.convert(opcode, sd, out)
+        got = host(out)
+        assert np.array_equal(got.view(np.uint8), ref.view(np.uint8)), opcode
+    with pytest.raises(B.WaferHipError):
+        hip.convert(165, dev(np.array([np.inf], np.float32)), torch.zeros(1, dtype=torch.int32, device="cuda"))
+
+
+@pytest.mark.parametrize("shape", [[1, 2, 3, 1031], [4, 5, 6, 7], [3, 64], [2, 3, 4, 5, 6]])
+def test_reduce_vs_oracle_bit_exact(hip, B, oracle, goldens, shape):
+    say("reduce", shape)
+    rng = np.random.default_rng(len(shape) + shape[-1])
+    x = rng.standard_normal(shape).astype(np.float32)
+    for op in (0, 1, 2):
+        for dim in (0, 1, 2, 3, 4, 5):
+            rank = len(shape)
+            if (dim <= 3 and dim >= rank) or (dim >= 4 and rank < 3):
+                continue
+            for fmt in ((B.F32,) if op == 0 else (B.F32, B.BF16)):
+                src = x if fmt == B.F32 else oracle.f32_to_bf16(x).reshape(shape)
+                ref = oracle.reduce(op, dim, fmt, shape, src)
+                out = torch.zeros(ref.size, dtype=torch.float32 if fmt == B.F32 else torch.int16, device="cuda")
+                hip.reduce(op, dim, fmt, shape, dev(src) if fmt == B.F32 else u16(src), out)
+                got = host(out)
+                assert np.array_equal(got.view(np.uint8), ref.ravel().view(np.uint8)), (op, dim, fmt)
+    g = goldens["reduce_sum_ncx"]
+    src = np.array([h(v) for v in g["input"]], np.uint32).view(np.float32)
+    out = torch.zeros(2, dtype=torch.float32, device="cuda")
+    hip.reduce(0, g["dim"], B.F32, g["shape"], dev(src), out)
+    assert [int(v) for v in host(out).view(np.uint32)] == [h(v) for v in g["expect"]]
+
+
+@pytest.mark.parametrize("fmt", [0, 2, 3, 5, 11])
+@pytest.mark.parametrize("layout", [0, 2, 3])
+@pytest.mark.parametrize("shape", [[5], [3, 1], [2, 3, 33], [1, 2, 3, 1025], [2, 2, 130], [3, 96], [2, 1, 129],
+                                   [4, 8, 64, 200]])
+def test_codec_vs_oracle(hip, B, oracle, fmt, layout, shape):
+    nbytes = B.physical_bytes(fmt, layout, shape)
+    geo = oracle.geometry(fmt, layout, shape)
+    assert nbytes == geo["physical_bytes"]
+    rng = np.random.default_rng(sum(shape) + fmt + layout)
+    dt = oracle.storage_dtype(fmt)
+    count = int(np.prod(shape))
+    logical = rng.integers(0, 120, size=count).astype(dt)
+    template = rng.integers(0, 256, size=nbytes).astype(np.uint8)
+    ref = oracle.pack(fmt, layout, shape, logical, template)
+    st = dev(template)
+    hip.pack(fmt, layout, shape, dev(logical), st)
+    assert np.array_equal(host(st), ref)
+    back = torch.zeros(count * np.dtype(dt).itemsize, dtype=torch.uint8, device="cuda")
+    hip.unpack(fmt, layout, shape, dev(ref), back)
+    assert np.array_equal(host(back).view(dt), logical)
+
+
+# ------------------------------------------------------------------ fused regions
+def test_regions_vs_oracle(hip, B, oracle):
+    say("regions")
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((64, 4096)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(4096)).astype(np.float32)
+    xb, wb = oracle.f32_to_bf16(x).reshape(x.shape), oracle.f32_to_bf16(w)
+    y = torch.zeros(x.shape, dtype=torch.int16, device="cuda")
+    hip.rmsnorm(u16(xb), u16(wb), y, 1e-5, fmt=B.BF16)
+    ref = oracle.rmsnorm(xb, wb, 1e-5)
+    attention_gate(oracle.bf16_to_f32(from_u16(y)), oracle.bf16_to_f32(ref), what="rmsnorm")
+    yf = torch.zeros(x.shape, dtype=torch.float32, device="cuda")
+    hip.rmsnorm(dev(x), dev(w), yf, 1e-5, fmt=B.F32)
+    rf = oracle.rmsnorm(x, w, 1e-5, fmt=oracle.F32)
+    assert np.allclose(host(yf), rf, rtol=2e-6, atol=1e-7)
+    hip.softmax(u16(xb), y, fmt=B.BF16)
+    attention_gate(oracle.bf16_to_f32(from_u16(y)), oracle.bf16_to_f32(oracle.softmax(xb)), what="softmax")
+    g, u = x[:, :2048].copy(), x[:, 2048:].copy()
+    gb, ub = oracle.f32_to_bf16(g).reshape(g.shape), oracle.f32_to_bf16(u).reshape(u.shape)
+    ys = torch.zeros(g.shape, dtype=torch.int16, device="cuda")
+    hip.silu_mul(u16(gb), u16(ub), ys, fmt=B.BF16)
+    attention_gate(oracle.bf16_to_f32(from_u16(ys)), oracle.bf16_to_f32(oracle.silu_mul(gb, ub)), what="swiglu")
+    yg = torch.zeros(x.shape, dtype=torch.float32, device="cuda")
+    hip.gelu_tanh(dev(x), yg, fmt=B.F32)
+    rg = oracle.gelu_tanh(x, fmt=oracle.F32)
+    assert np.all(np.abs(host(yg) - rg) <= 1e-5 * np.abs(rg) + 1e-6)
+    T, H, D = 1024, 8, 128
+    xr = rng.standard_normal((T, H, D)).astype(np.float32)
+    xrb = oracle.f32_to_bf16(xr).reshape(xr.shape)
+    pos = np.arange(T, dtype=np.int32)
+    yr = torch.zeros(xr.shape, dtype=torch.int16, device="cuda")
+    hip.rope(u16(xrb), yr, dev(pos), 1e4, fmt=B.BF16)
+    attention_gate(oracle.bf16_to_f32(from_u16(yr)), oracle.bf16_to_f32(oracle.rope(xrb, pos, 1e4)), what="rope")
+    bias = rng.standard_normal(4096).astype(np.float32)
+    yb = torch.zeros(x.shape, dtype=torch.float32, device="cuda")
+    hip.bias_add(dev(x), dev(bias), yb, fmt=B.F32)
+    assert np.array_equal(host(yb), oracle.bias_add(x, bias))
+
+
+def test_invalid_arguments_fail_without_launch(hip, B):
+    t = torch.zeros(16, dtype=torch.int16, device="cuda")
+    with pytest.raises(B.WaferHipError) as e:
+        hip.attention_prefill(t.view(1, 1, 1, 16), t.view(1, 1, 1, 16), t.view(1, 1, 1, 16), t.view(1, 1, 1, 16), 0.1)
+    assert e.value.status == -3  # head_dim 16 is not served
+    with pytest.raises(B.WaferHipError):
+        hip.gemm(t, t, t, 0, 1, 1)
+    with pytest.raises(B.WaferHipError):
+        hip.gemm_i8(t, t, t, t, 100, 64, 128)

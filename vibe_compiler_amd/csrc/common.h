@@ -1,0 +1,173 @@
+// common.h -- shared helpers for the gfx950 numeric backend: status plumbing,
+// scalar codecs (f32 <-> bf16/f16 with the reference's rounding rules), and
+// MFMA operand vector types.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+
+#include "wafer_hip.h"
+
+struct wafer_hip_context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  // FD partial-state workspace (grown on demand, freed with the context).
+  void *workspace = nullptr;
+  size_t workspace_bytes = 0;
+  // Scratch for operand re-layout (transposed rhs), grown on demand.
+  void *relayout = nullptr;
+  size_t relayout_bytes = 0;
+  int cu_count = 0;
+};
+
+namespace wafer {
+
+// Thread-local last error, set by fail() and returned by wafer_hip_last_error.
+void set_error(const std::string &message);
+int fail(int code, const std::string &message);
+int check_hip(hipError_t err, const char *what);
+int ensure_workspace(wafer_hip_context *ctx, void **slot, size_t *slot_bytes,
+                     size_t need);
+int launch_status(const char *kernel);
+
+#define WAFER_CHECK_CTX(ctx)                                                   \
+  do {                                                                         \
+    if (!(ctx)) return ::wafer::fail(WAFER_HIP_E_INVALID_FIELD, "null context"); \
+  } while (0)
+
+#define WAFER_TRY(expr)                                                        \
+  do {                                                                         \
+    int _st = (expr);                                                          \
+    if (_st != WAFER_HIP_OK) return _st;                                       \
+  } while (0)
+
+inline bool is_float_format(uint32_t f) {
+  return f == WAFER_FMT_F32 || f == WAFER_FMT_BF16 || f == WAFER_FMT_F16;
+}
+inline int format_bytes(uint32_t f) {
+  switch (f) {
+  case WAFER_FMT_I8: case WAFER_FMT_U8: case WAFER_FMT_BOOL: return 1;
+  case WAFER_FMT_I16: case WAFER_FMT_F16: case WAFER_FMT_BF16: case WAFER_FMT_U16: return 2;
+  case WAFER_FMT_I32: case WAFER_FMT_F32: case WAFER_FMT_TF32: case WAFER_FMT_U32: return 4;
+  case WAFER_FMT_I64: case WAFER_FMT_U64: return 8;
+  default: return 0;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Device scalar codecs.  These restate the reference's conversions bit for
+// bit: F32 -> BF16 RNE with the canonical quiet NaN 0x7fc0
+// (lib/Wafer/Target/PhysicalTensor/TargetScalarConversion.cpp:282-290), F16
+// via halfToBits / halfFromBits
+// (lib/Wafer/Simulator/Reference/ManagedReferenceTargetModel.cpp:60-135).
+// ---------------------------------------------------------------------------
+__host__ __device__ inline uint32_t f2u(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  return u;
+}
+__host__ __device__ inline float u2f(uint32_t u) {
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+
+__host__ __device__ inline uint16_t f32_to_bf16(float v) {
+  uint32_t u = f2u(v);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__host__ __device__ inline float bf16_to_f32(uint16_t b) { return u2f((uint32_t)b << 16); }
+
+__host__ __device__ inline float f16_to_f32(uint16_t bits) {
+  uint32_t sign = (uint32_t)(bits & 0x8000u) << 16;
+  uint32_t exponent = (bits >> 10) & 0x1fu;
+  uint32_t fraction = bits & 0x03ffu;
+  if (exponent == 0) {
+    if (fraction == 0) return u2f(sign);
+    int32_t e = -14;
+    while ((fraction & 0x0400u) == 0) { fraction <<= 1; --e; }
+    fraction &= 0x03ffu;
+    return u2f(sign | ((uint32_t)(e + 127) << 23) | (fraction << 13));
+  }
+  if (exponent == 31) return u2f(sign | 0x7f800000u | (fraction << 13));
+  return u2f(sign | ((exponent - 15 + 127) << 23) | (fraction << 13));
+}
+
+// F32 -> F16, RNE, overflow to +-inf, gradual underflow; NaN -> 0x7e00.
+__host__ __device__ inline uint16_t f32_to_f16(float value) {
+  uint32_t bits = f2u(value);
+  uint16_t sign = (uint16_t)((bits >> 16) & 0x8000u);
+  uint32_t eb = (bits >> 23) & 0xffu;
+  uint32_t fraction = bits & 0x007fffffu;
+  if (eb == 0xffu) return fraction ? (uint16_t)0x7e00u : (uint16_t)(sign | 0x7c00u);
+  int32_t exponent = (int32_t)eb - 127;
+  if (exponent > 15) return (uint16_t)(sign | 0x7c00u);
+  if (exponent >= -14) {
+    uint32_t de = (uint32_t)(exponent + 15);
+    uint32_t df = fraction >> 13;
+    uint32_t rem = fraction & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (df & 1u))) {
+      ++df;
+      if (df == 0x400u) {
+        df = 0;
+        ++de;
+        if (de >= 0x1fu) return (uint16_t)(sign | 0x7c00u);
+      }
+    }
+    return (uint16_t)(sign | (de << 10) | df);
+  }
+  if (exponent < -25) return sign;
+  uint32_t significand = fraction | 0x00800000u;
+  uint32_t shift = (uint32_t)(-exponent - 1);
+  uint32_t df = significand >> shift;
+  uint32_t rem = significand & ((1u << shift) - 1u);
+  uint32_t half = 1u << (shift - 1);
+  if (rem > half || (rem == half && (df & 1u))) ++df;
+  return (uint16_t)(sign | df);
+}
+
+template <uint32_t F> __device__ inline float load_as_f32(const void *base, int64_t i);
+template <> __device__ inline float load_as_f32<WAFER_FMT_F32>(const void *b, int64_t i) {
+  return ((const float *)b)[i];
+}
+template <> __device__ inline float load_as_f32<WAFER_FMT_BF16>(const void *b, int64_t i) {
+  return bf16_to_f32(((const uint16_t *)b)[i]);
+}
+template <> __device__ inline float load_as_f32<WAFER_FMT_F16>(const void *b, int64_t i) {
+  return f16_to_f32(((const uint16_t *)b)[i]);
+}
+template <uint32_t F> __device__ inline void store_from_f32(void *base, int64_t i, float v);
+template <> __device__ inline void store_from_f32<WAFER_FMT_F32>(void *b, int64_t i, float v) {
+  ((float *)b)[i] = v;
+}
+template <> __device__ inline void store_from_f32<WAFER_FMT_BF16>(void *b, int64_t i, float v) {
+  ((uint16_t *)b)[i] = f32_to_bf16(v);
+}
+template <> __device__ inline void store_from_f32<WAFER_FMT_F16>(void *b, int64_t i, float v) {
+  ((uint16_t *)b)[i] = f32_to_f16(v);
+}
+
+// ExpLp: one RNE multiply by log2(e) = 0x1.715476p+0, then exp2
+// (ManagedReferenceTargetModel.cpp:265-270).  v_exp_f32 is the exp2.
+__device__ inline float explp(float x) {
+  return __builtin_amdgcn_exp2f(x * 0x1.715476p+0f);
+}
+
+// ---------------------------------------------------------------------------
+// MFMA operand types.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+}  // namespace wafer

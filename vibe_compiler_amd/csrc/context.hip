@@ -1,0 +1,100 @@
+// context.hip -- context lifecycle, stream binding, error reporting and the
+// workspace allocator shared by the entry points.
+#include "common.h"
+
+#include <cstdio>
+
+namespace wafer {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string &message) { g_last_error = message; }
+
+int fail(int code, const std::string &message) {
+  g_last_error = message;
+  return code;
+}
+
+int check_hip(hipError_t err, const char *what) {
+  if (err == hipSuccess) return WAFER_HIP_OK;
+  char buf[256];
+  std::snprintf(buf, sizeof(buf), "%s: %s", what, hipGetErrorString(err));
+  return fail(WAFER_HIP_E_RUNTIME, buf);
+}
+
+int launch_status(const char *kernel) {
+  return check_hip(hipGetLastError(), kernel);
+}
+
+// Grows *slot to at least `need` bytes.  The old contents are discarded; the
+// growth is stream-ordered by synchronising the context's stream first, so
+// in-flight kernels never see the buffer freed under them.
+int ensure_workspace(wafer_hip_context *ctx, void **slot, size_t *slot_bytes,
+                     size_t need) {
+  if (*slot_bytes >= need) return WAFER_HIP_OK;
+  WAFER_TRY(check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize"));
+  if (*slot) {
+    WAFER_TRY(check_hip(hipFree(*slot), "hipFree(workspace)"));
+    *slot = nullptr;
+    *slot_bytes = 0;
+  }
+  size_t rounded = (need + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+  WAFER_TRY(check_hip(hipMalloc(slot, rounded), "hipMalloc(workspace)"));
+  *slot_bytes = rounded;
+  return WAFER_HIP_OK;
+}
+
+}  // namespace wafer
+
+using namespace wafer;
+
+extern "C" int wafer_hip_context_create(int device, wafer_hip_context **out) {
+  if (!out) return fail(WAFER_HIP_E_INVALID_FIELD, "null output pointer");
+  *out = nullptr;
+  int count = 0;
+  WAFER_TRY(check_hip(hipGetDeviceCount(&count), "hipGetDeviceCount"));
+  if (device < 0 || device >= count)
+    return fail(WAFER_HIP_E_UNAVAILABLE, "no HIP device " + std::to_string(device));
+  hipDeviceProp_t prop;
+  WAFER_TRY(check_hip(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties"));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(WAFER_HIP_E_UNAVAILABLE,
+                std::string("device is ") + prop.gcnArchName + ", kernels are built for gfx950");
+  auto *ctx = new wafer_hip_context();
+  ctx->device = device;
+  ctx->cu_count = prop.multiProcessorCount;
+  *out = ctx;
+  return WAFER_HIP_OK;
+}
+
+extern "C" int wafer_hip_context_destroy(wafer_hip_context *ctx) {
+  if (!ctx) return WAFER_HIP_OK;
+  int st = WAFER_HIP_OK;
+  if (ctx->workspace || ctx->relayout) {
+    st = check_hip(hipSetDevice(ctx->device), "hipSetDevice");
+    if (st == WAFER_HIP_OK) st = check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    if (ctx->workspace) st = check_hip(hipFree(ctx->workspace), "hipFree(workspace)");
+    if (ctx->relayout) st = check_hip(hipFree(ctx->relayout), "hipFree(relayout)");
+  }
+  delete ctx;
+  return st;
+}
+
+extern "C" int wafer_hip_set_stream(wafer_hip_context *ctx, void *hip_stream) {
+  WAFER_CHECK_CTX(ctx);
+  ctx->stream = (hipStream_t)hip_stream;
+  return WAFER_HIP_OK;
+}
+
+extern "C" int wafer_hip_synchronize(wafer_hip_context *ctx) {
+  WAFER_CHECK_CTX(ctx);
+  return check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+}
+
+extern "C" const char *wafer_hip_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" const char *wafer_hip_implementation(void) {
+  return "wafer-hip gfx950: formal-order FMA GEMM, bf16/f16/i8 MFMA GEMM, "
+         "FA prefill (mfma_f32_32x32x16_bf16), FD decode (mfma_f32_16x16x32_bf16 + LSE fold), "
+         "managed elementwise/convert/reduce, Cx/NCx codec, fused regions";
+}

@@ -1,0 +1,334 @@
+// elementwise.hip -- the managed-reference command lane on the GPU:
+// elementwise, convert and reduce over logical (unpacked) tensors.
+//
+// Elementwise: per element decode -> float op -> RNE encode, the expressions
+// of evaluateElementwise
+// (lib/Wafer/Simulator/Reference/ManagedReferenceTargetModel.cpp:230-299).
+// The IEEE-exact ops (Abs, Neg, Recip, Square, Max, Min, Add, Sub, Mul, Relu,
+// Sqrt, Rsqrt = 1/sqrt) are correctly rounded on gfx950 and so bit-identical
+// to the host lane; the transcendental ops use the device math library and
+// match within its ulp bound.  Relations, logic ops, SatRelu and LeakyRelu
+// are outside the managed domain (:287-299) and are rejected the same way.
+//
+// Reduce: row-major traversal accumulating into the output index with the
+// reduced dimensions dropped (:382-458).  One thread owns one output and
+// walks its inputs in increasing linear order, which is exactly the order in
+// which the host loop visits them, so F32 sums are bit-identical as well.
+#include "common.h"
+
+namespace wafer {
+namespace {
+
+enum {
+  EW_ABS = 0, EW_RECIP = 1, EW_SQUARE = 2, EW_SQRT = 3, EW_RSQRT = 4, EW_NEG = 5,
+  EW_MAX = 6, EW_MIN = 7, EW_ADD = 8, EW_SUB = 9, EW_MUL = 10, EW_LOG2 = 22,
+  EW_LN = 23, EW_POW2 = 24, EW_EXP = 25, EW_EXPLP = 26, EW_SIN = 27, EW_COS = 28,
+  EW_TANH = 29, EW_SIGMOID = 30, EW_RELU = 31, EW_SOFTPLUS = 34
+};
+
+int ew_arity(uint32_t op) {
+  switch (op) {
+  case EW_MAX: case EW_MIN: case EW_ADD: case EW_SUB: case EW_MUL: return 2;
+  case EW_ABS: case EW_RECIP: case EW_SQUARE: case EW_SQRT: case EW_RSQRT: case EW_NEG:
+  case EW_LOG2: case EW_LN: case EW_POW2: case EW_EXP: case EW_EXPLP: case EW_SIN:
+  case EW_COS: case EW_TANH: case EW_SIGMOID: case EW_RELU: case EW_SOFTPLUS: return 1;
+  default: return 0;
+  }
+}
+
+template <int OP> __device__ inline float ew_eval(float a, float b) {
+  if (OP == EW_ABS) return fabsf(a);
+  if (OP == EW_NEG) return -a;
+  if (OP == EW_RECIP) return 1.0f / a;
+  if (OP == EW_SQUARE) return a * a;
+  if (OP == EW_MAX) return fmaxf(a, b);
+  if (OP == EW_MIN) return fminf(a, b);
+  if (OP == EW_ADD) return a + b;
+  if (OP == EW_SUB) return a - b;
+  if (OP == EW_MUL) return a * b;
+  if (OP == EW_RELU) return a < 0.0f ? 0.0f : a;
+  if (OP == EW_SQRT) return sqrtf(a);
+  if (OP == EW_RSQRT) return 1.0f / sqrtf(a);
+  if (OP == EW_LOG2) return log2f(a);
+  if (OP == EW_LN) return logf(a);
+  if (OP == EW_POW2) return exp2f(a);
+  if (OP == EW_EXP) return expf(a);
+  if (OP == EW_EXPLP) return exp2f(a * 0x1.715476p+0f);
+  if (OP == EW_SIN) return sinf(a);
+  if (OP == EW_COS) return cosf(a);
+  if (OP == EW_TANH) return tanhf(a);
+  if (OP == EW_SIGMOID) {
+    if (a >= 0.0f) return 1.0f / (1.0f + expf(-a));
+    return expf(a) / (1.0f + expf(a));
+  }
+  if (OP == EW_SOFTPLUS) return fmaxf(a, 0.0f) + log1pf(expf(-fabsf(a)));
+  return u2f(0x7fc00000u);
+}
+
+template <int OP, uint32_t F>
+__global__ __launch_bounds__(256) void ew_kernel(const void *__restrict__ in0,
+                                                 const void *__restrict__ in1,
+                                                 void *__restrict__ dst, uint64_t count) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+    const float a = load_as_f32<F>(in0, (int64_t)i);
+    const float b = in1 ? load_as_f32<F>(in1, (int64_t)i) : 0.0f;
+    float r = ew_eval<OP>(a, b);
+    if (r != r) r = u2f(0x7fc00000u);
+    store_from_f32<F>(dst, (int64_t)i, r);
+  }
+}
+
+template <int OP>
+int launch_ew(uint32_t fmt, hipStream_t st, const void *in0, const void *in1, void *dst,
+              uint64_t count) {
+  const unsigned blocks = (unsigned)std::min<uint64_t>((count + 255) / 256, 65536);
+  if (fmt == WAFER_FMT_F32)
+    hipLaunchKernelGGL((ew_kernel<OP, WAFER_FMT_F32>), dim3(blocks), dim3(256), 0, st, in0, in1, dst, count);
+  else if (fmt == WAFER_FMT_BF16)
+    hipLaunchKernelGGL((ew_kernel<OP, WAFER_FMT_BF16>), dim3(blocks), dim3(256), 0, st, in0, in1, dst, count);
+  else
+    hipLaunchKernelGGL((ew_kernel<OP, WAFER_FMT_F16>), dim3(blocks), dim3(256), 0, st, in0, in1, dst, count);
+  return launch_status("ew_kernel");
+}
+
+// ---- convert ---------------------------------------------------------------
+// Route table of the reference (lib/Wafer/Target/TargetFormat.cpp:164-196),
+// restricted to the int16/int32/f16/bf16/f32 routes.
+struct Route { uint32_t op, src, dst; };
+constexpr Route kRoutes[] = {
+    {143, WAFER_FMT_I16, WAFER_FMT_F16}, {144, WAFER_FMT_I16, WAFER_FMT_BF16},
+    {145, WAFER_FMT_I16, WAFER_FMT_F32}, {147, WAFER_FMT_I32, WAFER_FMT_F16},
+    {148, WAFER_FMT_I32, WAFER_FMT_BF16}, {149, WAFER_FMT_I32, WAFER_FMT_F32},
+    {152, WAFER_FMT_BF16, WAFER_FMT_I16}, {153, WAFER_FMT_BF16, WAFER_FMT_I32},
+    {154, WAFER_FMT_BF16, WAFER_FMT_F16}, {155, WAFER_FMT_BF16, WAFER_FMT_F32},
+    {158, WAFER_FMT_F16, WAFER_FMT_I16}, {159, WAFER_FMT_F16, WAFER_FMT_I32},
+    {160, WAFER_FMT_F16, WAFER_FMT_BF16}, {161, WAFER_FMT_F16, WAFER_FMT_F32},
+    {164, WAFER_FMT_F32, WAFER_FMT_I16}, {165, WAFER_FMT_F32, WAFER_FMT_I32},
+    {166, WAFER_FMT_F32, WAFER_FMT_F16}, {167, WAFER_FMT_F32, WAFER_FMT_BF16}};
+
+// Round a non-negative integer magnitude to `bits` significant bits, RNE.
+__device__ inline int64_t round_mag(int64_t mag, int bits) {
+  if (mag == 0) return 0;
+  const int msb = 63 - __builtin_clzll((unsigned long long)mag);
+  const int drop = msb - (bits - 1);
+  if (drop <= 0) return mag;
+  int64_t q = mag >> drop;
+  const int64_t rem = mag & ((1ll << drop) - 1);
+  const int64_t half = 1ll << (drop - 1);
+  if (rem > half || (rem == half && (q & 1))) ++q;
+  return q << drop;
+}
+
+// status: 0 ok, 1 non-finite float->int input, 2 out of range.
+__global__ __launch_bounds__(256) void convert_kernel(uint32_t sf, uint32_t df,
+                                                      const void *__restrict__ src,
+                                                      void *__restrict__ dst, uint64_t count,
+                                                      int *__restrict__ status) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+    const bool sfloat = sf == WAFER_FMT_F32 || sf == WAFER_FMT_BF16 || sf == WAFER_FMT_F16;
+    const bool dfloat = df == WAFER_FMT_F32 || df == WAFER_FMT_BF16 || df == WAFER_FMT_F16;
+    if (sfloat && dfloat) {
+      const float v = sf == WAFER_FMT_F32 ? ((const float *)src)[i]
+                      : sf == WAFER_FMT_BF16 ? bf16_to_f32(((const uint16_t *)src)[i])
+                                             : f16_to_f32(((const uint16_t *)src)[i]);
+      if (df == WAFER_FMT_F32) ((float *)dst)[i] = v;
+      else if (df == WAFER_FMT_BF16) ((uint16_t *)dst)[i] = f32_to_bf16(v);
+      else ((uint16_t *)dst)[i] = f32_to_f16(v);
+    } else if (!sfloat) {
+      const int64_t v = sf == WAFER_FMT_I16 ? (int64_t)((const int16_t *)src)[i]
+                                            : (int64_t)((const int32_t *)src)[i];
+      const int64_t mag = v < 0 ? -v : v;
+      const uint16_t sign = v < 0 ? 0x8000u : 0u;
+      if (df == WAFER_FMT_F32) {
+        ((float *)dst)[i] = (float)v;  // v_cvt_f32_i32 rounds to nearest even
+      } else if (df == WAFER_FMT_BF16) {
+        // one rounding from the exact integer to 8 significant bits
+        const int64_t keep = round_mag(mag, 8);
+        ((uint16_t *)dst)[i] = mag == 0 ? sign : (uint16_t)(sign | (f32_to_bf16((float)keep) & 0x7fffu));
+      } else {
+        uint16_t h;
+        if (mag >= 65520) h = (uint16_t)(sign | 0x7c00u);
+        else h = (uint16_t)(sign | f32_to_f16((float)round_mag(mag, 11)));
+        ((uint16_t *)dst)[i] = h;
+      }
+    } else {
+      const float v = sf == WAFER_FMT_F32 ? ((const float *)src)[i]
+                      : sf == WAFER_FMT_BF16 ? bf16_to_f32(((const uint16_t *)src)[i])
+                                             : f16_to_f32(((const uint16_t *)src)[i]);
+      if (!(fabsf(v) <= 3.402823466e38f)) { atomicMax(status, 1); continue; }
+      const float r = rintf(v);  // nearest even
+      if (df == WAFER_FMT_I32) {
+        if (r < -2147483648.0f || r >= 2147483648.0f) { atomicMax(status, 2); continue; }
+        ((int32_t *)dst)[i] = (int32_t)r;
+      } else {
+        if (r < -32768.0f || r > 32767.0f) { atomicMax(status, 2); continue; }
+        ((int16_t *)dst)[i] = (int16_t)r;
+      }
+    }
+  }
+}
+
+// ---- reduce ------------------------------------------------------------------
+struct ReduceGeom {
+  int rank;
+  int64_t shape[8];
+  int64_t in_stride[8];  // row-major strides of the input
+  int kept[8], nkept;    // kept dimensions, outer to inner
+  int red[8], nred;      // reduced dimensions, outer to inner
+  int64_t red_count, out_count;
+};
+
+template <uint32_t F>
+__global__ __launch_bounds__(256) void reduce_kernel(ReduceGeom g, int op,
+                                                     const void *__restrict__ src,
+                                                     void *__restrict__ dst) {
+  const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= g.out_count) return;
+  // base offset of this output's inputs
+  int64_t rem = o, base = 0;
+  for (int t = g.nkept - 1; t >= 0; --t) {
+    const int d = g.kept[t];
+    base += (rem % g.shape[d]) * g.in_stride[d];
+    rem /= g.shape[d];
+  }
+  float acc = op == 1 ? -__builtin_inff() : op == 2 ? __builtin_inff() : 0.0f;
+  int64_t coord[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int64_t r = 0; r < g.red_count; ++r) {
+    int64_t off = base;
+    for (int t = 0; t < g.nred; ++t) off += coord[t] * g.in_stride[g.red[t]];
+    const float v = load_as_f32<F>(src, off);
+    if (op == 0) {
+      acc = acc + v;
+    } else if (acc == 0.0f && v == 0.0f) {
+      const bool neg = op == 1 ? (signbit(acc) && signbit(v)) : (signbit(acc) || signbit(v));
+      acc = neg ? -0.0f : 0.0f;
+    } else {
+      acc = op == 1 ? fmaxf(acc, v) : fminf(acc, v);
+    }
+    for (int t = g.nred - 1; t >= 0; --t) {
+      if (++coord[t] < g.shape[g.red[t]]) break;
+      coord[t] = 0;
+    }
+  }
+  if (acc != acc) acc = u2f(0x7fc00000u);
+  store_from_f32<F>(dst, o, acc);
+}
+
+}  // namespace
+}  // namespace wafer
+
+using namespace wafer;
+
+extern "C" int wafer_hip_elementwise(wafer_hip_context *ctx, uint32_t op, uint32_t format,
+                                     const void *in0, const void *in1, void *dst, uint64_t count) {
+  WAFER_CHECK_CTX(ctx);
+  const int arity = ew_arity(op);
+  if (arity == 0)
+    return fail(WAFER_HIP_E_UNSUPPORTED, "elementwise: operation is not in the managed domain");
+  if (!is_float_format(format))
+    return fail(WAFER_HIP_E_UNSUPPORTED, "elementwise: format must be F16, BF16 or F32");
+  if (count == 0) return WAFER_HIP_OK;
+  if (!in0 || !dst || (arity == 2 && !in1))
+    return fail(WAFER_HIP_E_INVALID_FIELD, "elementwise: null tensor");
+  if (arity == 1) in1 = nullptr;
+  WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
+  hipStream_t st = ctx->stream;
+  switch (op) {
+#define EW_CASE(OPV) case OPV: return launch_ew<OPV>(format, st, in0, in1, dst, count);
+  EW_CASE(EW_ABS) EW_CASE(EW_RECIP) EW_CASE(EW_SQUARE) EW_CASE(EW_SQRT) EW_CASE(EW_RSQRT)
+  EW_CASE(EW_NEG) EW_CASE(EW_MAX) EW_CASE(EW_MIN) EW_CASE(EW_ADD) EW_CASE(EW_SUB)
+  EW_CASE(EW_MUL) EW_CASE(EW_LOG2) EW_CASE(EW_LN) EW_CASE(EW_POW2) EW_CASE(EW_EXP)
+  EW_CASE(EW_EXPLP) EW_CASE(EW_SIN) EW_CASE(EW_COS) EW_CASE(EW_TANH) EW_CASE(EW_SIGMOID)
+  EW_CASE(EW_RELU) EW_CASE(EW_SOFTPLUS)
+#undef EW_CASE
+  default: return fail(WAFER_HIP_E_UNSUPPORTED, "elementwise: unknown operation");
+  }
+}
+
+extern "C" int wafer_hip_convert(wafer_hip_context *ctx, uint32_t opcode, uint32_t rounding,
+                                 const void *src, void *dst, uint64_t count) {
+  WAFER_CHECK_CTX(ctx);
+  if (rounding != 0) return fail(WAFER_HIP_E_UNSUPPORTED, "convert: only NearestEven rounding is served");
+  const Route *route = nullptr;
+  for (const Route &r : kRoutes)
+    if (r.op == opcode) route = &r;
+  if (!route) return fail(WAFER_HIP_E_UNSUPPORTED, "convert: unknown or unserved route " + std::to_string(opcode));
+  if (count == 0) return WAFER_HIP_OK;
+  if (!src || !dst) return fail(WAFER_HIP_E_INVALID_FIELD, "convert: null tensor");
+  WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
+  const bool checks = !is_float_format(route->dst);
+  int *status = nullptr;
+  if (checks) {
+    WAFER_TRY(ensure_workspace(ctx, &ctx->workspace, &ctx->workspace_bytes, 256));
+    status = (int *)ctx->workspace;
+    WAFER_TRY(check_hip(hipMemsetAsync(status, 0, sizeof(int), ctx->stream), "hipMemsetAsync"));
+  }
+  const unsigned blocks = (unsigned)std::min<uint64_t>((count + 255) / 256, 65536);
+  hipLaunchKernelGGL(convert_kernel, dim3(blocks), dim3(256), 0, ctx->stream, route->src, route->dst,
+                     src, dst, count, status);
+  WAFER_TRY(launch_status("convert_kernel"));
+  if (checks) {
+    int host = 0;
+    WAFER_TRY(check_hip(hipMemcpyAsync(&host, status, sizeof(int), hipMemcpyDeviceToHost, ctx->stream),
+                        "hipMemcpyAsync"));
+    WAFER_TRY(check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize"));
+    if (host == 1) return fail(WAFER_HIP_E_NUMERIC, "convert: non-finite input to an integer route");
+    if (host == 2) return fail(WAFER_HIP_E_NUMERIC, "convert: value out of the integer range");
+  }
+  return WAFER_HIP_OK;
+}
+
+extern "C" int wafer_hip_reduce(wafer_hip_context *ctx, uint32_t op, uint32_t dim, uint32_t format,
+                                const int64_t *shape, uint32_t rank, const void *src, void *dst) {
+  WAFER_CHECK_CTX(ctx);
+  if (op > 2) return fail(WAFER_HIP_E_UNSUPPORTED, "reduce: only Sum, Max and Min are in the managed domain");
+  if (!is_float_format(format)) return fail(WAFER_HIP_E_UNSUPPORTED, "reduce: format must be F16, BF16 or F32");
+  if (op == 0 && format != WAFER_FMT_F32)
+    return fail(WAFER_HIP_E_UNSUPPORTED, "reduce: Sum is F32 only");
+  if (!shape || rank == 0 || rank > 8) return fail(WAFER_HIP_E_INVALID_FIELD, "reduce: rank must be 1..8");
+  int mask[8] = {0};
+  int t[3], nt = 0;
+  switch (dim) {
+  case 0: case 1: case 2: case 3:
+    if (dim < rank) t[nt++] = (int)(rank - 1 - dim);
+    break;
+  case 4:
+    if (rank >= 3) { t[nt++] = (int)rank - 3; t[nt++] = (int)rank - 2; }
+    break;
+  case 5:
+    if (rank >= 3) { t[nt++] = (int)rank - 3; t[nt++] = (int)rank - 2; t[nt++] = (int)rank - 1; }
+    break;
+  default:
+    return fail(WAFER_HIP_E_INVALID_FIELD, "reduce: unknown dimension selector");
+  }
+  if (nt == 0) return fail(WAFER_HIP_E_INVALID_FIELD, "reduce has no logical dimensions");
+  for (int i = 0; i < nt; ++i) mask[t[i]] = 1;
+  ReduceGeom g{};
+  g.rank = (int)rank;
+  int64_t stride = 1;
+  g.red_count = 1;
+  g.out_count = 1;
+  for (int d = (int)rank - 1; d >= 0; --d) {
+    if (shape[d] < 0) return fail(WAFER_HIP_E_INVALID_FIELD, "reduce: negative dimension");
+    g.shape[d] = shape[d];
+    g.in_stride[d] = stride;
+    stride *= shape[d];
+  }
+  for (int d = 0; d < (int)rank; ++d) {
+    if (mask[d]) { g.red[g.nred++] = d; g.red_count *= shape[d]; }
+    else { g.kept[g.nkept++] = d; g.out_count *= shape[d]; }
+  }
+  if (g.out_count == 0) return WAFER_HIP_OK;
+  if (!src || !dst) return fail(WAFER_HIP_E_INVALID_FIELD, "reduce: null tensor");
+  WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
+  const unsigned blocks = (unsigned)((g.out_count + 255) / 256);
+  if (format == WAFER_FMT_F32)
+    hipLaunchKernelGGL(reduce_kernel<WAFER_FMT_F32>, dim3(blocks), dim3(256), 0, ctx->stream, g, (int)op, src, dst);
+  else if (format == WAFER_FMT_BF16)
+    hipLaunchKernelGGL(reduce_kernel<WAFER_FMT_BF16>, dim3(blocks), dim3(256), 0, ctx->stream, g, (int)op, src, dst);
+  else
+    hipLaunchKernelGGL(reduce_kernel<WAFER_FMT_F16>, dim3(blocks), dim3(256), 0, ctx->stream, g, (int)op, src, dst);
+  return launch_status("reduce_kernel");
+}

@@ -1,0 +1,147 @@
+// gemm_formal.hip -- per-command GEMM with the reference's formal semantics.
+//
+// executeGemm (lib/Wafer/Simulator/Reference/Numeric/FormalTensorNumeric.cpp:272-361)
+// with evaluateFormalGemmFusedMultiplyAdd
+// (lib/Wafer/Simulator/Reference/Formal/FormalNumericGemm.cpp:24-113) and
+// evaluateFormalGemmFinalize (:116-157): per output, acc = +0, then for
+// k = 0..K-1 in order acc = fma(widen(lhs), widen(rhs), acc) (binary32, one
+// RNE rounding: v_fma_f32), then acc = acc + psum (F32 add) when a partial
+// sum is given, then one RNE narrowing to the destination format.  NaN
+// results are the canonical quiet NaN.  Orientation changes indexing only
+// (:302-309).  Because every output keeps the exact k-order chain, results
+// are bit-identical to the formal lane, not merely close.
+//
+// Layout on the GPU: 64x64 output tile per 256-thread workgroup, 4x4
+// independent fma chains per thread (ILP across chains, never inside one),
+// operands widened to f32 once into LDS in 16-deep k slices.
+#include "common.h"
+
+namespace wafer {
+namespace {
+
+constexpr int TM = 64, TN = 64, TK = 16;
+
+template <uint32_t IN, uint32_t OUT>
+__global__ __launch_bounds__(256) void gemm_formal_kernel(
+    const void *__restrict__ lhs, const void *__restrict__ rhs, void *__restrict__ dst,
+    const float *__restrict__ psum, int m, int k, int n, int lhs_t, int rhs_t) {
+  __shared__ float As[TK][TM + 1];
+  __shared__ float Bs[TK][TN + 1];
+  const int b = blockIdx.z;
+  const int m0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int64_t lb = (int64_t)b * m * k, rb = (int64_t)b * k * n, ob = (int64_t)b * m * n;
+
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+
+  for (int k0 = 0; k0 < k; k0 += TK) {
+    // 64 x 16 slice of lhs and 16 x 64 slice of rhs, 4 elements per thread each
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int e = tid + 256 * r;
+      const int kk = e & 15, mm = e >> 4;  // lhs: row mm, depth kk
+      const int gm = m0 + mm, gk = k0 + kk;
+      float a = 0.0f;
+      if (gm < m && gk < k)
+        a = load_as_f32<IN>(lhs, lb + (lhs_t ? (int64_t)gk * m + gm : (int64_t)gm * k + gk));
+      As[kk][mm] = a;
+      const int nn = e & 63, kb = e >> 6;  // rhs: depth kb, column nn
+      const int gn = n0 + nn, gk2 = k0 + kb;
+      float bv = 0.0f;
+      if (gn < n && gk2 < k)
+        bv = load_as_f32<IN>(rhs, rb + (rhs_t ? (int64_t)gn * k + gk2 : (int64_t)gk2 * n + gn));
+      Bs[kb][nn] = bv;
+    }
+    __syncthreads();
+    const int kend = min(TK, k - k0);
+    for (int kk = 0; kk < kend; ++kk) {
+      float av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = As[kk][ty + 16 * i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = Bs[kk][tx + 16 * j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int gm = m0 + ty + 16 * i, gn = n0 + tx + 16 * j;
+      if (gm >= m || gn >= n) continue;
+      float v = acc[i][j];
+      const int64_t o = ob + (int64_t)gm * n + gn;
+      if (psum) v = v + psum[o];
+      if (v != v) v = u2f(0x7fc00000u);
+      store_from_f32<OUT>(dst, o, v);
+    }
+}
+
+template <uint32_t IN>
+int launch_out(uint32_t out, dim3 grid, hipStream_t st, const void *lhs, const void *rhs,
+               void *dst, const float *psum, int m, int k, int n, int lt, int rt) {
+  switch (out) {
+  case WAFER_FMT_F32:
+    hipLaunchKernelGGL((gemm_formal_kernel<IN, WAFER_FMT_F32>), grid, dim3(256), 0, st, lhs, rhs,
+                       dst, psum, m, k, n, lt, rt);
+    break;
+  case WAFER_FMT_BF16:
+    hipLaunchKernelGGL((gemm_formal_kernel<IN, WAFER_FMT_BF16>), grid, dim3(256), 0, st, lhs, rhs,
+                       dst, psum, m, k, n, lt, rt);
+    break;
+  default:
+    hipLaunchKernelGGL((gemm_formal_kernel<IN, WAFER_FMT_F16>), grid, dim3(256), 0, st, lhs, rhs,
+                       dst, psum, m, k, n, lt, rt);
+    break;
+  }
+  return launch_status("gemm_formal_kernel");
+}
+
+}  // namespace
+}  // namespace wafer
+
+using namespace wafer;
+
+extern "C" int wafer_hip_gemm(wafer_hip_context *ctx, const void *lhs, const void *rhs,
+                              void *dst, const void *psum, uint32_t m, uint32_t k, uint32_t n,
+                              uint32_t batch, uint32_t in_format, uint32_t out_format,
+                              uint32_t psum_format, uint32_t lhs_orientation,
+                              uint32_t rhs_orientation) {
+  WAFER_CHECK_CTX(ctx);
+  // validateFormalGemmOperation bounds (lib/Wafer/Simulator/Reference/Formal/FormalOperations.cpp:274-281)
+  if (m == 0 || k == 0 || n == 0 || batch == 0 || m > 65535 || k > 65535 || n > 65535 ||
+      batch > 65535)
+    return fail(WAFER_HIP_E_INVALID_FIELD, "gemm: m, k, n and batch must be in [1, 65535]");
+  if (!is_float_format(in_format) || !is_float_format(out_format))
+    return fail(WAFER_HIP_E_UNSUPPORTED, "gemm: formats must be F16, BF16 or F32");
+  if (lhs_orientation > 1 || rhs_orientation > 1)
+    return fail(WAFER_HIP_E_INVALID_FIELD, "gemm: orientation must be Normal (0) or Transpose (1)");
+  const float *ps = nullptr;
+  if (psum_format != WAFER_GEMM_PSUM_DISABLED) {
+    if (psum_format != WAFER_FMT_F32)
+      return fail(WAFER_HIP_E_UNSUPPORTED, "gemm: partial sums must be F32");
+    if (!psum) return fail(WAFER_HIP_E_INVALID_FIELD, "gemm: psum format given without a psum tensor");
+    ps = (const float *)psum;
+  }
+  if (!lhs || !rhs || !dst) return fail(WAFER_HIP_E_INVALID_FIELD, "gemm: null tensor");
+  WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
+  dim3 grid((n + TN - 1) / TN, (m + TM - 1) / TM, batch);
+  const int lt = (int)lhs_orientation, rt = (int)rhs_orientation;
+  switch (in_format) {
+  case WAFER_FMT_F32:
+    return launch_out<WAFER_FMT_F32>(out_format, grid, ctx->stream, lhs, rhs, dst, ps, m, k, n, lt, rt);
+  case WAFER_FMT_BF16:
+    return launch_out<WAFER_FMT_BF16>(out_format, grid, ctx->stream, lhs, rhs, dst, ps, m, k, n, lt, rt);
+  default:
+    return launch_out<WAFER_FMT_F16>(out_format, grid, ctx->stream, lhs, rhs, dst, ps, m, k, n, lt, rt);
+  }
+}

@@ -1,0 +1,233 @@
+// regions.hip -- fused TileRegions: RMSNorm, softmax, SwiGLU, GELU-tanh,
+// RoPE and bias-add, each one coalesced single pass over HBM (two reads of
+// the row for the row-reduction regions, the second from L2).
+//
+// Each region is the composition of managed elementwise / reduce commands
+// the compiler emits for it, with the op mapping of getInstrElementwiseKindAttr
+// (lib/Wafer/Conversion/TileToInstr/ComputeLowering.cpp:2555-2606): Exp ->
+// ExpLp, Div -> Recip then Mul, no tile-level Sigmoid.  Intermediates stay
+// F32 and are rounded per operation in the same order as the commands
+// (built with -ffp-contract=off, so no multiply-add is fused), with one
+// narrowing at the region output.  The row sums use a parallel tree, so they
+// match the host's left-to-right sums within tolerance rather than bit for
+// bit; every other step is the same IEEE operation sequence.
+#include "common.h"
+
+namespace wafer {
+namespace {
+
+constexpr int RT = 256;  // threads per row workgroup
+
+__device__ inline float block_sum(float v, float *red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < RT / 64; ++i) s += red[i];
+  __syncthreads();
+  return s;
+}
+__device__ inline float block_max(float v, float *red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float s = red[0];
+#pragma unroll
+  for (int i = 1; i < RT / 64; ++i) s = fmaxf(s, red[i]);
+  __syncthreads();
+  return s;
+}
+
+__device__ inline float explp_acc(float x) { return exp2f(x * 0x1.715476p+0f); }
+
+// y = x * Rsqrt(Sum(x*x) * (1/N) + eps) * w
+template <uint32_t F>
+__global__ __launch_bounds__(RT) void rmsnorm_kernel(const void *__restrict__ x,
+                                                     const void *__restrict__ w,
+                                                     void *__restrict__ y, int64_t cols,
+                                                     float inv_n, float eps) {
+  __shared__ float red[RT / 64];
+  const int64_t base = (int64_t)blockIdx.x * cols;
+  float s = 0.0f;
+  for (int64_t c = threadIdx.x; c < cols; c += RT) {
+    const float v = load_as_f32<F>(x, base + c);
+    s += v * v;
+  }
+  s = block_sum(s, red);
+  const float rs = 1.0f / sqrtf(s * inv_n + eps);
+  for (int64_t c = threadIdx.x; c < cols; c += RT) {
+    const float v = load_as_f32<F>(x, base + c);
+    store_from_f32<F>(y, base + c, v * rs * load_as_f32<F>(w, c));
+  }
+}
+
+// e = ExpLp(x - rowmax); y = e * Recip(Sum(e))
+template <uint32_t F>
+__global__ __launch_bounds__(RT) void softmax_kernel(const void *__restrict__ x,
+                                                     void *__restrict__ y, int64_t cols) {
+  __shared__ float red[RT / 64];
+  const int64_t base = (int64_t)blockIdx.x * cols;
+  float m = -__builtin_inff();
+  for (int64_t c = threadIdx.x; c < cols; c += RT) m = fmaxf(m, load_as_f32<F>(x, base + c));
+  m = block_max(m, red);
+  float s = 0.0f;
+  for (int64_t c = threadIdx.x; c < cols; c += RT) s += explp_acc(load_as_f32<F>(x, base + c) - m);
+  s = block_sum(s, red);
+  const float rc = 1.0f / s;
+  for (int64_t c = threadIdx.x; c < cols; c += RT)
+    store_from_f32<F>(y, base + c, explp_acc(load_as_f32<F>(x, base + c) - m) * rc);
+}
+
+// y = g * Recip(1 + ExpLp(-g)) * u
+template <uint32_t F>
+__global__ __launch_bounds__(256) void silu_mul_kernel(const void *__restrict__ gate,
+                                                       const void *__restrict__ up,
+                                                       void *__restrict__ y, uint64_t count) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+    const float g = load_as_f32<F>(gate, (int64_t)i);
+    const float sig = 1.0f / (1.0f + explp_acc(-g));
+    store_from_f32<F>(y, (int64_t)i, g * sig * load_as_f32<F>(up, (int64_t)i));
+  }
+}
+
+// y = 0.5*x*(1 + Tanh(sqrt(2/pi)*(x + 0.044715*x^3)))
+template <uint32_t F>
+__global__ __launch_bounds__(256) void gelu_tanh_kernel(const void *__restrict__ x,
+                                                        void *__restrict__ y, uint64_t count) {
+  const float k0 = 0.7978845608028654f, k1 = 0.044715f;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+    const float v = load_as_f32<F>(x, (int64_t)i);
+    const float inner = k0 * (v + k1 * (v * v * v));
+    store_from_f32<F>(y, (int64_t)i, 0.5f * v * (1.0f + tanhf(inner)));
+  }
+}
+
+// Rotate-half RoPE: inv_freq[i] = 1/theta^(2i/D), angle = pos*inv_freq[d mod D/2],
+// y = x*cos(angle) + rotate_half(x)*sin(angle), rotate_half(x) = [-x2, x1].
+template <uint32_t F>
+__global__ __launch_bounds__(256) void rope_kernel(const void *__restrict__ x, void *__restrict__ y,
+                                                   int64_t tokens, int64_t heads, int64_t head_dim,
+                                                   const int32_t *__restrict__ positions,
+                                                   float theta) {
+  const int64_t count = tokens * heads * head_dim;
+  const int64_t half = head_dim / 2;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < count; e += stride) {
+    const int64_t d = e % head_dim;
+    const int64_t row = e - d;
+    const int64_t t = e / (heads * head_dim);
+    const int64_t i = d % half;
+    const float inv_freq = 1.0f / powf(theta, (float)(2 * i) / (float)head_dim);
+    const float angle = (float)positions[t] * inv_freq;
+    const float c = cosf(angle), s = sinf(angle);
+    const float xv = load_as_f32<F>(x, e);
+    const float rot = d < half ? -load_as_f32<F>(x, row + d + half) : load_as_f32<F>(x, row + d - half);
+    store_from_f32<F>(y, e, xv * c + rot * s);
+  }
+}
+
+template <uint32_t F>
+__global__ __launch_bounds__(256) void bias_add_kernel(const void *__restrict__ x,
+                                                       const float *__restrict__ bias,
+                                                       void *__restrict__ y, int64_t rows,
+                                                       int64_t cols) {
+  const int64_t count = rows * cols;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < count; e += stride)
+    store_from_f32<F>(y, e, load_as_f32<F>(x, e) + bias[e % cols]);
+}
+
+unsigned grid_for(uint64_t count) {
+  return (unsigned)std::min<uint64_t>((count + 255) / 256, 65536);
+}
+
+#define DISPATCH_F(format, KERNEL, GRID, BLOCK, ...)                                           \
+  do {                                                                                         \
+    if ((format) == WAFER_FMT_F32)                                                             \
+      hipLaunchKernelGGL(KERNEL<WAFER_FMT_F32>, GRID, BLOCK, 0, ctx->stream, __VA_ARGS__);    \
+    else if ((format) == WAFER_FMT_BF16)                                                       \
+      hipLaunchKernelGGL(KERNEL<WAFER_FMT_BF16>, GRID, BLOCK, 0, ctx->stream, __VA_ARGS__);   \
+    else                                                                                       \
+      hipLaunchKernelGGL(KERNEL<WAFER_FMT_F16>, GRID, BLOCK, 0, ctx->stream, __VA_ARGS__);    \
+  } while (0)
+
+int prologue(wafer_hip_context *ctx, uint32_t format, const char *what) {
+  WAFER_CHECK_CTX(ctx);
+  if (!is_float_format(format))
+    return fail(WAFER_HIP_E_UNSUPPORTED, std::string(what) + ": format must be F16, BF16 or F32");
+  return check_hip(hipSetDevice(ctx->device), "hipSetDevice");
+}
+
+}  // namespace
+}  // namespace wafer
+
+using namespace wafer;
+
+extern "C" int wafer_hip_rmsnorm(wafer_hip_context *ctx, uint32_t format, const void *x,
+                                 const void *w, void *y, uint64_t rows, uint64_t cols, float eps) {
+  WAFER_TRY(prologue(ctx, format, "rmsnorm"));
+  if (rows == 0 || cols == 0) return WAFER_HIP_OK;
+  if (!x || !w || !y) return fail(WAFER_HIP_E_INVALID_FIELD, "rmsnorm: null tensor");
+  if (rows > 0x7fffffffull) return fail(WAFER_HIP_E_INVALID_FIELD, "rmsnorm: too many rows");
+  const float inv_n = 1.0f / (float)cols;
+  DISPATCH_F(format, rmsnorm_kernel, dim3((unsigned)rows), dim3(RT), x, w, y, (int64_t)cols, inv_n, eps);
+  return launch_status("rmsnorm_kernel");
+}
+
+extern "C" int wafer_hip_softmax(wafer_hip_context *ctx, uint32_t format, const void *x, void *y,
+                                 uint64_t rows, uint64_t cols) {
+  WAFER_TRY(prologue(ctx, format, "softmax"));
+  if (rows == 0 || cols == 0) return WAFER_HIP_OK;
+  if (!x || !y) return fail(WAFER_HIP_E_INVALID_FIELD, "softmax: null tensor");
+  if (rows > 0x7fffffffull) return fail(WAFER_HIP_E_INVALID_FIELD, "softmax: too many rows");
+  DISPATCH_F(format, softmax_kernel, dim3((unsigned)rows), dim3(RT), x, y, (int64_t)cols);
+  return launch_status("softmax_kernel");
+}
+
+extern "C" int wafer_hip_silu_mul(wafer_hip_context *ctx, uint32_t format, const void *gate,
+                                  const void *up, void *y, uint64_t count) {
+  WAFER_TRY(prologue(ctx, format, "silu_mul"));
+  if (count == 0) return WAFER_HIP_OK;
+  if (!gate || !up || !y) return fail(WAFER_HIP_E_INVALID_FIELD, "silu_mul: null tensor");
+  DISPATCH_F(format, silu_mul_kernel, dim3(grid_for(count)), dim3(256), gate, up, y, count);
+  return launch_status("silu_mul_kernel");
+}
+
+extern "C" int wafer_hip_gelu_tanh(wafer_hip_context *ctx, uint32_t format, const void *x, void *y,
+                                   uint64_t count) {
+  WAFER_TRY(prologue(ctx, format, "gelu_tanh"));
+  if (count == 0) return WAFER_HIP_OK;
+  if (!x || !y) return fail(WAFER_HIP_E_INVALID_FIELD, "gelu_tanh: null tensor");
+  DISPATCH_F(format, gelu_tanh_kernel, dim3(grid_for(count)), dim3(256), x, y, count);
+  return launch_status("gelu_tanh_kernel");
+}
+
+extern "C" int wafer_hip_rope(wafer_hip_context *ctx, uint32_t format, const void *x, void *y,
+                              uint64_t tokens, uint64_t heads, uint64_t head_dim,
+                              const int32_t *positions, float theta) {
+  WAFER_TRY(prologue(ctx, format, "rope"));
+  if (head_dim % 2) return fail(WAFER_HIP_E_INVALID_FIELD, "rope: head_dim must be even");
+  const uint64_t count = tokens * heads * head_dim;
+  if (count == 0) return WAFER_HIP_OK;
+  if (!x || !y || !positions) return fail(WAFER_HIP_E_INVALID_FIELD, "rope: null tensor");
+  DISPATCH_F(format, rope_kernel, dim3(grid_for(count)), dim3(256), x, y, (int64_t)tokens,
+             (int64_t)heads, (int64_t)head_dim, positions, theta);
+  return launch_status("rope_kernel");
+}
+
+extern "C" int wafer_hip_bias_add(wafer_hip_context *ctx, uint32_t format, const void *x,
+                                  const float *bias, void *y, uint64_t rows, uint64_t cols) {
+  WAFER_TRY(prologue(ctx, format, "bias_add"));
+  if (rows * cols == 0) return WAFER_HIP_OK;
+  if (!x || !bias || !y) return fail(WAFER_HIP_E_INVALID_FIELD, "bias_add: null tensor");
+  DISPATCH_F(format, bias_add_kernel, dim3(grid_for(rows * cols)), dim3(256), x, bias, y,
+             (int64_t)rows, (int64_t)cols);
+  return launch_status("bias_add_kernel");
+}
