@@ -540,3 +540,44 @@ def test_invalid_arguments_fail_without_launch(hip, B):
         hip.gemm(t, t, t, 0, 1, 1)
     with pytest.raises(B.WaferHipError):
         hip.gemm_i8(t, t, t, t, 100, 64, 128)
+
+
+def test_split_state_counters_rearm(hip, B, oracle):
+    """FA's split pieces and FD's fused fold use arrival counters that every
+    launch re-arms: repeated launches are bit-identical, and a large FD shape
+    followed by a smaller one (counters at other indices) stays correct."""
+    say("counters re-arm")
+    rng = np.random.default_rng(77)
+    q, k, v = (_bf16_randn(oracle, rng, (1, 4, 1024, 128)) for _ in range(3))
+    outs = []
+    for _ in range(3):
+        o = torch.zeros((1, 4, 1024, 128), dtype=torch.int16, device="cuda")
+        hip.attention_prefill(u16(q), u16(k), u16(v), o, 0.088, causal=True)
+        outs.append(host(o))
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[1], outs[2])
+    ref = oracle.attention_prefill(q, k, v, 0.088, causal=True, block_k=64)
+    attention_gate(oracle.bf16_to_f32(outs[0].view(np.uint16)), oracle.bf16_to_f32(ref), what="FA repeated")
+    for (Bn, Hq, Hkv, L) in [(8, 16, 4, 2048), (2, 4, 2, 300), (8, 16, 4, 2048)]:
+        qd = _bf16_randn(oracle, rng, (Bn, Hq, 1, 128))
+        kd = _bf16_randn(oracle, rng, (Bn, Hkv, L, 128))
+        vd = _bf16_randn(oracle, rng, (Bn, Hkv, L, 128))
+        o = torch.zeros((Bn, Hq, 1, 128), dtype=torch.int16, device="cuda")
+        hip.attention_decode(u16(qd), u16(kd), u16(vd), o, 0.088, chunks=16)
+        ref = oracle.attention_decode(qd, kd, vd, 0.088, chunks=16, block_k=64)
+        attention_gate(oracle.bf16_to_f32(from_u16(o)), oracle.bf16_to_f32(ref), what=f"FD {Bn}x{L}")
+
+
+@pytest.mark.parametrize("Bn,Hq,Hkv,L,chunks", [(64, 8, 4, 2048, 16), (48, 16, 4, 1000, 5), (64, 4, 4, 777, 16),
+                                               (32, 8, 8, 513, 3)])
+def test_fd_decode_group_path(hip, B, oracle, Bn, Hq, Hkv, L, chunks):
+    """Large batch*kv_heads takes the one-workgroup-per-(batch, kv head)
+    path (16 waves, waves split the chunks); ragged chunk lengths included."""
+    say("fd group path", Bn, Hq, Hkv, L, chunks)
+    rng = np.random.default_rng(L + Bn)
+    q = _bf16_randn(oracle, rng, (Bn, Hq, 1, 128))
+    k = _bf16_randn(oracle, rng, (Bn, Hkv, L, 128))
+    v = _bf16_randn(oracle, rng, (Bn, Hkv, L, 128))
+    ref = oracle.attention_decode(q, k, v, 0.088, chunks=chunks, block_k=64)
+    o = torch.zeros((Bn, Hq, 1, 128), dtype=torch.int16, device="cuda")
+    hip.attention_decode(u16(q), u16(k), u16(v), o, 0.088, chunks=chunks)
+    attention_gate(oracle.bf16_to_f32(from_u16(o)), oracle.bf16_to_f32(ref), what="FD group path")

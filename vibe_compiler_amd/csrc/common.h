@@ -14,9 +14,12 @@
 struct wafer_hip_context {
   int device = 0;
   hipStream_t stream = nullptr;
-  // FD partial-state workspace (grown on demand, freed with the context).
+  // FD chunk states of the small-batch path (grown on demand, freed with
+  // the context).
   void *workspace = nullptr;
   size_t workspace_bytes = 0;
+  // Error word of the convert kernel.
+  int *status = nullptr;
   // Scratch for operand re-layout (transposed rhs), grown on demand.
   void *relayout = nullptr;
   size_t relayout_bytes = 0;

@@ -261,8 +261,8 @@ extern "C" int wafer_hip_convert(wafer_hip_context *ctx, uint32_t opcode, uint32
   const bool checks = !is_float_format(route->dst);
   int *status = nullptr;
   if (checks) {
-    WAFER_TRY(ensure_workspace(ctx, &ctx->workspace, &ctx->workspace_bytes, 256));
-    status = (int *)ctx->workspace;
+    if (!ctx->status) WAFER_TRY(check_hip(hipMalloc((void **)&ctx->status, 256), "hipMalloc(status)"));
+    status = ctx->status;
     WAFER_TRY(check_hip(hipMemsetAsync(status, 0, sizeof(int), ctx->stream), "hipMemsetAsync"));
   }
   const unsigned blocks = (unsigned)std::min<uint64_t>((count + 255) / 256, 65536);

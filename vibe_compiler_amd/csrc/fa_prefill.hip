@@ -8,25 +8,37 @@
 //   m' = max(m, rowmax S), alpha = ExpLp(m - m'), P = ExpLp(S - m'),
 //   l = l*alpha + rowsum(P) (unrounded P), acc = acc*alpha + bf16(P).V,
 //   out = bf16(acc * (1/l)), 0 for a row with l == 0.
+// The two partial states of interleaved key sets combine with the state
+// merge of OnlineAttentionMaterialization.cpp:264-373: m = max(mL, mR),
+// sL = ExpLp(mL - m), sR = ExpLp(mR - m), l = lL sL + lR sR,
+// acc = accL sL + accR sR.
 //
 // Mapping onto CDNA4:
-//  * one workgroup = 4 waves = 128 queries of one (batch, head); each wave owns
-//    32 queries for the whole KV sweep;
-//  * scores are computed transposed, S^T = K . Q^T with
-//    v_mfma_f32_32x32x16_bf16 (A = 32 keys x 16 d from LDS, B = Q^T held in
-//    VGPRs for the whole sweep), so each lane's accumulator column is one
-//    query: row max / row sum / alpha are lane-local plus one xor-32 exchange;
-//  * the output is accumulated transposed too, O^T = V^T . P^T, so the
-//    rescale by alpha is lane-local and P^T feeds the MFMA B operand straight
-//    from the score registers (after RNE narrowing to bf16);
+//  * a workgroup (8 waves) serves two 64-query blocks of one (batch, head):
+//    block i and block n-1-i of the causal triangle, so every workgroup does
+//    the same amount of work (i+1 + n-i key blocks) and one launch of
+//    heads*n/2 workgroups fills the CUs evenly with no cross-workgroup merge;
+//  * wave w: group g = w>>2 (0: the late block, 1: the early block), query
+//    tile w&1 (32 queries), key half (w>>1)&1.  The two key halves sweep the
+//    even and the odd 64-key blocks; each SIMD holds one late-block and one
+//    early-block wave, so all SIMDs carry equal work and one wave's softmax
+//    VALU work overlaps the other's MFMAs;
+//  * scores are computed transposed, S^T = K . Q^T, on
+//    v_mfma_f32_32x32x16_bf16 (A = 32 keys x 16 d from LDS, B = Q^T kept in
+//    VGPRs), so each lane's accumulator column is one query: row max / sum /
+//    alpha are lane-local plus one xor-32 exchange;
+//  * the output is accumulated transposed as well, O^T = V^T . P^T: the
+//    rescale by alpha is lane-local and P^T feeds the MFMA B operand from the
+//    score registers after RNE narrowing (v_cvt_pk_bf16_f32).  The rescale is
+//    skipped when alpha == 1 for the whole wave (x * 1 == x exactly);
 //  * K tiles sit row-major in LDS, V tiles transposed (d-major) with keys
-//    permuted inside every 16-key group so that the 8 keys one lane needs for
-//    one MFMA are contiguous (one ds_read_b128); both are double-buffered and
-//    staged global -> VGPR -> LDS one block ahead;
-//  * causal: blocks past a wave's last query are skipped, diagonal blocks are
-//    masked; workgroups are issued longest-first, and consecutive workgroup
-//    ids walk (batch, head) so each head's blocks land on one XCD (ids are
-//    dealt round-robin over the 8 XCDs) and share that XCD's L2.
+//    permuted inside every 16-key group so the 8 keys one lane needs for one
+//    MFMA are contiguous (one ds_read_b128); per key half double-buffered and
+//    staged global -> VGPR -> LDS one iteration ahead; both query blocks of a
+//    workgroup read the same tiles for their common key prefix;
+//  * consecutive workgroup ids walk (batch*head), so each head's workgroups
+//    land on one XCD (ids are dealt round-robin over the 8 XCDs) and share
+//    its L2.
 //
 // Arithmetic note: ExpLp(S*scale - m) is evaluated as
 // exp2(fma(s_raw, scale*log2e, -m_raw*scale*log2e)) (one rounding fewer than
@@ -38,10 +50,11 @@ namespace wafer {
 namespace {
 
 constexpr int D = 128;
-constexpr int BQ = 128;           // queries per workgroup
-constexpr int BK = 64;            // keys per pipeline stage
+constexpr int QB = 64;            // queries per query block
+constexpr int BK = 64;            // keys per KV block
 constexpr int KPITCH = D + 8;     // LDS row pitch of K tiles (elements): 272 B
 constexpr int VPITCH = BK + 8;    // LDS row pitch of V^T tiles (elements): 144 B
+constexpr int THREADS = 512;
 
 __device__ inline int permute_key(int key) {
   // swap bits 2 and 3 of the key index inside its 16-key group
@@ -49,51 +62,54 @@ __device__ inline int permute_key(int key) {
 }
 
 template <bool CAUSAL>
-__global__ __launch_bounds__(256) void fa_prefill_bf16_d128(
+__global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
-    const uint16_t *__restrict__ V, uint16_t *__restrict__ O, int q_heads,
-    int kv_heads, int q_len, int kv_len, float scale_log2e, int n_qblocks,
-    int bh_count) {
-  __shared__ __align__(16) uint16_t sK[2][BK * KPITCH];
-  __shared__ __align__(16) uint16_t sV[2][D * VPITCH];
+    const uint16_t *__restrict__ V, uint16_t *__restrict__ O, int q_heads, int kv_heads,
+    int q_len, int kv_len, float c, int bh_count, int n_qblocks) {
+  __shared__ __align__(16) uint16_t sK[2][2][BK * KPITCH];  // [half][buf]
+  __shared__ __align__(16) uint16_t sV[2][2][D * VPITCH];
 
   const int bid = blockIdx.x;
-  const int rank = bid / bh_count;
-  const int bh = bid - rank * bh_count;
-  const int qb = CAUSAL ? (n_qblocks - 1 - rank) : rank;
+  const int pair = bid / bh_count;
+  const int bh = bid - pair * bh_count;
   const int b = bh / q_heads;
   const int h = bh - b * q_heads;
   const int kvh = h / (q_heads / kv_heads);
-
-  const uint16_t *Qp = Q + ((size_t)(b * q_heads + h) * q_len) * D;
+  const uint16_t *Qp = Q + ((size_t)bh * q_len) * D;
   const uint16_t *Kp = K + ((size_t)(b * kv_heads + kvh) * kv_len) * D;
   const uint16_t *Vp = V + ((size_t)(b * kv_heads + kvh) * kv_len) * D;
-  uint16_t *Op = O + ((size_t)(b * q_heads + h) * q_len) * D;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int l32 = lane & 31;
-  const int g = lane >> 5;
-  const int q0 = qb * BQ + wave * 32;
+  const int grp = wave >> 2, tile = wave & 1, half = (wave >> 1) & 1;
+  const int l32 = lane & 31, g = lane >> 5;
+  // causal: pair the early block `pair` with the late block n-1-pair
+  const int qb_lo = CAUSAL ? pair : 2 * pair;
+  const int qb_hi = CAUSAL ? n_qblocks - 1 - pair : 2 * pair + 1;
+  const int qb = grp == 0 ? qb_hi : qb_lo;
+  const int q0 = qb * QB + tile * 32;
   const int my_q = q0 + l32;
+  const int kv_blocks = kv_len / BK;
+  const int nk_hi = CAUSAL ? min(kv_blocks, qb_hi + 1) : kv_blocks;
+  const int nk_mine = CAUSAL ? min(kv_blocks, qb + 1) : kv_blocks;
 
   // Q^T as the MFMA B operand: lane holds query l32, d = s*16 + g*8 + [0,8).
   bf16x8 qreg[8];
 #pragma unroll
   for (int s = 0; s < 8; ++s)
     qreg[s] = *(const bf16x8 *)(Qp + (size_t)my_q * D + s * 16 + g * 8);
+  // Drain the Q loads here.  Without this, the waitcnt pass ties Q's
+  // registers to the in-loop prefetch loads and makes every iteration wait
+  // for the next K/V block to arrive before its first MFMA.
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
 
-  int kv_end = kv_len;
-  if (CAUSAL) kv_end = min(kv_len, (qb + 1) * BQ);
-  const int nkb = (kv_end + BK - 1) / BK;
-
-  // global -> VGPR staging coordinates
-  const int k_row = tid >> 4, k_col = (tid & 15) * 8;   // rows k_row + 16 i
-  const int v_kg = tid & 15, v_dc = tid >> 4;           // keys 4 v_kg + i, d 8 v_dc
+  // global -> VGPR staging: the 4 waves of a key half load that half's block
+  const int ltid = (((wave & 1) | ((wave >> 2) << 1)) << 6) | lane;  // 0..255 within the half
+  const int k_row = ltid >> 4, k_col = (ltid & 15) * 8;               // rows k_row + 16 i
+  const int v_kg = ltid & 15, v_dc = ltid >> 4;                       // keys 4 v_kg + i, d 8 v_dc
   const int v_pos = permute_key(4 * v_kg);
   u32x4 kst[4], vst[4];
-
   auto gload = [&](int kb) {
     const uint16_t *kp = Kp + (size_t)(kb * BK) * D;
     const uint16_t *vp = Vp + (size_t)(kb * BK) * D;
@@ -105,9 +121,10 @@ __global__ __launch_bounds__(256) void fa_prefill_bf16_d128(
       vst[i] = *(const u32x4 *)(vp + (size_t)(4 * v_kg + i) * D + 8 * v_dc);
   };
   auto sstore = [&](int buf) {
+    uint16_t *sk = sK[half][buf];
+    uint16_t *sv = sV[half][buf];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *(u32x4 *)&sK[buf][(k_row + 16 * i) * KPITCH + k_col] = kst[i];
+    for (int i = 0; i < 4; ++i) *(u32x4 *)&sk[(k_row + 16 * i) * KPITCH + k_col] = kst[i];
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       const uint32_t a0 = vst[0][w], a1 = vst[1][w], a2 = vst[2][w], a3 = vst[3][w];
@@ -116,8 +133,8 @@ __global__ __launch_bounds__(256) void fa_prefill_bf16_d128(
       lo[1] = __builtin_amdgcn_perm(a3, a2, 0x05040100u);
       hi[0] = __builtin_amdgcn_perm(a1, a0, 0x07060302u);
       hi[1] = __builtin_amdgcn_perm(a3, a2, 0x07060302u);
-      *(u32x2 *)&sV[buf][(8 * v_dc + 2 * w) * VPITCH + v_pos] = lo;
-      *(u32x2 *)&sV[buf][(8 * v_dc + 2 * w + 1) * VPITCH + v_pos] = hi;
+      *(u32x2 *)&sv[(8 * v_dc + 2 * w) * VPITCH + v_pos] = lo;
+      *(u32x2 *)&sv[(8 * v_dc + 2 * w + 1) * VPITCH + v_pos] = hi;
     }
   };
 
@@ -129,15 +146,23 @@ __global__ __launch_bounds__(256) void fa_prefill_bf16_d128(
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc_o[dt][r] = 0.0f;
 
-  gload(0);
-  sstore(0);
+  const int niter = (nk_hi + 1) / 2;
+  if (half < nk_hi) {
+    gload(half);
+    sstore(0);
+  }
   __syncthreads();
 
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int buf = kb & 1;
-    if (kb + 1 < nkb) gload(kb + 1);
-    const bool active = !CAUSAL || (kb * BK <= q0 + 31);
+  for (int i = 0; i < niter; ++i) {
+    const int buf = i & 1;
+    const int kb = 2 * i + half;
+    const int kbn = kb + 2;
+    const bool prefetch = (i + 1 < niter) && (kbn < nk_hi);
+    if (prefetch) gload(kbn);
+    const bool active = (kb < nk_mine) && (!CAUSAL || kb * BK <= q0 + 31);
     if (active) {
+      const uint16_t *sk = sK[half][buf];
+      const uint16_t *sv = sV[half][buf];
       f32x16 sacc[2];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
@@ -145,7 +170,7 @@ __global__ __launch_bounds__(256) void fa_prefill_bf16_d128(
         for (int r = 0; r < 16; ++r) sacc[t][r] = 0.0f;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-          const bf16x8 a = *(const bf16x8 *)&sK[buf][(t * 32 + l32) * KPITCH + s * 16 + g * 8];
+          const bf16x8 a = *(const bf16x8 *)&sk[(t * 32 + l32) * KPITCH + s * 16 + g * 8];
           sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[s], sacc[t], 0, 0, 0);
         }
       }
@@ -165,26 +190,28 @@ __global__ __launch_bounds__(256) void fa_prefill_bf16_d128(
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[t][r]);
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float m_new = fmaxf(m_raw, mx);
-      const float mc = (m_new == -__builtin_inff()) ? 0.0f : m_new * scale_log2e;
-      const float alpha = __builtin_amdgcn_exp2f(m_raw * scale_log2e - mc);
+      const float mc = (m_new == -__builtin_inff()) ? 0.0f : m_new * c;
+      const float alpha = __builtin_amdgcn_exp2f(m_raw * c - mc);
       float rs = 0.0f;
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][r], scale_log2e, -mc));
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][r], c, -mc));
           sacc[t][r] = p;
           rs += p;
         }
       rs += __shfl_xor(rs, 32);
       l_sum = l_sum * alpha + rs;
       m_raw = m_new;
+      if (!__all(alpha == 1.0f)) {
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
+        for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha;
-      // P^T operands: (t, half) covers keys t*32 + half*16 + [0,16); lane's 8
-      // keys are accumulator rows half*8 + [0,8) of tile t.
+          for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha;
+      }
+      // P^T operands: (t, hf) covers keys t*32 + hf*16 + [0,16); the lane's 8
+      // keys are accumulator rows hf*8 + [0,8) of tile t.
       bf16x8 pb[2][2];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
@@ -198,19 +225,48 @@ __global__ __launch_bounds__(256) void fa_prefill_bf16_d128(
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
           for (int dt = 0; dt < 4; ++dt) {
-            const bf16x8 va = *(const bf16x8 *)&sV[buf][(dt * 32 + l32) * VPITCH + t * 32 + hf * 16 + g * 8];
+            const bf16x8 va = *(const bf16x8 *)&sv[(dt * 32 + l32) * VPITCH + t * 32 + hf * 16 + g * 8];
             acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[t][hf], acc_o[dt], 0, 0, 0);
           }
     }
-    if (kb + 1 < nkb) {
-      sstore(buf ^ 1);
+    if (i + 1 < niter) {
+      if (prefetch) sstore(buf ^ 1);
       __syncthreads();
     }
   }
 
+  // ---- merge the odd-block half into the even-block half through LDS ----
+  __syncthreads();
+  float *xacc = (float *)&sK[0][0][0];  // [grp*2+tile][dt][r][lane], 64 KiB
+  float *xml = (float *)&sV[0][0][0];   // m [slot][lane], l [slot][lane]
+  const int slot = grp * 2 + tile;
+  if (half == 1) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) xacc[((slot * 4 + dt) * 16 + r) * 64 + lane] = acc_o[dt][r];
+    xml[slot * 64 + lane] = m_raw;
+    xml[256 + slot * 64 + lane] = l_sum;
+  }
+  __syncthreads();
+  if (half == 1) return;
+  {
+    const float m1 = xml[slot * 64 + lane], l1 = xml[256 + slot * 64 + lane];
+    const float m = fmaxf(m_raw, m1);
+    const float e = (m == -__builtin_inff()) ? 0.0f : m * c;
+    const float s0 = __builtin_amdgcn_exp2f(m_raw * c - e);
+    const float s1 = __builtin_amdgcn_exp2f(m1 * c - e);
+    l_sum = l_sum * s0 + l1 * s1;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        acc_o[dt][r] = acc_o[dt][r] * s0 + xacc[((slot * 4 + dt) * 16 + r) * 64 + lane] * s1;
+  }
+
   // finalize: coefficient = Recip(l) (0 for an empty row), out = bf16(acc * coef)
   const float coef = (l_sum == 0.0f) ? 0.0f : 1.0f / l_sum;
-  uint16_t *orow = Op + (size_t)my_q * D;
+  uint16_t *orow = O + ((size_t)bh * q_len + my_q) * D;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -245,27 +301,25 @@ extern "C" int wafer_hip_attention_prefill(wafer_hip_context *ctx, uint32_t form
     return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill: empty dimension");
   if (q_heads % kv_heads != 0)
     return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill: q_heads % kv_heads != 0");
-  if (q_len % BQ != 0 || kv_len % BK != 0)
+  if (q_len % (2 * QB) != 0 || kv_len % BK != 0)
     return fail(WAFER_HIP_E_UNSUPPORTED, "attention_prefill: q_len must be a multiple of 128 and kv_len of 64");
   if (causal && kv_len < q_len)
     return fail(WAFER_HIP_E_UNSUPPORTED, "attention_prefill: causal needs kv_len >= q_len");
   if (!(scale > 0.0f)) return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill: scale must be positive");
-  if ((uint64_t)batch * q_heads * (q_len / BQ) > 0x7fffffffull)
+  if ((uint64_t)batch * q_heads * (q_len / (2 * QB)) > 0x7fffffffull)
     return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill: grid too large");
   WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
-  const int n_qblocks = (int)(q_len / BQ);
+  const int n_qblocks = (int)(q_len / QB);
   const int bh_count = (int)(batch * q_heads);
   const float c = scale * 0x1.715476p+0f;
-  dim3 grid((unsigned)(n_qblocks * bh_count));
+  dim3 grid((unsigned)(bh_count * (n_qblocks / 2)));
   if (causal)
-    hipLaunchKernelGGL(fa_prefill_bf16_d128<true>, grid, dim3(256), 0, ctx->stream,
-                       (const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)v,
-                       (uint16_t *)o, (int)q_heads, (int)kv_heads, (int)q_len, (int)kv_len,
-                       c, n_qblocks, bh_count);
+    hipLaunchKernelGGL(fa_prefill_bf16_d128<true>, grid, dim3(THREADS), 0, ctx->stream,
+                       (const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)v, (uint16_t *)o,
+                       (int)q_heads, (int)kv_heads, (int)q_len, (int)kv_len, c, bh_count, n_qblocks);
   else
-    hipLaunchKernelGGL(fa_prefill_bf16_d128<false>, grid, dim3(256), 0, ctx->stream,
-                       (const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)v,
-                       (uint16_t *)o, (int)q_heads, (int)kv_heads, (int)q_len, (int)kv_len,
-                       c, n_qblocks, bh_count);
+    hipLaunchKernelGGL(fa_prefill_bf16_d128<false>, grid, dim3(THREADS), 0, ctx->stream,
+                       (const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)v, (uint16_t *)o,
+                       (int)q_heads, (int)kv_heads, (int)q_len, (int)kv_len, c, bh_count, n_qblocks);
   return launch_status("fa_prefill_bf16_d128");
 }

@@ -11,20 +11,23 @@
 // (:302-309).  Because every output keeps the exact k-order chain, results
 // are bit-identical to the formal lane, not merely close.
 //
-// Layout on the GPU: 64x64 output tile per 256-thread workgroup, 4x4
-// independent fma chains per thread (ILP across chains, never inside one),
-// operands widened to f32 once into LDS in 16-deep k slices.
+// Layout on the GPU: a (16 MT)x(16 MT) output tile per 256-thread workgroup,
+// MT x MT independent fma chains per thread (ILP across chains, never inside
+// one), operands widened to f32 once into LDS in 16-deep k slices.  MT = 4
+// for large outputs; MT = 1 when the 64x64 grid would leave CUs idle (a
+// chain is sequential in k, so parallelism can only come from outputs).
 #include "common.h"
 
 namespace wafer {
 namespace {
 
-constexpr int TM = 64, TN = 64, TK = 16;
+constexpr int TK = 16;
 
-template <uint32_t IN, uint32_t OUT>
+template <uint32_t IN, uint32_t OUT, int MT>
 __global__ __launch_bounds__(256) void gemm_formal_kernel(
     const void *__restrict__ lhs, const void *__restrict__ rhs, void *__restrict__ dst,
     const float *__restrict__ psum, int m, int k, int n, int lhs_t, int rhs_t) {
+  constexpr int TM = 16 * MT, TN = 16 * MT, LOADS = TM * TK / 256;
   __shared__ float As[TK][TM + 1];
   __shared__ float Bs[TK][TN + 1];
   const int b = blockIdx.z;
@@ -32,16 +35,16 @@ __global__ __launch_bounds__(256) void gemm_formal_kernel(
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
   const int64_t lb = (int64_t)b * m * k, rb = (int64_t)b * k * n, ob = (int64_t)b * m * n;
 
-  float acc[4][4];
+  float acc[MT][MT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+    for (int j = 0; j < MT; ++j) acc[i][j] = 0.0f;
 
   for (int k0 = 0; k0 < k; k0 += TK) {
-    // 64 x 16 slice of lhs and 16 x 64 slice of rhs, 4 elements per thread each
+    // TM x 16 slice of lhs and 16 x TN slice of rhs, LOADS elements per thread each
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < LOADS; ++r) {
       const int e = tid + 256 * r;
       const int kk = e & 15, mm = e >> 4;  // lhs: row mm, depth kk
       const int gm = m0 + mm, gk = k0 + kk;
@@ -49,7 +52,7 @@ __global__ __launch_bounds__(256) void gemm_formal_kernel(
       if (gm < m && gk < k)
         a = load_as_f32<IN>(lhs, lb + (lhs_t ? (int64_t)gk * m + gm : (int64_t)gm * k + gk));
       As[kk][mm] = a;
-      const int nn = e & 63, kb = e >> 6;  // rhs: depth kb, column nn
+      const int nn = e % TN, kb = e / TN;  // rhs: depth kb, column nn
       const int gn = n0 + nn, gk2 = k0 + kb;
       float bv = 0.0f;
       if (gn < n && gk2 < k)
@@ -59,23 +62,23 @@ __global__ __launch_bounds__(256) void gemm_formal_kernel(
     __syncthreads();
     const int kend = min(TK, k - k0);
     for (int kk = 0; kk < kend; ++kk) {
-      float av[4], bv[4];
+      float av[MT], bv[MT];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = As[kk][ty + 16 * i];
+      for (int i = 0; i < MT; ++i) av[i] = As[kk][ty + 16 * i];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = Bs[kk][tx + 16 * j];
+      for (int j = 0; j < MT; ++j) bv[j] = Bs[kk][tx + 16 * j];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < MT; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
+        for (int j = 0; j < MT; ++j) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
     }
     __syncthreads();
   }
 
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < MT; ++j) {
       const int gm = m0 + ty + 16 * i, gn = n0 + tx + 16 * j;
       if (gm >= m || gn >= n) continue;
       float v = acc[i][j];
@@ -86,24 +89,35 @@ __global__ __launch_bounds__(256) void gemm_formal_kernel(
     }
 }
 
-template <uint32_t IN>
+template <uint32_t IN, int MT>
 int launch_out(uint32_t out, dim3 grid, hipStream_t st, const void *lhs, const void *rhs,
                void *dst, const float *psum, int m, int k, int n, int lt, int rt) {
   switch (out) {
   case WAFER_FMT_F32:
-    hipLaunchKernelGGL((gemm_formal_kernel<IN, WAFER_FMT_F32>), grid, dim3(256), 0, st, lhs, rhs,
+    hipLaunchKernelGGL((gemm_formal_kernel<IN, WAFER_FMT_F32, MT>), grid, dim3(256), 0, st, lhs, rhs,
                        dst, psum, m, k, n, lt, rt);
     break;
   case WAFER_FMT_BF16:
-    hipLaunchKernelGGL((gemm_formal_kernel<IN, WAFER_FMT_BF16>), grid, dim3(256), 0, st, lhs, rhs,
+    hipLaunchKernelGGL((gemm_formal_kernel<IN, WAFER_FMT_BF16, MT>), grid, dim3(256), 0, st, lhs, rhs,
                        dst, psum, m, k, n, lt, rt);
     break;
   default:
-    hipLaunchKernelGGL((gemm_formal_kernel<IN, WAFER_FMT_F16>), grid, dim3(256), 0, st, lhs, rhs,
+    hipLaunchKernelGGL((gemm_formal_kernel<IN, WAFER_FMT_F16, MT>), grid, dim3(256), 0, st, lhs, rhs,
                        dst, psum, m, k, n, lt, rt);
     break;
   }
   return launch_status("gemm_formal_kernel");
+}
+
+template <uint32_t IN>
+int launch_in(uint32_t out, int cus, hipStream_t st, const void *lhs, const void *rhs, void *dst,
+              const float *psum, uint32_t m, uint32_t k, uint32_t n, uint32_t batch, int lt, int rt) {
+  const uint64_t big = (uint64_t)((n + 63) / 64) * ((m + 63) / 64) * batch;
+  if (big >= (uint64_t)cus)
+    return launch_out<IN, 4>(out, dim3((n + 63) / 64, (m + 63) / 64, batch), st, lhs, rhs, dst, psum,
+                             m, k, n, lt, rt);
+  return launch_out<IN, 1>(out, dim3((n + 15) / 16, (m + 15) / 16, batch), st, lhs, rhs, dst, psum, m,
+                           k, n, lt, rt);
 }
 
 }  // namespace
@@ -134,14 +148,14 @@ extern "C" int wafer_hip_gemm(wafer_hip_context *ctx, const void *lhs, const voi
   }
   if (!lhs || !rhs || !dst) return fail(WAFER_HIP_E_INVALID_FIELD, "gemm: null tensor");
   WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
-  dim3 grid((n + TN - 1) / TN, (m + TM - 1) / TM, batch);
   const int lt = (int)lhs_orientation, rt = (int)rhs_orientation;
+  const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
   switch (in_format) {
   case WAFER_FMT_F32:
-    return launch_out<WAFER_FMT_F32>(out_format, grid, ctx->stream, lhs, rhs, dst, ps, m, k, n, lt, rt);
+    return launch_in<WAFER_FMT_F32>(out_format, cus, ctx->stream, lhs, rhs, dst, ps, m, k, n, batch, lt, rt);
   case WAFER_FMT_BF16:
-    return launch_out<WAFER_FMT_BF16>(out_format, grid, ctx->stream, lhs, rhs, dst, ps, m, k, n, lt, rt);
+    return launch_in<WAFER_FMT_BF16>(out_format, cus, ctx->stream, lhs, rhs, dst, ps, m, k, n, batch, lt, rt);
   default:
-    return launch_out<WAFER_FMT_F16>(out_format, grid, ctx->stream, lhs, rhs, dst, ps, m, k, n, lt, rt);
+    return launch_in<WAFER_FMT_F16>(out_format, cus, ctx->stream, lhs, rhs, dst, ps, m, k, n, batch, lt, rt);
   }
 }
