@@ -41,6 +41,7 @@ I8_N = 4096
 I8_OPS = 2 * I8_N ** 3
 MLP_FLOPS = 2 * 128 * 512 * 2048 * 2
 SEED = 20260803
+COPY_BYTES = 1 << 30
 
 
 def cores() -> int:
@@ -201,12 +202,22 @@ def bench_mlp(torch, hip, B, steps, warmup, with_cpu=True):
     return res
 
 
+def bench_copy(torch, steps, warmup):
+    """A plain device copy of known size: the calibration kernel for the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE counters (reads and writes COPY_BYTES)."""
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(7)
+    dst = torch.empty_like(src)
+    ms = timed(torch, lambda: dst.copy_(src), steps, warmup)
+    return {"workload": f"device copy of {COPY_BYTES} bytes (counter calibration)", "metric": "GB/s",
+            "ms": ms, "value": 2 * COPY_BYTES / (ms * 1e-3) / 1e9, "unit": "GB/s"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="fa,fd,i8,mlp", help="comma list of fa, fd, i8, mlp")
+    ap.add_argument("--only", default="fa,fd,i8,mlp", help="comma list of fa, fd, i8, mlp, copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -233,6 +244,8 @@ def main() -> int:
         secondary.append(dict(name="gemm_i8", **bench_i8(torch, hip, args.steps, args.warmup, with_cpu)))
     if "mlp" in only:
         secondary.append(dict(name="mlp_fp32", **bench_mlp(torch, hip, B, args.steps, args.warmup, with_cpu)))
+    if "copy" in only:
+        secondary.append(dict(name="copy", **bench_copy(torch, args.steps, args.warmup)))
     hip.close()
 
     line = {
