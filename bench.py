@@ -9,8 +9,9 @@ config (bf16 Q,K,V [1,16,2048,128], causal) in TFLOP/s of
 algorithmic (causal, visible-pair) work; FD decode (config 2), the int8 GEMM
 (config 3) and the fp32 MLP block (config 0) are reported in `secondary`,
 each with its own roofline fraction and CPU baseline.  Timing: W untimed
-launches, then exactly K launches between two HIP events recorded on the
-stream the kernels run on (torch's current stream, which the backend binds).
+launches, then exactly K launches captured into one HIP graph and replayed
+between two HIP events on the stream the kernels run on (the backend binds
+torch's current stream at each call, the capture stream during capture).
 
 cpu_baseline: the CPU oracle (oracle/, a C restatement of the Reference
 backend's semantics, test infrastructure) timed on this host's cores over a
@@ -64,15 +65,30 @@ def traffic_for(kernel: str):
 
 
 def timed(torch, fn, steps: int, warmup: int) -> float:
-    """Average milliseconds per launch over exactly `steps` launches."""
+    """Average milliseconds per step over exactly `steps` steps.
+
+    The W warmup steps run eagerly (they also size the backend's workspace).
+    The K timed steps are captured once into a HIP graph and replayed between
+    two HIP events on the replay stream, so the figure is the GPU's time for
+    K back-to-back steps, free of the Python binding's per-call host cost
+    (a C++ caller of the C ABI does not pay it)."""
     for _ in range(warmup):
         fn()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for _ in range(steps):
+                fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph.replay()  # untimed: first replay uploads the graph
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
-    for _ in range(steps):
-        fn()
+    graph.replay()
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps

@@ -33,8 +33,8 @@
 //    skipped when alpha == 1 for the whole wave (x * 1 == x exactly);
 //  * K tiles sit row-major in LDS, V tiles transposed (d-major) with keys
 //    permuted inside every 16-key group so the 8 keys one lane needs for one
-//    MFMA are contiguous (one ds_read_b128); per key half double-buffered and
-//    staged global -> VGPR -> LDS one iteration ahead; both query blocks of a
+//    MFMA are contiguous (one ds_read_b128); per key half double-buffered in
+//    LDS and staged global -> VGPR two iterations ahead; both query blocks of a
 //    workgroup read the same tiles for their common key prefix;
 //  * consecutive workgroup ids walk (batch*head), so each head's workgroups
 //    land on one XCD (ids are dealt round-robin over the 8 XCDs) and share
@@ -46,6 +46,8 @@
 // f32 argument and far inside the attention tolerance.
 #include "common.h"
 
+#include <type_traits>
+
 namespace wafer {
 namespace {
 
@@ -56,10 +58,11 @@ constexpr int KPITCH = D + 8;     // LDS row pitch of K tiles (elements): 272 B
 constexpr int VPITCH = BK + 8;    // LDS row pitch of V^T tiles (elements): 144 B
 constexpr int THREADS = 512;
 
-__device__ inline int permute_key(int key) {
-  // swap bits 2 and 3 of the key index inside its 16-key group
-  return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
-}
+// V^T LDS column p of a 64-key block holds key swap23(p): bits 2 and 3 of
+// the key index swapped, so the 8 keys one lane feeds into one PV MFMA are
+// contiguous (the 32x32 accumulator layout puts rows 8(r/4) + 4g + r%4 in a
+// lane) and one ds_read_b128 fetches them.
+__device__ inline int swap23(int p) { return (p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1); }
 
 template <bool CAUSAL>
 __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
@@ -99,35 +102,38 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
 #pragma unroll
   for (int s = 0; s < 8; ++s)
     qreg[s] = *(const bf16x8 *)(Qp + (size_t)my_q * D + s * 16 + g * 8);
-  // Drain the Q loads here.  Without this, the waitcnt pass ties Q's
-  // registers to the in-loop prefetch loads and makes every iteration wait
-  // for the next K/V block to arrive before its first MFMA.
-  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+  // (the Q loads are drained in the prologue below, together with the first
+  // K/V block: without an explicit drain the waitcnt pass ties Q's registers
+  // to the in-loop prefetch loads and stalls every iteration on them)
 
-  // global -> VGPR staging: the 4 waves of a key half load that half's block
+  // global -> VGPR staging: the 4 waves of a key half load that half's
+  // block (K: 16 lanes per 256-byte key row; V: 4 consecutive keys per lane,
+  // so the V^T stores of 16 lanes fill one 128-byte LDS row segment without
+  // bank conflicts).  Two register slots keep the loads two iterations ahead
+  // of their use.
   const int ltid = (((wave & 1) | ((wave >> 2) << 1)) << 6) | lane;  // 0..255 within the half
   const int k_row = ltid >> 4, k_col = (ltid & 15) * 8;               // rows k_row + 16 i
   const int v_kg = ltid & 15, v_dc = ltid >> 4;                       // keys 4 v_kg + i, d 8 v_dc
-  const int v_pos = permute_key(4 * v_kg);
-  u32x4 kst[4], vst[4];
-  auto gload = [&](int kb) {
+  const int v_pos = swap23(4 * v_kg);
+  u32x4 kst[2][4], vst[2][4];
+  auto gload = [&](int kb, auto slot) __attribute__((always_inline)) {
     const uint16_t *kp = Kp + (size_t)(kb * BK) * D;
     const uint16_t *vp = Vp + (size_t)(kb * BK) * D;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      kst[i] = *(const u32x4 *)(kp + (size_t)(k_row + 16 * i) * D + k_col);
+      kst[slot][i] = *(const u32x4 *)(kp + (size_t)(k_row + 16 * i) * D + k_col);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      vst[i] = *(const u32x4 *)(vp + (size_t)(4 * v_kg + i) * D + 8 * v_dc);
+      vst[slot][i] = *(const u32x4 *)(vp + (size_t)(4 * v_kg + i) * D + 8 * v_dc);
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](int buf, auto slot) __attribute__((always_inline)) {
     uint16_t *sk = sK[half][buf];
     uint16_t *sv = sV[half][buf];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *(u32x4 *)&sk[(k_row + 16 * i) * KPITCH + k_col] = kst[i];
+    for (int i = 0; i < 4; ++i) *(u32x4 *)&sk[(k_row + 16 * i) * KPITCH + k_col] = kst[slot][i];
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const uint32_t a0 = vst[0][w], a1 = vst[1][w], a2 = vst[2][w], a3 = vst[3][w];
+      const uint32_t a0 = vst[slot][0][w], a1 = vst[slot][1][w], a2 = vst[slot][2][w], a3 = vst[slot][3][w];
       u32x2 lo, hi;
       lo[0] = __builtin_amdgcn_perm(a1, a0, 0x05040100u);
       lo[1] = __builtin_amdgcn_perm(a3, a2, 0x05040100u);
@@ -146,93 +152,107 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc_o[dt][r] = 0.0f;
 
-  const int niter = (nk_hi + 1) / 2;
-  if (half < nk_hi) {
-    gload(half);
-    sstore(0);
-  }
-  __syncthreads();
-
-  for (int i = 0; i < niter; ++i) {
-    const int buf = i & 1;
-    const int kb = 2 * i + half;
-    const int kbn = kb + 2;
-    const bool prefetch = (i + 1 < niter) && (kbn < nk_hi);
-    if (prefetch) gload(kbn);
-    const bool active = (kb < nk_mine) && (!CAUSAL || kb * BK <= q0 + 31);
-    if (active) {
-      const uint16_t *sk = sK[half][buf];
-      const uint16_t *sv = sV[half][buf];
-      f32x16 sacc[2];
+  // one 64-key block: S^T = K.Q^T, online-softmax update, O^T += V^T.P^T
+  auto compute = [&](int kb, const uint16_t *sk, const uint16_t *sv) __attribute__((always_inline)) {
+    f32x16 sacc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[t][r] = 0.0f;
+    // the two key tiles alternate so consecutive MFMAs are independent
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[t][r] = 0.0f;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const bf16x8 a = *(const bf16x8 *)&sk[(t * 32 + l32) * KPITCH + s * 16 + g * 8];
-          sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[s], sacc[t], 0, 0, 0);
-        }
+        const bf16x8 a = *(const bf16x8 *)&sk[(t * 32 + l32) * KPITCH + s * 16 + g * 8];
+        sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[s], sacc[t], 0, 0, 0);
       }
-      if (CAUSAL && kb * BK + BK - 1 > q0) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = kb * BK + t * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (key > my_q) sacc[t][r] = -__builtin_inff();
-          }
-      }
-      float mx = sacc[0][0];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[t][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_raw, mx);
-      const float mc = (m_new == -__builtin_inff()) ? 0.0f : m_new * c;
-      const float alpha = __builtin_amdgcn_exp2f(m_raw * c - mc);
-      float rs = 0.0f;
+    if (CAUSAL && kb * BK + BK - 1 > q0) {
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][r], c, -mc));
-          sacc[t][r] = p;
-          rs += p;
+          const int key = kb * BK + t * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (key > my_q) sacc[t][r] = -__builtin_inff();
         }
-      rs += __shfl_xor(rs, 32);
-      l_sum = l_sum * alpha + rs;
-      m_raw = m_new;
-      if (!__all(alpha == 1.0f)) {
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha;
-      }
-      // P^T operands: (t, hf) covers keys t*32 + hf*16 + [0,16); the lane's 8
-      // keys are accumulator rows hf*8 + [0,8) of tile t.
-      bf16x8 pb[2][2];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) pb[t][hf][e] = (__bf16)sacc[t][hf * 8 + e];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-          for (int dt = 0; dt < 4; ++dt) {
-            const bf16x8 va = *(const bf16x8 *)&sv[(dt * 32 + l32) * VPITCH + t * 32 + hf * 16 + g * 8];
-            acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[t][hf], acc_o[dt], 0, 0, 0);
-          }
     }
+    float mx = sacc[0][0];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[t][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_raw, mx);
+    const float mc = (m_new == -__builtin_inff()) ? 0.0f : m_new * c;
+    const float alpha = __builtin_amdgcn_exp2f(m_raw * c - mc);
+    float rs = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][r], c, -mc));
+        sacc[t][r] = p;
+        rs += p;
+      }
+    rs += __shfl_xor(rs, 32);
+    l_sum = l_sum * alpha + rs;
+    m_raw = m_new;
+    if (!__all(alpha == 1.0f)) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha;
+    }
+    // P^T operands: (t, hf) covers S^T rows t*32 + hf*16 + [0,16); the
+    // lane's 8 values are accumulator rows hf*8 + [0,8) of tile t.
+    bf16x8 pb[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pb[t][hf][e] = (__bf16)sacc[t][hf * 8 + e];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const bf16x8 va = *(const bf16x8 *)&sv[(dt * 32 + l32) * VPITCH + t * 32 + hf * 16 + g * 8];
+          acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[t][hf], acc_o[dt], 0, 0, 0);
+        }
+  };
+
+  // Pipeline (per key half; iteration i works on block 2 i + half):
+  //   LDS buffer i%2 holds iteration i's block; register slot (i+1)%2 holds
+  //   iteration i+1's block, loaded one iteration earlier; iteration i loads
+  //   iteration i+2's block into slot i%2, computes, stores slot (i+1)%2 into
+  //   LDS buffer (i+1)%2, and meets the other waves at one barrier.  Loads
+  //   and stores are unconditional (block index clamped to the last block)
+  //   so the waitcnt pass counts them exactly and waits only for the older
+  //   slot.
+  const int niter = (nk_hi + 1) / 2;
+  const int last = nk_hi - 1;
+  gload(min(half, last), std::integral_constant<int, 0>{});
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): Q and the first block
+  sstore(0, std::integral_constant<int, 0>{});
+  gload(min(half + 2, last), std::integral_constant<int, 1>{});
+  __syncthreads();
+
+  auto step = [&](int i, auto slot) __attribute__((always_inline)) {
+    constexpr int P = decltype(slot)::value;  // == i % 2
+    const int kb = 2 * i + half;
+    gload(min(kb + 4, last), std::integral_constant<int, P>{});
+    const bool active = (kb < nk_mine) && (!CAUSAL || kb * BK <= q0 + 31);
+    if (active) compute(kb, sK[half][P], sV[half][P]);
     if (i + 1 < niter) {
-      if (prefetch) sstore(buf ^ 1);
+      sstore(P ^ 1, std::integral_constant<int, P ^ 1>{});
       __syncthreads();
     }
+  };
+  for (int i = 0; i < niter; i += 2) {
+    step(i, std::integral_constant<int, 0>{});
+    if (i + 1 < niter) step(i + 1, std::integral_constant<int, 1>{});
   }
 
   // ---- merge the odd-block half into the even-block half through LDS ----
