@@ -1,13 +1,14 @@
 #!/usr/bin/env python3
 """Benchmark of the gfx950 numeric backend on BASELINE.json's headline metric.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fa,fd,i8,mlp]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fa,fd,i8,mlp,llama]
 
 One step = one launch of the hot path over one batch of synthetic, seeded
 input already resident in HBM.  The headline (`value`) is the FA prefill
 config (bf16 Q,K,V [1,16,2048,128], causal) in TFLOP/s of
 algorithmic (causal, visible-pair) work; FD decode (config 2), the int8 GEMM
-(config 3) and the fp32 MLP block (config 0) are reported in `secondary`,
+(config 3), the fp32 MLP block (config 0) and the decoder layer (config 4)
+are reported in `secondary`,
 each with its own roofline fraction and CPU baseline.  Timing: W untimed
 launches, then exactly K launches captured into one HIP graph and replayed
 between two HIP events on the stream the kernels run on (the backend binds
@@ -26,6 +27,8 @@ import os
 import pathlib
 import sys
 import time
+
+import numpy as np
 
 ROOT = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
@@ -218,6 +221,45 @@ def bench_mlp(torch, hip, B, steps, warmup, with_cpu=True):
     return res
 
 
+def bench_llama(torch, hip, steps, warmup, with_cpu=True):
+    """one Llama-style decoder layer forward, [1,1024,4096]
+    bf16, GQA 32/8, FFN 14336, through vibe_compiler_amd.decoder_layer."""
+    from vibe_compiler_amd import decoder_layer as DL
+
+    gen = torch.Generator(device="cuda").manual_seed(SEED)
+    W = DL.random_weights(torch, gen)
+    x = torch.randn((1024, 4096), device="cuda", generator=gen).to(torch.bfloat16)
+    y = torch.empty_like(x)
+    layer = DL.DecoderLayer(hip, W, 1024)
+    ms = timed(torch, lambda: layer.forward(x, y), steps, warmup)
+    fl = DL.flops()
+    tf = fl / (ms * 1e-3) / 1e12
+    res = {
+        "workload": "Llama-style decoder layer x[1,1024,4096] bf16, GQA 32/8 (head_dim 128), FFN 14336, "
+                    "RMSNorm eps 1e-5, RoPE theta 1e4, causal; weights ~N(0,0.02) bf16",
+        "metric": "TFLOP/s", "ms": ms, "value": tf, "unit": "TFLOP/s",
+        "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK["bf16"], "unit": "TFLOP/s",
+                     "frac": tf / PEAK["bf16"], "traffic": None},
+    }
+    if with_cpu:
+        from oracle import oracle as orc
+        rows = 16
+        h = x[:rows].contiguous().cpu().view(torch.int16).numpy().view("uint16")
+        mats = [W[n].cpu().view(torch.int16).numpy().view("uint16") for n in ("wqkv", "wo", "wgate", "wup")]
+        wd = W["wdown"].cpu().view(torch.int16).numpy().view("uint16")
+        act = np.zeros((rows, 14336), dtype=np.uint16)
+        t0 = time.perf_counter()
+        for w in mats:
+            orc.gemm_formal(3, 3, h, w, rows, 4096, w.shape[0], rhs_t=True, nthreads=cores())
+        orc.gemm_formal(3, 3, act, wd, rows, 14336, 4096, rhs_t=True, nthreads=cores())
+        dt = time.perf_counter() - t0
+        sample = 2 * rows * 218_103_808
+        res["cpu_baseline"] = {"value": sample / dt / 1e12, "unit": "TFLOP/s", "cores": cores(), "kind": "port",
+                               "sample": f"the seven projection GEMMs (97% of the layer's FLOPs) for {rows} of "
+                                         f"1024 tokens on the formal-order lane, {dt:.2f} s wall"}
+    return res
+
+
 def bench_copy(torch, steps, warmup):
     """A plain device copy of known size: the calibration kernel for the
     rocprofv3 FETCH_SIZE / WRITE_SIZE counters (reads and writes COPY_BYTES)."""
@@ -233,7 +275,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="fa,fd,i8,mlp", help="comma list of fa, fd, i8, mlp, copy")
+    ap.add_argument("--only", default="fa,fd,i8,mlp,llama", help="comma list of fa, fd, i8, mlp, llama, copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -260,6 +302,8 @@ def main() -> int:
         secondary.append(dict(name="gemm_i8", **bench_i8(torch, hip, args.steps, args.warmup, with_cpu)))
     if "mlp" in only:
         secondary.append(dict(name="mlp_fp32", **bench_mlp(torch, hip, B, args.steps, args.warmup, with_cpu)))
+    if "llama" in only:
+        secondary.append(dict(name="llama_layer", **bench_llama(torch, hip, args.steps, args.warmup, with_cpu)))
     if "copy" in only:
         secondary.append(dict(name="copy", **bench_copy(torch, args.steps, args.warmup)))
     hip.close()

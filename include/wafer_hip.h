@@ -214,7 +214,7 @@ int wafer_hip_silu_mul(wafer_hip_context *ctx, uint32_t format,
 int wafer_hip_gelu_tanh(wafer_hip_context *ctx, uint32_t format, const void *x,
                         void *y, uint64_t count);
 /* Rotate-half RoPE over x [tokens, heads, head_dim] with positions [tokens]
- * (int32, device) and inv_freq[i] = 1/theta^(2i/head_dim). */
+ * (int32, device) and inv_freq[i] = 1/theta^(2i/head_dim).  y may alias x. */
 int wafer_hip_rope(wafer_hip_context *ctx, uint32_t format, const void *x,
                    void *y, uint64_t tokens, uint64_t heads,
                    uint64_t head_dim, const int32_t *positions, float theta);
@@ -222,6 +222,20 @@ int wafer_hip_rope(wafer_hip_context *ctx, uint32_t format, const void *x,
 int wafer_hip_bias_add(wafer_hip_context *ctx, uint32_t format, const void *x,
                        const float *bias, void *y, uint64_t rows,
                        uint64_t cols);
+
+/* ---- layout: token-major <-> head-major ---------------------------------------
+ * The movement step a lowered decoder layer performs between its fused QKV
+ * projection and the attention regions, and back before the output
+ * projection (strided head slices, TargetModelStridedMemory.cpp:124-140 for
+ * the reference's strided-movement addressing).  Bit-exact copy.
+ * direction 0: src token-major, element (t, h, d) at src[t*token_stride +
+ * h*head_dim + d] -> dst head-major [heads, tokens, head_dim];
+ * direction 1: src head-major -> dst token-major with row stride token_stride.
+ * head_dim and token_stride multiples of 16 bytes, tensors 16-byte aligned. */
+int wafer_hip_head_permute(wafer_hip_context *ctx, uint32_t format,
+                           const void *src, void *dst, uint64_t tokens,
+                           uint64_t heads, uint64_t head_dim,
+                           uint64_t token_stride, uint32_t direction);
 
 #ifdef __cplusplus
 }

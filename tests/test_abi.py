@@ -61,3 +61,11 @@ def test_physical_bytes_matches_oracle(oracle, fmt, layout, shape):
     from vibe_compiler_amd import backend
 
     assert backend.physical_bytes(fmt, layout, shape) == oracle.geometry(fmt, layout, shape)["physical_bytes"]
+
+
+def test_decoder_layer_flop_count():
+    """The composite's algorithmic FLOPs at BASELINE config 4 (projections
+    2*T*218,103,808 plus causal attention 4*Hq*D*T(T+1)/2)."""
+    from vibe_compiler_amd import decoder_layer as DL
+
+    assert DL.flops() == 2 * 1024 * 218_103_808 + 8_598_323_200 == 455_274_921_984

@@ -43,7 +43,7 @@ EXPORTS = (
     "wafer_hip_convert", "wafer_hip_reduce", "wafer_hip_physical_bytes", "wafer_hip_pack",
     "wafer_hip_unpack", "wafer_hip_attention_prefill", "wafer_hip_attention_decode",
     "wafer_hip_rmsnorm", "wafer_hip_softmax", "wafer_hip_silu_mul", "wafer_hip_gelu_tanh",
-    "wafer_hip_rope", "wafer_hip_bias_add",
+    "wafer_hip_rope", "wafer_hip_bias_add", "wafer_hip_head_permute",
 )
 
 
@@ -97,6 +97,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wafer_hip_gelu_tanh.argtypes = [vp, u32, vp, vp, u64]
     L.wafer_hip_rope.argtypes = [vp, u32, vp, vp, u64, u64, u64, vp, f32]
     L.wafer_hip_bias_add.argtypes = [vp, u32, vp, vp, vp, u64, u64]
+    L.wafer_hip_head_permute.argtypes = [vp, u32, vp, vp, u64, u64, u64, u64, u32]
 
 
 def _check(status: int) -> None:
@@ -233,6 +234,25 @@ class Context:
     def rope(self, x, y, positions, theta, fmt=BF16):
         T, H, D = x.shape
         _check(self._L.wafer_hip_rope(self._bind(), fmt, _p(x), _p(y), T, H, D, _p(positions), float(theta)))
+
+    def head_permute(self, src, dst, tokens, heads, head_dim, token_stride, direction, fmt=BF16,
+                     src_offset=0, dst_offset=0):
+        """direction 0: token-major rows (stride token_stride) -> [heads, tokens, head_dim];
+        direction 1: the reverse.  `src_offset`/`dst_offset` (elements) address a
+        column slice of a contiguous token-major tensor, e.g. K inside a fused QKV."""
+        es = 4 if fmt == F32 else 2
+        tok_extent = (tokens - 1) * token_stride + heads * head_dim if tokens and heads else 0
+        head_extent = heads * tokens * head_dim
+        tok, hm = (src, dst) if direction == 0 else (dst, src)
+        tok_off, hm_off = (src_offset, dst_offset) if direction == 0 else (dst_offset, src_offset)
+        if min(tok_off, hm_off) < 0 or tok_off + tok_extent > tok.numel() or hm_off + head_extent > hm.numel():
+            raise ValueError("head_permute: the addressed region exceeds a tensor")
+        if src.element_size() != es or dst.element_size() != es:
+            raise ValueError("head_permute: tensor element size does not match the format")
+        sp = ctypes.c_void_p(_p(src).value + src_offset * es)
+        dp = ctypes.c_void_p(_p(dst).value + dst_offset * es)
+        _check(self._L.wafer_hip_head_permute(self._bind(), fmt, sp, dp, tokens, heads, head_dim,
+                                              token_stride, direction))
 
     def bias_add(self, x, bias, y, fmt=F32):
         cols = x.shape[-1]

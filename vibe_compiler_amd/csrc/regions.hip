@@ -111,25 +111,28 @@ __global__ __launch_bounds__(256) void gelu_tanh_kernel(const void *__restrict__
 
 // Rotate-half RoPE: inv_freq[i] = 1/theta^(2i/D), angle = pos*inv_freq[d mod D/2],
 // y = x*cos(angle) + rotate_half(x)*sin(angle), rotate_half(x) = [-x2, x1].
+// One thread per rotation pair (d, d + head_dim/2) of a row: both outputs
+// come from the same two inputs, so y may alias x.
 template <uint32_t F>
-__global__ __launch_bounds__(256) void rope_kernel(const void *__restrict__ x, void *__restrict__ y,
+__global__ __launch_bounds__(256) void rope_kernel(const void *x, void *y,
                                                    int64_t tokens, int64_t heads, int64_t head_dim,
                                                    const int32_t *__restrict__ positions,
                                                    float theta) {
-  const int64_t count = tokens * heads * head_dim;
   const int64_t half = head_dim / 2;
+  const int64_t pairs = tokens * heads * half;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < count; e += stride) {
-    const int64_t d = e % head_dim;
-    const int64_t row = e - d;
-    const int64_t t = e / (heads * head_dim);
-    const int64_t i = d % half;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < pairs; e += stride) {
+    const int64_t i = e % half;
+    const int64_t rowi = e / half;  // (token, head)
+    const int64_t t = rowi / heads;
+    const int64_t lo = rowi * head_dim + i, hi = lo + half;
     const float inv_freq = 1.0f / powf(theta, (float)(2 * i) / (float)head_dim);
     const float angle = (float)positions[t] * inv_freq;
     const float c = cosf(angle), s = sinf(angle);
-    const float xv = load_as_f32<F>(x, e);
-    const float rot = d < half ? -load_as_f32<F>(x, row + d + half) : load_as_f32<F>(x, row + d - half);
-    store_from_f32<F>(y, e, xv * c + rot * s);
+    const float xl = load_as_f32<F>(x, lo), xh = load_as_f32<F>(x, hi);
+    // y[d] = x[d]*cos + rot[d]*sin with rot = (-x[d+half], x[d-half])
+    store_from_f32<F>(y, lo, xl * c + (-xh) * s);
+    store_from_f32<F>(y, hi, xh * c + xl * s);
   }
 }
 
@@ -217,7 +220,7 @@ extern "C" int wafer_hip_rope(wafer_hip_context *ctx, uint32_t format, const voi
   const uint64_t count = tokens * heads * head_dim;
   if (count == 0) return WAFER_HIP_OK;
   if (!x || !y || !positions) return fail(WAFER_HIP_E_INVALID_FIELD, "rope: null tensor");
-  DISPATCH_F(format, rope_kernel, dim3(grid_for(count)), dim3(256), x, y, (int64_t)tokens,
+  DISPATCH_F(format, rope_kernel, dim3(grid_for(count / 2)), dim3(256), x, y, (int64_t)tokens,
              (int64_t)heads, (int64_t)head_dim, positions, theta);
   return launch_status("rope_kernel");
 }

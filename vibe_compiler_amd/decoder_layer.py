@@ -1,0 +1,138 @@
+"""Decoder layer (Llama-style) composed from the gfx950 backend's regions.
+
+This is the order of regions a lowered Llama decoder block runs through the
+backend, each one a C-ABI call of ``libwafer_hip.so`` on the caller's stream:
+
+    h    = RMSNorm(x) * w_in                          wafer_hip_rmsnorm
+    qkv  = h . Wqkv^T        [T, (Hq + 2 Hkv) D]      wafer_hip_gemm_mfma (bf16 MFMA)
+    q,k,v -> head-major      [H, T, D]                wafer_hip_head_permute
+    q,k  = RoPE(q), RoPE(k)  rotate-half, theta       wafer_hip_rope
+    o    = causal GQA attention(q, k, v)              wafer_hip_attention_prefill (FA)
+    a    = o -> token-major  [T, Hq D]                wafer_hip_head_permute
+    x1   = x + a . Wo^T                               wafer_hip_gemm_mfma, wafer_hip_elementwise(Add)
+    h2   = RMSNorm(x1) * w_post
+    y    = x1 + (silu(h2 . Wg^T) * (h2 . Wu^T)) . Wd^T
+                                                      wafer_hip_gemm_mfma, wafer_hip_silu_mul, Add
+
+The math is the reference's CPU reference of the decoder block
+(test/Tools/Inputs/wafer_pytorch_xla_capture.py:1183-1260: rms_norm with
+reciprocal-sqrt of the mean square plus eps, q/k/v/o/gate/up/down linear
+layers as x . W^T, rotate-half RoPE with inv_freq = 1/theta^(2i/D), causal
+softmax attention with scale 1/sqrt(D), SwiGLU MLP) and of the board case
+built on the Hugging Face decoder layer
+(test/Board/PyTorch/wafer_pytorch_board_cases.py:817-866).  Storage between
+regions is bf16, every region computes in f32; results match an f32 torch
+evaluation of the same layer within the attention tolerance, not bit for bit.
+
+Weights are kept in the nn.Linear orientation [out, in] (rhs Transpose for
+the GEMM), so no re-layout pass runs per call.  All buffers are allocated
+once in the constructor; ``forward`` launches only.
+"""
+from __future__ import annotations
+
+import math
+
+from . import backend as B
+
+ADD = B.EW["Add"]  # TargetElementwiseOperation::Add
+
+
+class DecoderLayer:
+    """One decoder layer on one GPU, bf16 weights resident in HBM."""
+
+    def __init__(self, hip: "B.Context", weights: dict, tokens: int, hidden: int = 4096,
+                 q_heads: int = 32, kv_heads: int = 8, head_dim: int = 128, ffn: int = 14336,
+                 eps: float = 1e-5, theta: float = 1e4):
+        import torch
+
+        self.hip, self.T, self.hidden = hip, tokens, hidden
+        self.Hq, self.Hkv, self.D, self.ffn = q_heads, kv_heads, head_dim, ffn
+        self.eps, self.theta = eps, theta
+        if q_heads * head_dim != hidden:
+            raise ValueError("q_heads * head_dim must equal hidden")
+        dev = torch.device("cuda", hip.device)
+        bf = torch.bfloat16
+
+        def w(name, shape):
+            t = weights[name]
+            if tuple(t.shape) != shape or t.dtype != bf or t.device != dev:
+                raise ValueError(f"weight {name}: expected bf16 {shape} on {dev}, got {t.dtype} {tuple(t.shape)}")
+            return t.contiguous()
+
+        qkv_n = (q_heads + 2 * kv_heads) * head_dim
+        self.w_in = w("input_norm", (hidden,))
+        self.w_post = w("post_norm", (hidden,))
+        self.wqkv = w("wqkv", (qkv_n, hidden))
+        self.wo = w("wo", (hidden, hidden))
+        self.wg = w("wgate", (ffn, hidden))
+        self.wu = w("wup", (ffn, hidden))
+        self.wd = w("wdown", (hidden, ffn))
+
+        T = tokens
+        e = lambda *s: torch.empty(s, dtype=bf, device=dev)
+        self.h = e(T, hidden)
+        self.qkv = e(T, qkv_n)
+        self.q = e(q_heads, T, head_dim)
+        self.k = e(kv_heads, T, head_dim)
+        self.v = e(kv_heads, T, head_dim)
+        self.o = e(q_heads, T, head_dim)
+        self.attn = e(T, hidden)
+        self.proj = e(T, hidden)
+        self.x1 = e(T, hidden)
+        self.gate = e(T, ffn)
+        self.up = e(T, ffn)
+        self.act = e(T, ffn)
+        self.down = e(T, hidden)
+        # RoPE runs on the head-major tensors as [heads*T, 1, D] rows, so the
+        # position of row (h, t) is t
+        pos = torch.arange(T, dtype=torch.int32, device=dev)
+        self.pos_q = pos.repeat(q_heads)
+        self.pos_k = pos.repeat(kv_heads)
+
+    def forward(self, x, y):
+        """x, y: bf16 [tokens, hidden] device tensors (y may not alias x)."""
+        hip, T, Hd, D = self.hip, self.T, self.hidden, self.D
+        Hq, Hkv, F = self.Hq, self.Hkv, self.ffn
+        qkv_n = self.qkv.shape[1]
+        hip.rmsnorm(x, self.w_in, self.h, self.eps)
+        hip.gemm_mfma(self.h, self.wqkv, self.qkv, T, Hd, qkv_n, out_fmt=B.BF16, rhs_t=True)
+        hip.head_permute(self.qkv, self.q, T, Hq, D, qkv_n, 0)
+        hip.head_permute(self.qkv, self.k, T, Hkv, D, qkv_n, 0, src_offset=Hq * D)
+        hip.head_permute(self.qkv, self.v, T, Hkv, D, qkv_n, 0, src_offset=(Hq + Hkv) * D)
+        hip.rope(self.q.view(Hq * T, 1, D), self.q.view(Hq * T, 1, D), self.pos_q, self.theta)
+        hip.rope(self.k.view(Hkv * T, 1, D), self.k.view(Hkv * T, 1, D), self.pos_k, self.theta)
+        hip.attention_prefill(self.q.view(1, Hq, T, D), self.k.view(1, Hkv, T, D), self.v.view(1, Hkv, T, D),
+                              self.o.view(1, Hq, T, D), 1.0 / math.sqrt(D), causal=True)
+        hip.head_permute(self.o, self.attn, T, Hq, D, Hd, 1)
+        hip.gemm_mfma(self.attn, self.wo, self.proj, T, Hd, Hd, out_fmt=B.BF16, rhs_t=True)
+        hip.elementwise(ADD, B.BF16, x, self.x1, self.proj)
+        hip.rmsnorm(self.x1, self.w_post, self.h, self.eps)
+        hip.gemm_mfma(self.h, self.wg, self.gate, T, Hd, F, out_fmt=B.BF16, rhs_t=True)
+        hip.gemm_mfma(self.h, self.wu, self.up, T, Hd, F, out_fmt=B.BF16, rhs_t=True)
+        hip.silu_mul(self.gate, self.up, self.act)
+        hip.gemm_mfma(self.act, self.wd, self.down, T, F, Hd, out_fmt=B.BF16, rhs_t=True)
+        hip.elementwise(ADD, B.BF16, self.x1, y, self.down)
+        return y
+
+
+def flops(tokens: int = 1024, hidden: int = 4096, q_heads: int = 32, kv_heads: int = 8, head_dim: int = 128,
+          ffn: int = 14336) -> int:
+    """Algorithmic FLOPs of one layer: 2*T*(weights) for the projections plus
+    4*Hq*D*(causal visible pairs) for attention."""
+    weights = hidden * (q_heads + 2 * kv_heads) * head_dim + hidden * hidden + 3 * hidden * ffn
+    return 2 * tokens * weights + 4 * q_heads * head_dim * (tokens * (tokens + 1) // 2)
+
+
+def random_weights(torch, gen, hidden=4096, q_heads=32, kv_heads=8, head_dim=128, ffn=14336, std=0.02):
+    """bf16 ~N(0, std) weights in the layout DecoderLayer takes; norm weights 1."""
+    dev = gen.device
+    r = lambda *s: (torch.randn(s, device=dev, generator=gen) * std).to(torch.bfloat16)
+    return {
+        "input_norm": torch.ones(hidden, dtype=torch.bfloat16, device=dev),
+        "post_norm": torch.ones(hidden, dtype=torch.bfloat16, device=dev),
+        "wqkv": r((q_heads + 2 * kv_heads) * head_dim, hidden),
+        "wo": r(hidden, hidden),
+        "wgate": r(ffn, hidden),
+        "wup": r(ffn, hidden),
+        "wdown": r(hidden, ffn),
+    }
