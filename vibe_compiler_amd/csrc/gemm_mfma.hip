@@ -6,14 +6,17 @@
 // LDS read:
 //   bf16/f16: v_mfma_f32_32x32x16_{bf16,f16}  (16 elements = 32 B of K/step)
 //   int8:     v_mfma_i32_32x32x32_i8          (32 elements = 32 B of K/step)
-// A workgroup of 4 waves computes a BMxBN tile (256x256 or 128x128; waves
-// 2x2), staging 64-byte K slices of A and Bt through double-buffered LDS.
-// LDS rows are 64 B with the 16-byte chunk index XOR-swizzled by
-// ((row >> 1) & 3) so the 8 lanes that share a bank window read 8 different
-// chunks (conflict-free ds_read_b128).  A normal (K-major) rhs is first
-// re-laid out to Bt by a tiled transpose kernel into context scratch.
-// Workgroup ids are mapped so that the 32 tiles served by one XCD form a
-// 4x8 block of the output, bounding that XCD's L2 working set.
+// A workgroup of 8 waves (2 x 4) computes a BMxBN tile (256x256, or 128x128
+// when the 256 grid would leave CUs idle); each wave owns (BM/2) x (BN/4),
+// two waves per SIMD.  64-byte K slices of A and Bt go global -> LDS directly
+// (global_load_lds_dwordx4, no VGPR round trip) into a ring of 4 stage
+// buffers, issued 3 stages ahead; one barrier per stage.  LDS rows are 64 B
+// with the 16-byte chunk index XOR-swizzled by ((row >> 2) & 3), so any 16
+// consecutive rows read at one chunk hit 16 distinct bank groups
+// (conflict-free ds_read_b128; SQ_LDS_BANK_CONFLICT reads 0).  A normal
+// (K-major) rhs is first re-laid out to Bt by a transpose kernel into
+// context scratch.  Workgroup ids are mapped so that the 32 tiles served by
+// one XCD form a 4x8 block of the output, bounding that XCD's L2 working set.
 //
 // int8 semantics (no reference implementation exists; the closed form on the
 // reference's conversion routes): acc = sum_k int32(a)*int32(b) exactly
@@ -29,7 +32,7 @@ namespace {
 enum { KIND_BF16 = 0, KIND_F16 = 1, KIND_I8 = 2 };
 constexpr int BKB = 64;  // bytes of K per LDS stage (2 MFMA steps)
 
-__device__ inline int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 3); }
+__device__ inline int swz(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
 
 template <int KIND> struct Acc;
 template <> struct Acc<KIND_BF16> { typedef f32x16 T; };
@@ -68,11 +71,12 @@ struct GemmArgs {
 };
 
 template <int KIND, int BM, int BN, int OUT>
-__global__ __launch_bounds__(256) void gemm_nt_kernel(GemmArgs args) {
-  constexpr int WTM = BM / 64, WTN = BN / 64;  // 32x32 MFMA tiles per wave (waves 2x2)
-  constexpr int A_LOADS = BM * 4 / 256, B_LOADS = BN * 4 / 256;
-  __shared__ __align__(16) u32x4 sA[2][BM * 4];
-  __shared__ __align__(16) u32x4 sB[2][BN * 4];
+__global__ __launch_bounds__(512) void gemm_nt_kernel(GemmArgs args) {
+  // 8 waves as 2 (M) x 4 (N); each wave owns a (BM/2) x (BN/4) sub-tile
+  constexpr int NT = 512, WM = 2, WN = 4;
+  constexpr int WTM = BM / WM / 32, WTN = BN / WN / 32;  // 32x32 MFMA tiles per wave
+  __shared__ __align__(16) u32x4 sA[4][BM * 4];
+  __shared__ __align__(16) u32x4 sB[4][BN * 4];
 
   // XCD-aware tile order: ids are dealt round-robin over 8 XCDs; the ids one
   // XCD receives cover a 4 x 8 block of output tiles when the grid allows it.
@@ -99,7 +103,7 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(GemmArgs args) {
   const int m0 = tm * BM, n0 = tn * BN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int l32 = lane & 31, g = lane >> 5;
 
   typename Acc<KIND>::T acc[WTM][WTN];
@@ -110,50 +114,58 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(GemmArgs args) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-  const int ld_row = tid >> 2, ld_chunk = tid & 3;  // rows ld_row + 64 i
-  u32x4 ra[A_LOADS], rb[B_LOADS];
+  // Direct-to-LDS staging: NS stage buffers in a ring, loads issued NS-1
+  // stages ahead with global_load_lds_dwordx4 (no VGPR round trip).  One
+  // instruction fills 1 KiB = 16 rows x 4 chunks of a stage buffer: lane l
+  // writes LDS chunk position (l & 3) of row (l >> 2), so it loads the global
+  // chunk that the XOR swizzle maps there.
+  constexpr int NS = 4;
+  constexpr int A_INSTR = BM / 16, B_INSTR = BN / 16;      // 1 KiB DMA per instruction
+  constexpr int PER_WAVE = (A_INSTR + B_INSTR) / (NT / 64);
+  static_assert((A_INSTR + B_INSTR) % (NT / 64) == 0, "DMA instructions must split evenly over the waves");
+  const uint32_t kb32 = (uint32_t)args.kbytes;
+  const int nkt = args.kbytes / BKB;
   const size_t kb = (size_t)args.kbytes;
-  auto gload = [&](int kt) {
-    const size_t koff = (size_t)kt * BKB + ld_chunk * 16;
+  const uint8_t *abase = args.a + (size_t)m0 * kb;
+  const uint8_t *bbase = args.bt + (size_t)n0 * kb;
+  const int dma_row = lane >> 2, dma_pos = lane & 3;
+  auto issue = [&](int kt) __attribute__((always_inline)) {
+    const int st = kt % NS;
+    const uint32_t koff = (uint32_t)min(kt, nkt - 1) * BKB;
 #pragma unroll
-    for (int i = 0; i < A_LOADS; ++i)
-      ra[i] = *(const u32x4 *)(args.a + (size_t)(m0 + ld_row + 64 * i) * kb + koff);
-#pragma unroll
-    for (int i = 0; i < B_LOADS; ++i)
-      rb[i] = *(const u32x4 *)(args.bt + (size_t)(n0 + ld_row + 64 * i) * kb + koff);
-  };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) {
-      const int row = ld_row + 64 * i;
-      sA[buf][row * 4 + swz(row, ld_chunk)] = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < B_LOADS; ++i) {
-      const int row = ld_row + 64 * i;
-      sB[buf][row * 4 + swz(row, ld_chunk)] = rb[i];
+    for (int q = 0; q < PER_WAVE; ++q) {
+      const int ins = wave * PER_WAVE + q;  // 0 .. A_INSTR + B_INSTR - 1
+      const bool is_a = ins < A_INSTR;
+      const int row = (is_a ? ins : ins - A_INSTR) * 16 + dma_row;
+      const int chunk = swz(row, dma_pos);  // swz is an involution on the chunk index
+      const uint8_t *src = (is_a ? abase : bbase) + (row * kb32 + koff + chunk * 16);
+      u32x4 *dst = is_a ? &sA[st][(ins * 16) * 4] : &sB[st][((ins - A_INSTR) * 16) * 4];
+      __builtin_amdgcn_global_load_lds((const void *)src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
     }
   };
 
-  const int nkt = args.kbytes / BKB;
-  gload(0);
-  sstore(0);
-  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) issue(s);
   for (int kt = 0; kt < nkt; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nkt) gload(kt + 1);
+    const int buf = kt % NS;
+    // own loads of stage kt done (the NS-2 later stages may stay in flight),
+    // then the barrier makes every wave's stage-kt data visible and frees
+    // the buffer of stage kt-1 for the next issue; the asm keeps the compiler
+    // from moving LDS accesses across it
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE) : "memory");
+    issue(kt + NS - 1);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int chunk = ks * 2 + g;
       u32x4 fa[WTM], fb[WTN];
 #pragma unroll
       for (int i = 0; i < WTM; ++i) {
-        const int row = wm * (BM / 2) + i * 32 + l32;
+        const int row = wm * (BM / WM) + i * 32 + l32;
         fa[i] = sA[buf][row * 4 + swz(row, chunk)];
       }
 #pragma unroll
       for (int j = 0; j < WTN; ++j) {
-        const int row = wn * (BN / 2) + j * 32 + l32;
+        const int row = wn * (BN / WN) + j * 32 + l32;
         fb[j] = sB[buf][row * 4 + swz(row, chunk)];
       }
 #pragma unroll
@@ -161,23 +173,21 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(GemmArgs args) {
 #pragma unroll
         for (int j = 0; j < WTN; ++j) acc[i][j] = mfma<KIND>(fa[i], fb[j], acc[i][j]);
     }
-    if (kt + 1 < nkt) {
-      sstore(buf ^ 1);
-      __syncthreads();
-    }
   }
+  // the clamped tail loads are still in flight: drain before the LDS goes away
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // epilogue: lane holds column l32 and rows 8*(r/4) + 4*g + r%4 of each tile
 #pragma unroll
   for (int i = 0; i < WTM; ++i)
 #pragma unroll
     for (int j = 0; j < WTN; ++j) {
-      const int col = n0 + wn * (BN / 2) + j * 32 + l32;
+      const int col = n0 + wn * (BN / WN) + j * 32 + l32;
       float sc = 0.0f;
       if (OUT == OUT_I8_DEQUANT) sc = args.scale[col];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        const int row = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
         const size_t o = (size_t)row * args.n + col;
         if (OUT == OUT_F32) {
           ((float *)args.y)[o] = (float)acc[i][j][r];
@@ -195,21 +205,78 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(GemmArgs args) {
     }
 }
 
-// [rows, cols] -> [cols, rows] for 1- or 2-byte elements, 64x64 tiles.
-template <typename T>
-__global__ __launch_bounds__(256) void transpose_kernel(const T *__restrict__ src, T *__restrict__ dst,
-                                                        int rows, int cols) {
-  __shared__ T tile[64][65];
-  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int i = ty; i < 64; i += 4) {
-    const int r = r0 + i, c = c0 + tx;
-    if (r < rows && c < cols) tile[i][tx] = src[(size_t)r * cols + c];
+// Re-layout of a normal rhs B [K, N] into Bt [N, K].  16-byte loads along
+// N, an in-register byte (or half-word) transpose with v_perm, a dword tile
+// in LDS, and 16-byte stores along K, so both HBM sides move whole lines.
+//
+// int8: a 128-thread block moves a 64 (k) x 128 (n) tile.  Thread (k4, n16)
+// loads rows 4 k4 .. 4 k4 + 3 at bytes 16 n16 .. +15; each output dword is
+// the 4 k-bytes of one column.
+__global__ __launch_bounds__(128) void transpose_i8_kernel(const uint8_t *__restrict__ src,
+                                                           uint8_t *__restrict__ dst, int K, int N) {
+  __shared__ uint32_t T[128][17];  // [n][k / 4], padded
+  const int k0 = blockIdx.y * 64, n0 = blockIdx.x * 128;
+  const int tid = threadIdx.x, k4 = tid & 15, n16 = tid >> 4;
+  u32x4 r[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    r[i] = *(const u32x4 *)(src + (size_t)(k0 + 4 * k4 + i) * N + n0 + 16 * n16);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    // rows a0..a3 hold columns 4w..4w+3; out[c] = bytes c of a0, a1, a2, a3
+    const uint32_t a0 = r[0][w], a1 = r[1][w], a2 = r[2][w], a3 = r[3][w];
+    const uint32_t t01l = __builtin_amdgcn_perm(a1, a0, 0x05010400u);
+    const uint32_t t01h = __builtin_amdgcn_perm(a1, a0, 0x07030602u);
+    const uint32_t t23l = __builtin_amdgcn_perm(a3, a2, 0x05010400u);
+    const uint32_t t23h = __builtin_amdgcn_perm(a3, a2, 0x07030602u);
+    const int n = 16 * n16 + 4 * w;
+    T[n + 0][k4] = __builtin_amdgcn_perm(t23l, t01l, 0x05040100u);
+    T[n + 1][k4] = __builtin_amdgcn_perm(t23l, t01l, 0x07060302u);
+    T[n + 2][k4] = __builtin_amdgcn_perm(t23h, t01h, 0x05040100u);
+    T[n + 3][k4] = __builtin_amdgcn_perm(t23h, t01h, 0x07060302u);
   }
   __syncthreads();
-  for (int i = ty; i < 64; i += 4) {
-    const int c = c0 + i, r = r0 + tx;
-    if (r < rows && c < cols) dst[(size_t)c * rows + r] = tile[tx][i];
+  // thread tid writes row n0 + tid of Bt: 64 bytes of k
+  uint8_t *d = dst + (size_t)(n0 + tid) * K + k0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    u32x4 v;
+    v[0] = T[tid][4 * q + 0];
+    v[1] = T[tid][4 * q + 1];
+    v[2] = T[tid][4 * q + 2];
+    v[3] = T[tid][4 * q + 3];
+    *(u32x4 *)(d + 16 * q) = v;
+  }
+}
+
+// 16-bit: a 128-thread block moves a 32 (k) x 64 (n) tile.  Thread (k2, n8)
+// loads rows 2 k2, 2 k2 + 1 at elements 8 n8 .. +7; each output dword is the
+// 2 k-elements of one column.
+__global__ __launch_bounds__(128) void transpose_b16_kernel(const uint16_t *__restrict__ src,
+                                                            uint16_t *__restrict__ dst, int K, int N) {
+  __shared__ uint32_t T[64][17];  // [n][k / 2], padded
+  const int k0 = blockIdx.y * 32, n0 = blockIdx.x * 64;
+  const int tid = threadIdx.x, k2 = tid & 15, n8 = tid >> 4;
+  const u32x4 r0 = *(const u32x4 *)(src + (size_t)(k0 + 2 * k2) * N + n0 + 8 * n8);
+  const u32x4 r1 = *(const u32x4 *)(src + (size_t)(k0 + 2 * k2 + 1) * N + n0 + 8 * n8);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int n = 8 * n8 + 2 * w;
+    T[n + 0][k2] = __builtin_amdgcn_perm(r1[w], r0[w], 0x05040100u);
+    T[n + 1][k2] = __builtin_amdgcn_perm(r1[w], r0[w], 0x07060302u);
+  }
+  __syncthreads();
+  // thread tid writes half of row n0 + tid/2 of Bt: 32 bytes of k
+  const int n = tid >> 1, q0 = (tid & 1) * 2;
+  uint16_t *d = dst + (size_t)(n0 + n) * K + k0;
+#pragma unroll
+  for (int q = q0; q < q0 + 2; ++q) {
+    u32x4 v;
+    v[0] = T[n][4 * q + 0];
+    v[1] = T[n][4 * q + 1];
+    v[2] = T[n][4 * q + 2];
+    v[3] = T[n][4 * q + 3];
+    *(u32x4 *)(d + 8 * q) = v;
   }
 }
 
@@ -218,11 +285,11 @@ int launch_gemm(hipStream_t st, GemmArgs args, int ctas_256) {
   if (args.m % 256 == 0 && args.n % 256 == 0 && ctas_256 >= 192) {
     args.tiles_n = args.n / 256;
     dim3 grid((args.m / 256) * args.tiles_n);
-    hipLaunchKernelGGL((gemm_nt_kernel<KIND, 256, 256, OUT>), grid, dim3(256), 0, st, args);
+    hipLaunchKernelGGL((gemm_nt_kernel<KIND, 256, 256, OUT>), grid, dim3(512), 0, st, args);
   } else {
     args.tiles_n = args.n / 128;
     dim3 grid((args.m / 128) * args.tiles_n);
-    hipLaunchKernelGGL((gemm_nt_kernel<KIND, 128, 128, OUT>), grid, dim3(256), 0, st, args);
+    hipLaunchKernelGGL((gemm_nt_kernel<KIND, 128, 128, OUT>), grid, dim3(512), 0, st, args);
   }
   return launch_status("gemm_nt_kernel");
 }
@@ -231,14 +298,15 @@ int relayout_rhs(wafer_hip_context *ctx, const void *rhs, uint32_t k, uint32_t n
                  const uint8_t **bt) {
   const size_t need = (size_t)k * n * esize;
   WAFER_TRY(ensure_workspace(ctx, &ctx->relayout, &ctx->relayout_bytes, need));
-  dim3 grid((n + 63) / 64, (k + 63) / 64);
+  // check_shape guarantees n % 128 == 0 and k a multiple of 64 (int8) or
+  // 32 (16-bit), so every tile is full
   if (esize == 1)
-    hipLaunchKernelGGL(transpose_kernel<uint8_t>, grid, dim3(256), 0, ctx->stream,
+    hipLaunchKernelGGL(transpose_i8_kernel, dim3(n / 128, k / 64), dim3(128), 0, ctx->stream,
                        (const uint8_t *)rhs, (uint8_t *)ctx->relayout, (int)k, (int)n);
   else
-    hipLaunchKernelGGL(transpose_kernel<uint16_t>, grid, dim3(256), 0, ctx->stream,
+    hipLaunchKernelGGL(transpose_b16_kernel, dim3(n / 64, k / 32), dim3(128), 0, ctx->stream,
                        (const uint16_t *)rhs, (uint16_t *)ctx->relayout, (int)k, (int)n);
-  WAFER_TRY(launch_status("transpose_kernel"));
+  WAFER_TRY(launch_status("transpose kernel"));
   *bt = (const uint8_t *)ctx->relayout;
   return WAFER_HIP_OK;
 }
@@ -248,8 +316,9 @@ int check_shape(uint32_t m, uint32_t k, uint32_t n, int esize, const char *what)
   if (m % 128 || n % 128 || ((uint64_t)k * esize) % BKB)
     return fail(WAFER_HIP_E_UNSUPPORTED,
                 std::string(what) + ": needs m, n multiples of 128 and k*elem_bytes a multiple of 64");
-  if ((uint64_t)m * k * esize > 0x7fffffffffull || (uint64_t)k * esize > 0x7fffffffull)
-    return fail(WAFER_HIP_E_INVALID_FIELD, std::string(what) + ": operand too large");
+  // in-tile offsets (row * k * esize over 256 rows) are 32-bit
+  if ((uint64_t)m * k * esize > 0x7fffffffffull || (uint64_t)k * esize >= (1u << 24))
+    return fail(WAFER_HIP_E_INVALID_FIELD, std::string(what) + ": operand too large (k * element bytes must be below 16 MiB)");
   return WAFER_HIP_OK;
 }
 
