@@ -173,4 +173,49 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// Eight consecutive elements from element index i (a multiple of 8) with
+// 16-byte accesses: one for 16-bit formats, two for F32.  The caller checks
+// 16-byte alignment of the base.
+template <uint32_t F> __device__ inline void load8(const void *b, int64_t i, float (&v)[8]) {
+  if constexpr (F == WAFER_FMT_F32) {
+    const u32x4 lo = ((const u32x4 *)b)[i / 4], hi = ((const u32x4 *)b)[i / 4 + 1];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = u2f(lo[e]);
+      v[4 + e] = u2f(hi[e]);
+    }
+  } else {
+    const u32x4 w = ((const u32x4 *)b)[i / 8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint16_t l = (uint16_t)(w[e] & 0xffffu), h = (uint16_t)(w[e] >> 16);
+      v[2 * e] = F == WAFER_FMT_BF16 ? bf16_to_f32(l) : f16_to_f32(l);
+      v[2 * e + 1] = F == WAFER_FMT_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+    }
+  }
+}
+template <uint32_t F> __device__ inline void store8(void *b, int64_t i, const float (&v)[8]) {
+  if constexpr (F == WAFER_FMT_F32) {
+    u32x4 lo, hi;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      lo[e] = f2u(v[e]);
+      hi[e] = f2u(v[4 + e]);
+    }
+    ((u32x4 *)b)[i / 4] = lo;
+    ((u32x4 *)b)[i / 4 + 1] = hi;
+  } else {
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t l = F == WAFER_FMT_BF16 ? f32_to_bf16(v[2 * e]) : f32_to_f16(v[2 * e]);
+      const uint32_t h = F == WAFER_FMT_BF16 ? f32_to_bf16(v[2 * e + 1]) : f32_to_f16(v[2 * e + 1]);
+      w[e] = l | (h << 16);
+    }
+    ((u32x4 *)b)[i / 8] = w;
+  }
+}
+inline bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+
 }  // namespace wafer

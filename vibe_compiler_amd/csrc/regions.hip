@@ -45,8 +45,9 @@ __device__ inline float block_max(float v, float *red) {
 
 __device__ inline float explp_acc(float x) { return exp2f(x * 0x1.715476p+0f); }
 
-// y = x * Rsqrt(Sum(x*x) * (1/N) + eps) * w
-template <uint32_t F>
+// y = x * Rsqrt(Sum(x*x) * (1/N) + eps) * w.  VEC: 8 columns per thread and
+// access (cols % 8 == 0, tensors 16-byte aligned).
+template <uint32_t F, bool VEC>
 __global__ __launch_bounds__(RT) void rmsnorm_kernel(const void *__restrict__ x,
                                                      const void *__restrict__ w,
                                                      void *__restrict__ y, int64_t cols,
@@ -54,15 +55,35 @@ __global__ __launch_bounds__(RT) void rmsnorm_kernel(const void *__restrict__ x,
   __shared__ float red[RT / 64];
   const int64_t base = (int64_t)blockIdx.x * cols;
   float s = 0.0f;
-  for (int64_t c = threadIdx.x; c < cols; c += RT) {
-    const float v = load_as_f32<F>(x, base + c);
-    s += v * v;
+  if constexpr (VEC) {
+    for (int64_t c = 8 * threadIdx.x; c < cols; c += 8 * RT) {
+      float v[8];
+      load8<F>(x, base + c, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += v[e] * v[e];
+    }
+  } else {
+    for (int64_t c = threadIdx.x; c < cols; c += RT) {
+      const float v = load_as_f32<F>(x, base + c);
+      s += v * v;
+    }
   }
   s = block_sum(s, red);
   const float rs = 1.0f / sqrtf(s * inv_n + eps);
-  for (int64_t c = threadIdx.x; c < cols; c += RT) {
-    const float v = load_as_f32<F>(x, base + c);
-    store_from_f32<F>(y, base + c, v * rs * load_as_f32<F>(w, c));
+  if constexpr (VEC) {
+    for (int64_t c = 8 * threadIdx.x; c < cols; c += 8 * RT) {
+      float v[8], wv[8], o[8];
+      load8<F>(x, base + c, v);
+      load8<F>(w, c, wv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = v[e] * rs * wv[e];
+      store8<F>(y, base + c, o);
+    }
+  } else {
+    for (int64_t c = threadIdx.x; c < cols; c += RT) {
+      const float v = load_as_f32<F>(x, base + c);
+      store_from_f32<F>(y, base + c, v * rs * load_as_f32<F>(w, c));
+    }
   }
 }
 
@@ -84,67 +105,134 @@ __global__ __launch_bounds__(RT) void softmax_kernel(const void *__restrict__ x,
 }
 
 // y = g * Recip(1 + ExpLp(-g)) * u
-template <uint32_t F>
+__device__ inline float silu_mul_1(float g, float u) {
+  const float sig = 1.0f / (1.0f + explp_acc(-g));
+  return g * sig * u;
+}
+template <uint32_t F, bool VEC>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const void *__restrict__ gate,
                                                        const void *__restrict__ up,
                                                        void *__restrict__ y, uint64_t count) {
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
-    const float g = load_as_f32<F>(gate, (int64_t)i);
-    const float sig = 1.0f / (1.0f + explp_acc(-g));
-    store_from_f32<F>(y, (int64_t)i, g * sig * load_as_f32<F>(up, (int64_t)i));
+  const uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint64_t tail = 0;
+  if constexpr (VEC) {
+    for (uint64_t q = gid; q < count / 8; q += stride) {
+      float g[8], u[8], r[8];
+      load8<F>(gate, (int64_t)(8 * q), g);
+      load8<F>(up, (int64_t)(8 * q), u);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = silu_mul_1(g[e], u[e]);
+      store8<F>(y, (int64_t)(8 * q), r);
+    }
+    tail = count / 8 * 8;
   }
+  for (uint64_t i = tail + gid; i < count; i += stride)
+    store_from_f32<F>(y, (int64_t)i, silu_mul_1(load_as_f32<F>(gate, (int64_t)i), load_as_f32<F>(up, (int64_t)i)));
 }
 
 // y = 0.5*x*(1 + Tanh(sqrt(2/pi)*(x + 0.044715*x^3)))
-template <uint32_t F>
+__device__ inline float gelu_tanh_1(float v) {
+  const float k0 = 0.7978845608028654f, k1 = 0.044715f;
+  const float inner = k0 * (v + k1 * (v * v * v));
+  return 0.5f * v * (1.0f + tanhf(inner));
+}
+template <uint32_t F, bool VEC>
 __global__ __launch_bounds__(256) void gelu_tanh_kernel(const void *__restrict__ x,
                                                         void *__restrict__ y, uint64_t count) {
-  const float k0 = 0.7978845608028654f, k1 = 0.044715f;
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
-    const float v = load_as_f32<F>(x, (int64_t)i);
-    const float inner = k0 * (v + k1 * (v * v * v));
-    store_from_f32<F>(y, (int64_t)i, 0.5f * v * (1.0f + tanhf(inner)));
+  const uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint64_t tail = 0;
+  if constexpr (VEC) {
+    for (uint64_t q = gid; q < count / 8; q += stride) {
+      float v[8], r[8];
+      load8<F>(x, (int64_t)(8 * q), v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = gelu_tanh_1(v[e]);
+      store8<F>(y, (int64_t)(8 * q), r);
+    }
+    tail = count / 8 * 8;
   }
+  for (uint64_t i = tail + gid; i < count; i += stride)
+    store_from_f32<F>(y, (int64_t)i, gelu_tanh_1(load_as_f32<F>(x, (int64_t)i)));
 }
 
 // Rotate-half RoPE: inv_freq[i] = 1/theta^(2i/D), angle = pos*inv_freq[d mod D/2],
 // y = x*cos(angle) + rotate_half(x)*sin(angle), rotate_half(x) = [-x2, x1].
-// One thread per rotation pair (d, d + head_dim/2) of a row: both outputs
-// come from the same two inputs, so y may alias x.
-template <uint32_t F>
+// One thread per rotation pair (d, d + head_dim/2) of a row (VEC: per 8
+// consecutive pairs, head_dim % 16 == 0 and 16-byte aligned tensors): both
+// outputs of a pair come from the same two inputs, so y may alias x.
+__device__ inline void rope_pair(float xl, float xh, float angle, float &yl, float &yh) {
+  const float c = cosf(angle), s = sinf(angle);
+  // y[d] = x[d]*cos + rot[d]*sin with rot = (-x[d+half], x[d-half])
+  yl = xl * c + (-xh) * s;
+  yh = xh * c + xl * s;
+}
+template <uint32_t F, bool VEC>
 __global__ __launch_bounds__(256) void rope_kernel(const void *x, void *y,
                                                    int64_t tokens, int64_t heads, int64_t head_dim,
                                                    const int32_t *__restrict__ positions,
                                                    float theta) {
   const int64_t half = head_dim / 2;
-  const int64_t pairs = tokens * heads * half;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < pairs; e += stride) {
-    const int64_t i = e % half;
-    const int64_t rowi = e / half;  // (token, head)
-    const int64_t t = rowi / heads;
-    const int64_t lo = rowi * head_dim + i, hi = lo + half;
-    const float inv_freq = 1.0f / powf(theta, (float)(2 * i) / (float)head_dim);
-    const float angle = (float)positions[t] * inv_freq;
-    const float c = cosf(angle), s = sinf(angle);
-    const float xl = load_as_f32<F>(x, lo), xh = load_as_f32<F>(x, hi);
-    // y[d] = x[d]*cos + rot[d]*sin with rot = (-x[d+half], x[d-half])
-    store_from_f32<F>(y, lo, xl * c + (-xh) * s);
-    store_from_f32<F>(y, hi, xh * c + xl * s);
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if constexpr (VEC) {
+    const int64_t per_row = half / 8;
+    const int64_t groups = tokens * heads * per_row;
+    for (int64_t e = gid; e < groups; e += stride) {
+      const int64_t i0 = (e % per_row) * 8;
+      const int64_t rowi = e / per_row;  // (token, head)
+      const float pos = (float)positions[rowi / heads];
+      const int64_t lo = rowi * head_dim + i0, hi = lo + half;
+      float xl[8], xh[8], yl[8], yh[8];
+      load8<F>(x, lo, xl);
+      load8<F>(x, hi, xh);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float inv_freq = 1.0f / powf(theta, (float)(2 * (i0 + k)) / (float)head_dim);
+        rope_pair(xl[k], xh[k], pos * inv_freq, yl[k], yh[k]);
+      }
+      store8<F>(y, lo, yl);
+      store8<F>(y, hi, yh);
+    }
+  } else {
+    const int64_t pairs = tokens * heads * half;
+    for (int64_t e = gid; e < pairs; e += stride) {
+      const int64_t i = e % half;
+      const int64_t rowi = e / half;  // (token, head)
+      const int64_t t = rowi / heads;
+      const int64_t lo = rowi * head_dim + i, hi = lo + half;
+      const float inv_freq = 1.0f / powf(theta, (float)(2 * i) / (float)head_dim);
+      float yl, yh;
+      rope_pair(load_as_f32<F>(x, lo), load_as_f32<F>(x, hi), (float)positions[t] * inv_freq, yl, yh);
+      store_from_f32<F>(y, lo, yl);
+      store_from_f32<F>(y, hi, yh);
+    }
   }
 }
 
-template <uint32_t F>
+// VEC: 8 columns per thread (cols % 8 == 0, tensors 16-byte aligned)
+template <uint32_t F, bool VEC>
 __global__ __launch_bounds__(256) void bias_add_kernel(const void *__restrict__ x,
                                                        const float *__restrict__ bias,
                                                        void *__restrict__ y, int64_t rows,
                                                        int64_t cols) {
   const int64_t count = rows * cols;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < count; e += stride)
-    store_from_f32<F>(y, e, load_as_f32<F>(x, e) + bias[e % cols]);
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if constexpr (VEC) {
+    for (int64_t q = gid; q < count / 8; q += stride) {
+      const int64_t e0 = 8 * q, c0 = e0 % cols;
+      float v[8], b[8], r[8];
+      load8<F>(x, e0, v);
+      load8<WAFER_FMT_F32>(bias, c0, b);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = v[e] + b[e];
+      store8<F>(y, e0, r);
+    }
+  } else {
+    for (int64_t e = gid; e < count; e += stride) store_from_f32<F>(y, e, load_as_f32<F>(x, e) + bias[e % cols]);
+  }
 }
 
 unsigned grid_for(uint64_t count) {
@@ -159,6 +247,26 @@ unsigned grid_for(uint64_t count) {
       hipLaunchKernelGGL(KERNEL<WAFER_FMT_BF16>, GRID, BLOCK, 0, ctx->stream, __VA_ARGS__);   \
     else                                                                                       \
       hipLaunchKernelGGL(KERNEL<WAFER_FMT_F16>, GRID, BLOCK, 0, ctx->stream, __VA_ARGS__);    \
+  } while (0)
+
+// format x {scalar, 8-wide} dispatch for the kernels with a VEC parameter
+#define DISPATCH_FB(format, vec, KERNEL, GRID, BLOCK, ...)                                      \
+  do {                                                                                         \
+    if (vec) {                                                                                 \
+      if ((format) == WAFER_FMT_F32)                                                           \
+        hipLaunchKernelGGL((KERNEL<WAFER_FMT_F32, true>), GRID, BLOCK, 0, ctx->stream, __VA_ARGS__);  \
+      else if ((format) == WAFER_FMT_BF16)                                                     \
+        hipLaunchKernelGGL((KERNEL<WAFER_FMT_BF16, true>), GRID, BLOCK, 0, ctx->stream, __VA_ARGS__); \
+      else                                                                                     \
+        hipLaunchKernelGGL((KERNEL<WAFER_FMT_F16, true>), GRID, BLOCK, 0, ctx->stream, __VA_ARGS__);  \
+    } else {                                                                                   \
+      if ((format) == WAFER_FMT_F32)                                                           \
+        hipLaunchKernelGGL((KERNEL<WAFER_FMT_F32, false>), GRID, BLOCK, 0, ctx->stream, __VA_ARGS__); \
+      else if ((format) == WAFER_FMT_BF16)                                                     \
+        hipLaunchKernelGGL((KERNEL<WAFER_FMT_BF16, false>), GRID, BLOCK, 0, ctx->stream, __VA_ARGS__);\
+      else                                                                                     \
+        hipLaunchKernelGGL((KERNEL<WAFER_FMT_F16, false>), GRID, BLOCK, 0, ctx->stream, __VA_ARGS__); \
+    }                                                                                          \
   } while (0)
 
 int prologue(wafer_hip_context *ctx, uint32_t format, const char *what) {
@@ -180,7 +288,8 @@ extern "C" int wafer_hip_rmsnorm(wafer_hip_context *ctx, uint32_t format, const 
   if (!x || !w || !y) return fail(WAFER_HIP_E_INVALID_FIELD, "rmsnorm: null tensor");
   if (rows > 0x7fffffffull) return fail(WAFER_HIP_E_INVALID_FIELD, "rmsnorm: too many rows");
   const float inv_n = 1.0f / (float)cols;
-  DISPATCH_F(format, rmsnorm_kernel, dim3((unsigned)rows), dim3(RT), x, w, y, (int64_t)cols, inv_n, eps);
+  const bool vec = cols % 8 == 0 && aligned16(x) && aligned16(w) && aligned16(y);
+  DISPATCH_FB(format, vec, rmsnorm_kernel, dim3((unsigned)rows), dim3(RT), x, w, y, (int64_t)cols, inv_n, eps);
   return launch_status("rmsnorm_kernel");
 }
 
@@ -199,7 +308,9 @@ extern "C" int wafer_hip_silu_mul(wafer_hip_context *ctx, uint32_t format, const
   WAFER_TRY(prologue(ctx, format, "silu_mul"));
   if (count == 0) return WAFER_HIP_OK;
   if (!gate || !up || !y) return fail(WAFER_HIP_E_INVALID_FIELD, "silu_mul: null tensor");
-  DISPATCH_F(format, silu_mul_kernel, dim3(grid_for(count)), dim3(256), gate, up, y, count);
+  const bool vec = aligned16(gate) && aligned16(up) && aligned16(y);
+  DISPATCH_FB(format, vec, silu_mul_kernel, dim3(grid_for(vec ? (count + 7) / 8 : count)), dim3(256), gate, up,
+              y, count);
   return launch_status("silu_mul_kernel");
 }
 
@@ -208,7 +319,9 @@ extern "C" int wafer_hip_gelu_tanh(wafer_hip_context *ctx, uint32_t format, cons
   WAFER_TRY(prologue(ctx, format, "gelu_tanh"));
   if (count == 0) return WAFER_HIP_OK;
   if (!x || !y) return fail(WAFER_HIP_E_INVALID_FIELD, "gelu_tanh: null tensor");
-  DISPATCH_F(format, gelu_tanh_kernel, dim3(grid_for(count)), dim3(256), x, y, count);
+  const bool vec = aligned16(x) && aligned16(y);
+  DISPATCH_FB(format, vec, gelu_tanh_kernel, dim3(grid_for(vec ? (count + 7) / 8 : count)), dim3(256), x, y,
+              count);
   return launch_status("gelu_tanh_kernel");
 }
 
@@ -220,8 +333,9 @@ extern "C" int wafer_hip_rope(wafer_hip_context *ctx, uint32_t format, const voi
   const uint64_t count = tokens * heads * head_dim;
   if (count == 0) return WAFER_HIP_OK;
   if (!x || !y || !positions) return fail(WAFER_HIP_E_INVALID_FIELD, "rope: null tensor");
-  DISPATCH_F(format, rope_kernel, dim3(grid_for(count / 2)), dim3(256), x, y, (int64_t)tokens,
-             (int64_t)heads, (int64_t)head_dim, positions, theta);
+  const bool vec = head_dim % 16 == 0 && aligned16(x) && aligned16(y);
+  DISPATCH_FB(format, vec, rope_kernel, dim3(grid_for(vec ? count / 16 : count / 2)), dim3(256), x, y,
+              (int64_t)tokens, (int64_t)heads, (int64_t)head_dim, positions, theta);
   return launch_status("rope_kernel");
 }
 
@@ -230,7 +344,8 @@ extern "C" int wafer_hip_bias_add(wafer_hip_context *ctx, uint32_t format, const
   WAFER_TRY(prologue(ctx, format, "bias_add"));
   if (rows * cols == 0) return WAFER_HIP_OK;
   if (!x || !bias || !y) return fail(WAFER_HIP_E_INVALID_FIELD, "bias_add: null tensor");
-  DISPATCH_F(format, bias_add_kernel, dim3(grid_for(rows * cols)), dim3(256), x, bias, y,
-             (int64_t)rows, (int64_t)cols);
+  const bool vec = cols % 8 == 0 && aligned16(x) && aligned16(bias) && aligned16(y);
+  DISPATCH_FB(format, vec, bias_add_kernel, dim3(grid_for(vec ? rows * cols / 8 : rows * cols)), dim3(256), x,
+              bias, y, (int64_t)rows, (int64_t)cols);
   return launch_status("bias_add_kernel");
 }
