@@ -157,6 +157,20 @@ def test_formal_gemm_bit_exact_random(hip, B, oracle, fmt_in, fmt_out, lt, rt):
         assert np.array_equal(got.view(np.uint8), ref.view(np.uint8)), (m, k, n, batch)
 
 
+@pytest.mark.parametrize("m,k,n", [(128, 512, 2048), (128, 2048, 512), (256, 96, 1024)])
+def test_formal_gemm_bit_exact_config0_shapes(hip, B, oracle, m, k, n):
+    """The formal GEMM at the MLP's shapes (each picks a different per-thread
+    chain count): every output bit-identical to the CPU formal lane."""
+    say("formal gemm config0 shape", m, k, n)
+    rng = np.random.default_rng(m * 7 + k * 3 + n)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = (rng.standard_normal((k, n)) / math.sqrt(k)).astype(np.float32)
+    ref = oracle.gemm_formal(oracle.F32, oracle.F32, a, b, m, k, n)
+    out = torch.zeros(m * n, dtype=torch.float32, device="cuda")
+    hip.gemm(dev(a), dev(b), out, m, k, n)
+    assert np.array_equal(host(out).view(np.uint32), ref.view(np.uint32))
+
+
 def test_fp32_mlp_block_config0(hip, B, oracle):
     """x[128,512] @ W1 + b1, tanh-GELU, @ W2 + b2 (f32)."""
     say("fp32 mlp block")

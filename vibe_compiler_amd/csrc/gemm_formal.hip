@@ -11,25 +11,34 @@
 // (:302-309).  Because every output keeps the exact k-order chain, results
 // are bit-identical to the formal lane, not merely close.
 //
-// Layout on the GPU: a (16 MT)x(16 MT) output tile per 256-thread workgroup,
-// MT x MT independent fma chains per thread (ILP across chains, never inside
-// one), operands widened to f32 once into LDS in 16-deep k slices.  MT = 4
-// for large outputs; MT = 1 when the 64x64 grid would leave CUs idle (a
-// chain is sequential in k, so parallelism can only come from outputs).
+// Layout on the GPU: a (16 MT) x (16 MT) output tile per 256-thread
+// workgroup, MT x MT independent fma chains per thread (ILP across chains,
+// never inside one).  Operands are widened to f32 once and staged through
+// double-buffered LDS in 64-deep k slices, both k-contiguous (the rhs is
+// transposed on its way into LDS), so a thread fetches 4 consecutive k of
+// each operand with one ds_read_b128; the next slice's global loads are
+// issued before the current slice's chains run.  MT is the largest of 4, 2,
+// 1 whose grid still covers the CUs (a chain is sequential in k, so
+// parallelism comes only from outputs).
 #include "common.h"
 
 namespace wafer {
 namespace {
 
-constexpr int TK = 16;
+
+// k-slice depth (256/MT measured no faster than 64 for one or two chains
+// per thread)
+template <int MT> struct SliceDepth { static constexpr int TK = 64; };
 
 template <uint32_t IN, uint32_t OUT, int MT>
 __global__ __launch_bounds__(256) void gemm_formal_kernel(
     const void *__restrict__ lhs, const void *__restrict__ rhs, void *__restrict__ dst,
     const float *__restrict__ psum, int m, int k, int n, int lhs_t, int rhs_t) {
+  constexpr int TK = SliceDepth<MT>::TK;
+  constexpr int KP = TK + 4;  // LDS row pitch (floats): +16 B keeps b128 reads conflict-free
   constexpr int TM = 16 * MT, TN = 16 * MT, LOADS = TM * TK / 256;
-  __shared__ float As[TK][TM + 1];
-  __shared__ float Bs[TK][TN + 1];
+  __shared__ __align__(16) float As[2][TM][KP];
+  __shared__ __align__(16) float Bs[2][TN][KP];
   const int b = blockIdx.z;
   const int m0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
@@ -41,38 +50,74 @@ __global__ __launch_bounds__(256) void gemm_formal_kernel(
 #pragma unroll
     for (int j = 0; j < MT; ++j) acc[i][j] = 0.0f;
 
-  for (int k0 = 0; k0 < k; k0 += TK) {
-    // TM x 16 slice of lhs and 16 x TN slice of rhs, LOADS elements per thread each
+  // staging element e = tid + 256 r of a slice; the walk order follows the
+  // operand's contiguous dimension so global loads coalesce
+  float ra[LOADS], rbv[LOADS];
+  auto gload = [&](int k0) {
 #pragma unroll
     for (int r = 0; r < LOADS; ++r) {
       const int e = tid + 256 * r;
-      const int kk = e & 15, mm = e >> 4;  // lhs: row mm, depth kk
+      int mm, kk;
+      if (lhs_t) { mm = e % TM; kk = e / TM; } else { mm = e / TK; kk = e % TK; }
       const int gm = m0 + mm, gk = k0 + kk;
-      float a = 0.0f;
-      if (gm < m && gk < k)
-        a = load_as_f32<IN>(lhs, lb + (lhs_t ? (int64_t)gk * m + gm : (int64_t)gm * k + gk));
-      As[kk][mm] = a;
-      const int nn = e % TN, kb = e / TN;  // rhs: depth kb, column nn
+      ra[r] = (gm < m && gk < k)
+                  ? load_as_f32<IN>(lhs, lb + (lhs_t ? (int64_t)gk * m + gm : (int64_t)gm * k + gk))
+                  : 0.0f;
+      int nn, kb;
+      if (rhs_t) { nn = e / TK; kb = e % TK; } else { nn = e % TN; kb = e / TN; }
       const int gn = n0 + nn, gk2 = k0 + kb;
-      float bv = 0.0f;
-      if (gn < n && gk2 < k)
-        bv = load_as_f32<IN>(rhs, rb + (rhs_t ? (int64_t)gn * k + gk2 : (int64_t)gk2 * n + gn));
-      Bs[kb][nn] = bv;
+      rbv[r] = (gn < n && gk2 < k)
+                   ? load_as_f32<IN>(rhs, rb + (rhs_t ? (int64_t)gn * k + gk2 : (int64_t)gk2 * n + gn))
+                   : 0.0f;
     }
-    __syncthreads();
-    const int kend = min(TK, k - k0);
-    for (int kk = 0; kk < kend; ++kk) {
-      float av[MT], bv[MT];
+  };
+  auto sstore = [&](int buf) {
 #pragma unroll
-      for (int i = 0; i < MT; ++i) av[i] = As[kk][ty + 16 * i];
-#pragma unroll
-      for (int j = 0; j < MT; ++j) bv[j] = Bs[kk][tx + 16 * j];
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int j = 0; j < MT; ++j) acc[i][j] = __builtin_fmaf(av[i], bv[j], acc[i][j]);
+    for (int r = 0; r < LOADS; ++r) {
+      const int e = tid + 256 * r;
+      if (lhs_t) As[buf][e % TM][e / TM] = ra[r]; else As[buf][e / TK][e % TK] = ra[r];
+      if (rhs_t) Bs[buf][e / TK][e % TK] = rbv[r]; else Bs[buf][e % TN][e / TN] = rbv[r];
     }
-    __syncthreads();
+  };
+
+  const int nslices = (k + TK - 1) / TK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int sl = 0; sl < nslices; ++sl) {
+    const int buf = sl & 1;
+    if (sl + 1 < nslices) gload((sl + 1) * TK);
+    const int kend = min(TK, k - sl * TK);
+    if (kend == TK) {
+#pragma unroll
+      for (int kq = 0; kq < TK; kq += 4) {
+        f32x4 av[MT], bv[MT];
+#pragma unroll
+        for (int i = 0; i < MT; ++i) av[i] = *(const f32x4 *)&As[buf][ty + 16 * i][kq];
+#pragma unroll
+        for (int j = 0; j < MT; ++j) bv[j] = *(const f32x4 *)&Bs[buf][tx + 16 * j][kq];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int j = 0; j < MT; ++j) acc[i][j] = __builtin_fmaf(av[i][q], bv[j][q], acc[i][j]);
+      }
+    } else {
+      // the last, partial slice: exactly kend steps (a padded fma(0, 0, -0)
+      // would turn a -0 accumulator into +0)
+      for (int kk = 0; kk < kend; ++kk) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int j = 0; j < MT; ++j)
+            acc[i][j] = __builtin_fmaf(As[buf][ty + 16 * i][kk], Bs[buf][tx + 16 * j][kk], acc[i][j]);
+      }
+    }
+    if (sl + 1 < nslices) {
+      sstore(buf ^ 1);
+      __syncthreads();
+    }
   }
 
 #pragma unroll
@@ -112,9 +157,12 @@ int launch_out(uint32_t out, dim3 grid, hipStream_t st, const void *lhs, const v
 template <uint32_t IN>
 int launch_in(uint32_t out, int cus, hipStream_t st, const void *lhs, const void *rhs, void *dst,
               const float *psum, uint32_t m, uint32_t k, uint32_t n, uint32_t batch, int lt, int rt) {
-  const uint64_t big = (uint64_t)((n + 63) / 64) * ((m + 63) / 64) * batch;
-  if (big >= (uint64_t)cus)
+  auto grid = [&](uint32_t t) { return (uint64_t)((n + t - 1) / t) * ((m + t - 1) / t) * batch; };
+  if (grid(64) >= (uint64_t)cus)
     return launch_out<IN, 4>(out, dim3((n + 63) / 64, (m + 63) / 64, batch), st, lhs, rhs, dst, psum,
+                             m, k, n, lt, rt);
+  if (grid(32) >= (uint64_t)cus)
+    return launch_out<IN, 2>(out, dim3((n + 31) / 32, (m + 31) / 32, batch), st, lhs, rhs, dst, psum,
                              m, k, n, lt, rt);
   return launch_out<IN, 1>(out, dim3((n + 15) / 16, (m + 15) / 16, batch), st, lhs, rhs, dst, psum, m,
                            k, n, lt, rt);
