@@ -76,6 +76,15 @@ int wafer_hip_context_destroy(wafer_hip_context *ctx);
 int wafer_hip_set_stream(wafer_hip_context *ctx, void *hip_stream);
 int wafer_hip_synchronize(wafer_hip_context *ctx);
 const char *wafer_hip_last_error(void);
+/* Device buffers and synchronous copies for host-side callers that hold
+ * tensors in host memory (the seam's TargetModelNumericTensor storage);
+ * copies are ordered on the context's stream and complete on return. */
+int wafer_hip_buffer_alloc(wafer_hip_context *ctx, uint64_t bytes, void **out);
+int wafer_hip_buffer_free(wafer_hip_context *ctx, void *buffer);
+int wafer_hip_copy_to_device(wafer_hip_context *ctx, void *dst, const void *src,
+                             uint64_t bytes);
+int wafer_hip_copy_to_host(wafer_hip_context *ctx, void *dst, const void *src,
+                           uint64_t bytes);
 /* Implementation string, the analogue of the evidence `implementation`
  * field (include/Wafer/Simulator/Kernel/TargetModelKernel.h:144-182). */
 const char *wafer_hip_implementation(void);
@@ -136,6 +145,10 @@ int wafer_hip_elementwise(wafer_hip_context *ctx, uint32_t op, uint32_t format,
 int wafer_hip_convert(wafer_hip_context *ctx, uint32_t opcode,
                       uint32_t rounding, const void *src, void *dst,
                       uint64_t count);
+/* The (source, destination) formats of a served convert route, for callers
+ * validating a FormalConvertOperation's descriptors (host only). */
+int wafer_hip_convert_route(uint32_t opcode, uint32_t *source_format,
+                            uint32_t *destination_format);
 /* op TargetReduceOperation {Sum, Max, Min} and dim TargetReduceDimension
  * (TargetOperation.h:102-113); shape is the logical shape (rank <= 8) and dst
  * holds the shape with reduced dimensions set to 1. */

@@ -69,3 +69,24 @@ def test_decoder_layer_flop_count():
     from vibe_compiler_amd import decoder_layer as DL
 
     assert DL.flops() == 2 * 1024 * 218_103_808 + 8_598_323_200 == 455_274_921_984
+
+
+def test_seam_library_exports_and_fails_loudly_without_gpu():
+    """The C++ seam library is built and exports the backend; on a machine
+    without a gfx950 device, creating the backend fails with a typed error
+    (no CPU fallback)."""
+    import subprocess
+
+    lib = ROOT / "vibe_compiler_amd" / "lib" / "libwafer_hip_seam.so"
+    check = ROOT / "tests" / "seam" / "_build" / "seam_check"
+    if not lib.exists() or not check.exists():
+        pytest.skip("seam not built")
+    syms = subprocess.run(["nm", "-D", "-C", str(lib)], capture_output=True, text=True).stdout
+    for name in ("wafer::model::HipTargetModelBackend::create", "wafer::model::HipTargetModelBackend::tryExecute",
+                 "wafer::model::PhysicalTensorDescriptor::create", "wafer::model::stringifyTargetModelKernelErrorCode"):
+        assert name in syms, name
+    import torch
+
+    if torch.cuda.device_count() == 0:
+        r = subprocess.run([str(check)], capture_output=True, text=True, timeout=60)
+        assert r.returncode == 2 and "FAIL create" in r.stdout, r.stdout + r.stderr

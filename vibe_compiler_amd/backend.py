@@ -43,7 +43,8 @@ EXPORTS = (
     "wafer_hip_convert", "wafer_hip_reduce", "wafer_hip_physical_bytes", "wafer_hip_pack",
     "wafer_hip_unpack", "wafer_hip_attention_prefill", "wafer_hip_attention_decode",
     "wafer_hip_rmsnorm", "wafer_hip_softmax", "wafer_hip_silu_mul", "wafer_hip_gelu_tanh",
-    "wafer_hip_rope", "wafer_hip_bias_add", "wafer_hip_head_permute",
+    "wafer_hip_rope", "wafer_hip_bias_add", "wafer_hip_head_permute", "wafer_hip_buffer_alloc",
+    "wafer_hip_buffer_free", "wafer_hip_copy_to_device", "wafer_hip_copy_to_host", "wafer_hip_convert_route",
 )
 
 
@@ -98,6 +99,11 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wafer_hip_rope.argtypes = [vp, u32, vp, vp, u64, u64, u64, vp, f32]
     L.wafer_hip_bias_add.argtypes = [vp, u32, vp, vp, vp, u64, u64]
     L.wafer_hip_head_permute.argtypes = [vp, u32, vp, vp, u64, u64, u64, u64, u32]
+    L.wafer_hip_buffer_alloc.argtypes = [vp, u64, ctypes.POINTER(vp)]
+    L.wafer_hip_buffer_free.argtypes = [vp, vp]
+    L.wafer_hip_copy_to_device.argtypes = [vp, vp, vp, u64]
+    L.wafer_hip_copy_to_host.argtypes = [vp, vp, vp, u64]
+    L.wafer_hip_convert_route.argtypes = [u32, ctypes.POINTER(u32), ctypes.POINTER(u32)]
 
 
 def _check(status: int) -> None:

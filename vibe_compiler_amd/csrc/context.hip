@@ -99,3 +99,41 @@ extern "C" const char *wafer_hip_implementation(void) {
          "FA prefill (mfma_f32_32x32x16_bf16), FD decode (mfma_f32_16x16x32_bf16 + LSE fold), "
          "managed elementwise/convert/reduce, Cx/NCx codec, fused regions";
 }
+
+// ---- device buffers for host-side callers ---------------------------------
+// The seam adapter moves TargetModelNumericTensor storage through these, so
+// it needs nothing but this ABI.  Copies are ordered on the context's stream
+// and complete before the call returns.
+extern "C" int wafer_hip_buffer_alloc(wafer_hip_context *ctx, uint64_t bytes, void **out) {
+  WAFER_CHECK_CTX(ctx);
+  if (!out) return fail(WAFER_HIP_E_INVALID_FIELD, "buffer_alloc: null output pointer");
+  *out = nullptr;
+  WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
+  return check_hip(hipMalloc(out, bytes ? bytes : 1), "hipMalloc(buffer)");
+}
+
+extern "C" int wafer_hip_buffer_free(wafer_hip_context *ctx, void *buffer) {
+  WAFER_CHECK_CTX(ctx);
+  if (!buffer) return WAFER_HIP_OK;
+  WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
+  WAFER_TRY(check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize"));
+  return check_hip(hipFree(buffer), "hipFree(buffer)");
+}
+
+extern "C" int wafer_hip_copy_to_device(wafer_hip_context *ctx, void *dst, const void *src, uint64_t bytes) {
+  WAFER_CHECK_CTX(ctx);
+  if (bytes == 0) return WAFER_HIP_OK;
+  if (!dst || !src) return fail(WAFER_HIP_E_INVALID_FIELD, "copy_to_device: null pointer");
+  WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
+  WAFER_TRY(check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "hipMemcpyAsync(H2D)"));
+  return check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+}
+
+extern "C" int wafer_hip_copy_to_host(wafer_hip_context *ctx, void *dst, const void *src, uint64_t bytes) {
+  WAFER_CHECK_CTX(ctx);
+  if (bytes == 0) return WAFER_HIP_OK;
+  if (!dst || !src) return fail(WAFER_HIP_E_INVALID_FIELD, "copy_to_host: null pointer");
+  WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
+  WAFER_TRY(check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpyAsync(D2H)"));
+  return check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+}

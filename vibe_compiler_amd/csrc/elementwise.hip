@@ -277,6 +277,19 @@ extern "C" int wafer_hip_elementwise(wafer_hip_context *ctx, uint32_t op, uint32
   }
 }
 
+extern "C" int wafer_hip_convert_route(uint32_t opcode, uint32_t *source_format,
+                                       uint32_t *destination_format) {
+  if (!source_format || !destination_format)
+    return fail(WAFER_HIP_E_INVALID_FIELD, "convert_route: null output pointer");
+  for (const Route &r : kRoutes)
+    if (r.op == opcode) {
+      *source_format = r.src;
+      *destination_format = r.dst;
+      return WAFER_HIP_OK;
+    }
+  return fail(WAFER_HIP_E_UNSUPPORTED, "convert: opcode " + std::to_string(opcode) + " is not a served route");
+}
+
 extern "C" int wafer_hip_convert(wafer_hip_context *ctx, uint32_t opcode, uint32_t rounding,
                                  const void *src, void *dst, uint64_t count) {
   WAFER_CHECK_CTX(ctx);

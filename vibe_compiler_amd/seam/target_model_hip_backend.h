@@ -1,0 +1,236 @@
+// target_model_hip_backend.h -- the C++ host side of the gfx950 backend: the
+// reference simulator's two numeric backend seams, implemented over the C
+// ABI of libwafer_hip.so.
+//
+// The types mirror the reference's seam one for one (names, fields and
+// meaning), restated without LLVM so they build with the system compiler:
+//   TargetModelNumericTensor / Operands / *Request / *Result / *Evidence
+//     include/Wafer/Simulator/Kernel/TargetModelKernel.h:108-200
+//   TargetModelKernelErrorCode                      TargetModelKernel.h:21-32
+//   FormalGemmOperation, FormalElementwiseOperation, FormalConvertOperation,
+//   FormalReduceOperation      include/Wafer/Simulator/Reference/FormalOperations.h:21-113
+//   PhysicalTensorDescriptor   include/Wafer/Target/PhysicalTensor/PhysicalTensorDescriptor.h:20-55
+//   FormalNumericWorkBudget    include/Wafer/Simulator/Reference/FormalTensorNumeric.h:22-47
+// llvm::Expected<T> becomes Expected<T> below (a value or a typed error with
+// a detail string); llvm's ArrayRef/StringRef become std::vector/std::string.
+//
+// HipTargetModelBackend implements both interfaces:
+//   TargetModelOneDNNBackend::tryExecute(const TargetModelGemmRequest &)
+//   TargetModelManagedReferenceBackend::execute(Convert / Elementwise / Reduce, budget)
+// with the reference's contract: a result is complete and checked or the
+// call fails with no partial output; destination bytes not owned by logical
+// elements keep the destination template's bytes; evidence records one
+// matmul invocation per GEMM and one scalar evaluation per element.
+#pragma once
+
+#include <cstdint>
+#include <memory>
+#include <optional>
+#include <string>
+#include <utility>
+#include <vector>
+
+struct wafer_hip_context;
+
+namespace wafer::model {
+
+// ---- formats, layouts, operation codes (the reference's numbering) ----------
+enum class LogicalFormat : uint8_t { I8 = 0, I16 = 1, F16 = 2, BF16 = 3, I32 = 4, F32 = 5, TF32 = 6, Bool = 7 };
+enum class PhysicalTensorLayout : uint8_t { Tensor = 0, NTensor = 1, Cx = 2, NCx = 3 };
+enum class TargetGemmOrientation : uint8_t { Normal = 0, Transpose = 1 };
+// TargetElementwiseOperation (include/Wafer/Target/TargetOperation.h:58-93)
+enum class TargetElementwiseOperation : uint8_t {
+  Abs, Recip, Square, Sqrt, Rsqrt, Neg, Max, Min, Add, Sub, Mul,
+  Eq = 12, Ne, Ge, Gt, Le, Lt, LogicNot, LogicAnd, LogicOr, LogicXor,
+  Log2, Ln, Pow2, Exp, ExpLp, Sin, Cos, Tanh, Sigmoid, Relu, SatRelu, LeakyRelu, Softplus,
+};
+// TargetOperation.h:102-113 (Avg is not a managed-reference operation)
+enum class TargetReduceOperation : uint8_t { Sum, Max, Min, Avg };
+enum class TargetReduceDimension : uint8_t {
+  Trailing0 = 0, Trailing1 = 1, Trailing2 = 2, Trailing3 = 3, Trailing2And1 = 4, Trailing2And1And0 = 5,
+};
+
+// ---- errors --------------------------------------------------------------
+enum class TargetModelKernelErrorCode : uint8_t {
+  InvalidCommandField,
+  WorkBudgetExceeded,
+  UnsupportedCommand,
+  MemoryReadFailure,
+  FormalNumericFailure,
+  PhysicalCodecFailure,
+  ManagedReferenceBackendUnavailable,
+  ManagedReferenceBackendFailure,
+  OneDNNBackendUnavailable,
+  OneDNNBackendFailure,
+};
+const char *stringifyTargetModelKernelErrorCode(TargetModelKernelErrorCode code);
+
+struct TargetModelKernelError {
+  TargetModelKernelErrorCode code;
+  std::string detail;
+};
+
+// A value or an error, the role llvm::Expected plays in the reference.
+template <typename T> class Expected {
+public:
+  Expected(T value) : value_(std::move(value)) {}
+  Expected(TargetModelKernelError error) : error_(std::move(error)) {}
+  explicit operator bool() const { return value_.has_value(); }
+  T &operator*() { return *value_; }
+  const T &operator*() const { return *value_; }
+  T *operator->() { return &*value_; }
+  const TargetModelKernelError &error() const { return *error_; }
+
+private:
+  std::optional<T> value_;
+  std::optional<TargetModelKernelError> error_;
+};
+
+// ---- descriptors, tensors, budgets ------------------------------------------
+class PhysicalTensorDescriptor {
+public:
+  // Validates the format/layout pair and the shape (every extent >= 1,
+  // rank 1..8; Cx rank 2, NCx rank >= 3 as the reference's geometry needs).
+  static Expected<PhysicalTensorDescriptor> create(LogicalFormat format, PhysicalTensorLayout layout,
+                                                   std::vector<uint64_t> shape);
+  LogicalFormat getFormat() const { return format; }
+  PhysicalTensorLayout getLayout() const { return layout; }
+  const std::vector<uint64_t> &getShape() const { return shape; }
+  uint64_t getElementCount() const { return elementCount; }
+  // storage bytes of the physical image (wafer_hip_physical_bytes)
+  Expected<uint64_t> getStorageBytes() const;
+  friend bool operator==(const PhysicalTensorDescriptor &a, const PhysicalTensorDescriptor &b) {
+    return a.format == b.format && a.layout == b.layout && a.shape == b.shape;
+  }
+
+private:
+  PhysicalTensorDescriptor(LogicalFormat f, PhysicalTensorLayout l, std::vector<uint64_t> s, uint64_t n)
+      : format(f), layout(l), shape(std::move(s)), elementCount(n) {}
+  LogicalFormat format;
+  PhysicalTensorLayout layout;
+  std::vector<uint64_t> shape;
+  uint64_t elementCount;
+};
+
+class FormalNumericWorkBudget {
+public:
+  static constexpr FormalNumericWorkBudget create(uint64_t maximumScalarEvaluations,
+                                                  uint64_t maximumFusedMultiplyAdds) {
+    return FormalNumericWorkBudget(maximumScalarEvaluations, maximumFusedMultiplyAdds);
+  }
+  uint64_t getMaximumScalarEvaluations() const { return maximumScalarEvaluations; }
+  uint64_t getMaximumFusedMultiplyAdds() const { return maximumFusedMultiplyAdds; }
+
+private:
+  constexpr FormalNumericWorkBudget(uint64_t s, uint64_t f) : maximumScalarEvaluations(s), maximumFusedMultiplyAdds(f) {}
+  uint64_t maximumScalarEvaluations;
+  uint64_t maximumFusedMultiplyAdds;
+};
+
+struct TargetModelNumericTensor {
+  PhysicalTensorDescriptor key;
+  std::vector<uint8_t> storage;
+};
+
+struct TargetModelNumericOperands {
+  std::vector<TargetModelNumericTensor> inputs;
+  TargetModelNumericTensor destinationTemplate;
+};
+
+// ---- operations and requests ------------------------------------------------
+struct FormalGemmOperation {
+  PhysicalTensorDescriptor lhs, rhs, destination;
+  uint16_t m, k, n, batchCount;
+  TargetGemmOrientation lhsOrientation = TargetGemmOrientation::Normal;
+  TargetGemmOrientation rhsOrientation = TargetGemmOrientation::Normal;
+  std::optional<PhysicalTensorDescriptor> psum;
+};
+struct FormalElementwiseOperation {
+  TargetElementwiseOperation operation;
+  std::vector<PhysicalTensorDescriptor> inputs;
+  PhysicalTensorDescriptor destination;
+};
+struct FormalConvertOperation {
+  uint16_t opcode;  // a route of the Data_Format route table (TargetFormat.cpp:164-196)
+  PhysicalTensorDescriptor source, destination;
+};
+struct FormalReduceOperation {
+  TargetReduceOperation operation;
+  PhysicalTensorDescriptor input, destination;
+  TargetReduceDimension dimension;
+};
+
+struct TargetModelGemmRequest { FormalGemmOperation operation; TargetModelNumericOperands tensors; };
+struct TargetModelElementwiseRequest { FormalElementwiseOperation operation; TargetModelNumericOperands tensors; };
+struct TargetModelConvertRequest { FormalConvertOperation operation; TargetModelNumericOperands tensors; };
+struct TargetModelReduceRequest { FormalReduceOperation operation; TargetModelNumericOperands tensors; };
+
+// ---- results and evidence ---------------------------------------------------
+enum class TargetModelOneDNNEvidenceKind : uint8_t { None, ExactQualificationRecord, ManagedReferenceEnvironment };
+
+struct TargetModelOneDNNDispatchEvidence {
+  uint64_t matmulInvocations = 0;
+  uint64_t reorderInvocations = 0;
+  uint64_t formalFusedMultiplyAdds = 0;
+  TargetModelOneDNNEvidenceKind evidenceKind = TargetModelOneDNNEvidenceKind::None;
+  std::string evidenceDigest;
+  std::string implementation;
+};
+struct TargetModelOneDNNResult {
+  TargetModelNumericTensor destination;
+  TargetModelOneDNNDispatchEvidence evidence;
+};
+struct TargetModelManagedReferenceEvidence {
+  uint64_t scalarEvaluations = 0;
+  std::string environmentDigest;
+  std::string implementation;
+};
+struct TargetModelManagedReferenceResult {
+  TargetModelNumericTensor destination;
+  TargetModelManagedReferenceEvidence evidence;
+};
+
+// ---- the two seams ------------------------------------------------------------
+class TargetModelOneDNNBackend {
+public:
+  virtual ~TargetModelOneDNNBackend() = default;
+  // An empty optional means "not handled": the caller falls back to formal.
+  virtual Expected<std::optional<TargetModelOneDNNResult>> tryExecute(const TargetModelGemmRequest &request) const = 0;
+};
+
+class TargetModelManagedReferenceBackend {
+public:
+  virtual ~TargetModelManagedReferenceBackend() = default;
+  virtual Expected<TargetModelManagedReferenceResult> execute(const TargetModelConvertRequest &request,
+                                                              FormalNumericWorkBudget scalarBudget) const = 0;
+  virtual Expected<TargetModelManagedReferenceResult> execute(const TargetModelElementwiseRequest &request,
+                                                              FormalNumericWorkBudget scalarBudget) const = 0;
+  virtual Expected<TargetModelManagedReferenceResult> execute(const TargetModelReduceRequest &request,
+                                                              FormalNumericWorkBudget scalarBudget) const = 0;
+};
+
+// ---- the gfx950 implementation ----------------------------------------------------
+class HipTargetModelBackend final : public TargetModelOneDNNBackend, public TargetModelManagedReferenceBackend {
+public:
+  // One per run, like the reference's backend objects
+  // (tools/wafer-compile/wafer-compile.cpp:477-506).
+  static Expected<std::unique_ptr<HipTargetModelBackend>> create(int device);
+  ~HipTargetModelBackend() override;
+
+  // GEMM on the formal-order kernel: bit-identical to the formal lane, so a
+  // request is always handled (never the empty optional) unless it is
+  // outside the formal operation's own domain, which is reported as an error.
+  Expected<std::optional<TargetModelOneDNNResult>> tryExecute(const TargetModelGemmRequest &request) const override;
+  Expected<TargetModelManagedReferenceResult> execute(const TargetModelConvertRequest &request,
+                                                      FormalNumericWorkBudget scalarBudget) const override;
+  Expected<TargetModelManagedReferenceResult> execute(const TargetModelElementwiseRequest &request,
+                                                      FormalNumericWorkBudget scalarBudget) const override;
+  Expected<TargetModelManagedReferenceResult> execute(const TargetModelReduceRequest &request,
+                                                      FormalNumericWorkBudget scalarBudget) const override;
+
+private:
+  explicit HipTargetModelBackend(wafer_hip_context *ctx) : ctx(ctx) {}
+  wafer_hip_context *ctx;
+};
+
+}  // namespace wafer::model
