@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the gfx950 numeric backend on BASELINE.json's headline metric.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fa,fd,i8,mlp,llama]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fa,fd,i8,mlp,llama,mv]
 
 One step = one launch of the hot path over one batch of synthetic, seeded
 input already resident in HBM.  The headline (`value`) is the FA prefill
@@ -260,6 +260,34 @@ def bench_llama(torch, hip, steps, warmup, with_cpu=True):
     return res
 
 
+def bench_mv(torch, hip, steps, warmup):
+    """Movement commands: a strided tile gather (RDMA shape: 131072 rows of
+    4 KiB out of an 8 KiB-pitch matrix into a dense tile, 512 MiB payload,
+    working set above the 256 MB last-level cache) and
+    a 2-byte-element transpose of a 16384 x 16384 bf16 matrix (gather-scatter,
+    512 MiB payload).  Algorithmic bytes = payload read + payload written."""
+    rows, pitch, inner = 131072, 8192, 4096
+    src = torch.randint(0, 256, (rows * pitch,), dtype=torch.uint8, device="cuda")
+    tile = torch.empty(rows * inner, dtype=torch.uint8, device="cuda")
+    ms = timed(torch, lambda: hip.strided_copy(src, tile, inner, [pitch, 0, 0], [rows, 1, 1], [inner, 0, 0],
+                                               [rows, 1, 1]), steps, warmup)
+    gbs = 2 * rows * inner / (ms * 1e-3) / 1e9
+    n = 16384
+    x = torch.randint(-32768, 32767, (n, n), dtype=torch.int16, device="cuda")
+    t = torch.empty_like(x)
+    ms_t = timed(torch, lambda: hip.strided_copy(x, t, 2, [2, 2 * n, 0], [n, n, 1], [2 * n, 2, 0], [n, n, 1]),
+                 steps, warmup)
+    gbs_t = 2 * n * n * 2 / (ms_t * 1e-3) / 1e9
+    return {
+        "workload": "strided tile gather 131072 x 4 KiB segments at 8 KiB pitch -> dense (512 MiB payload)",
+        "metric": "GB/s", "ms": ms, "value": gbs, "unit": "GB/s",
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK["hbm"], "unit": "GB/s",
+                     "frac": gbs / PEAK["hbm"], "traffic": None},
+        "transpose": {"workload": "bf16 16384 x 16384 transpose, 2-byte segments (512 MiB payload)", "ms": ms_t,
+                      "value": gbs_t, "unit": "GB/s", "frac": gbs_t / PEAK["hbm"]},
+    }
+
+
 def bench_copy(torch, steps, warmup):
     """A plain device copy of known size: the calibration kernel for the
     rocprofv3 FETCH_SIZE / WRITE_SIZE counters (reads and writes COPY_BYTES)."""
@@ -275,7 +303,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="fa,fd,i8,mlp,llama", help="comma list of fa, fd, i8, mlp, llama, copy")
+    ap.add_argument("--only", default="fa,fd,i8,mlp,llama,mv", help="comma list of fa, fd, i8, mlp, llama, mv, copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -304,6 +332,8 @@ def main() -> int:
         secondary.append(dict(name="mlp_fp32", **bench_mlp(torch, hip, B, args.steps, args.warmup, with_cpu)))
     if "llama" in only:
         secondary.append(dict(name="llama_layer", **bench_llama(torch, hip, args.steps, args.warmup, with_cpu)))
+    if "mv" in only:
+        secondary.append(dict(name="movement", **bench_mv(torch, hip, args.steps, args.warmup)))
     if "copy" in only:
         secondary.append(dict(name="copy", **bench_copy(torch, args.steps, args.warmup)))
     hip.close()

@@ -107,6 +107,14 @@ int oracle_rope(int format, const void *x, void *y, int64_t tokens,
 int oracle_bias_add(int format, const void *x, const float *bias, void *y,
                     int64_t rows, int64_t cols);
 
+/* ---- movement and fill commands ---------------------------------------- */
+int oracle_strided_copy(const uint8_t *src, uint8_t *dst, uint32_t inner_bytes,
+                        const uint32_t src_strides[3], const uint32_t src_iterations[3],
+                        const uint32_t dst_strides[3], const uint32_t dst_iterations[3]);
+int oracle_memset(uint8_t *dst, int format, uint32_t value, int64_t count);
+int oracle_bit2fp(const uint8_t *bits, void *dst, int format, int64_t count);
+int oracle_mask_move(const void *src, const void *mask, void *dst, int format, int64_t count);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,7 @@ EXPORTS = (
     "wafer_hip_rmsnorm", "wafer_hip_softmax", "wafer_hip_silu_mul", "wafer_hip_gelu_tanh",
     "wafer_hip_rope", "wafer_hip_bias_add", "wafer_hip_head_permute", "wafer_hip_buffer_alloc",
     "wafer_hip_buffer_free", "wafer_hip_copy_to_device", "wafer_hip_copy_to_host", "wafer_hip_convert_route",
+    "wafer_hip_strided_copy", "wafer_hip_memset", "wafer_hip_bit2fp", "wafer_hip_mask_move",
 )
 
 
@@ -104,6 +105,11 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wafer_hip_copy_to_device.argtypes = [vp, vp, vp, u64]
     L.wafer_hip_copy_to_host.argtypes = [vp, vp, vp, u64]
     L.wafer_hip_convert_route.argtypes = [u32, ctypes.POINTER(u32), ctypes.POINTER(u32)]
+    u32p = ctypes.POINTER(u32)
+    L.wafer_hip_strided_copy.argtypes = [vp, vp, vp, u64, u32, u32p, u32p, u32p, u32p]
+    L.wafer_hip_memset.argtypes = [vp, vp, u32, u32, u64]
+    L.wafer_hip_bit2fp.argtypes = [vp, vp, vp, u32, u64]
+    L.wafer_hip_mask_move.argtypes = [vp, vp, vp, vp, u32, u64]
 
 
 def _check(status: int) -> None:
@@ -259,6 +265,41 @@ class Context:
         dp = ctypes.c_void_p(_p(dst).value + dst_offset * es)
         _check(self._L.wafer_hip_head_permute(self._bind(), fmt, sp, dp, tokens, heads, head_dim,
                                               token_stride, direction))
+
+    # ---- movement and fill commands (byte tensors are any contiguous dtype)
+    def strided_copy(self, src, dst, inner_bytes, src_strides, src_iterations, dst_strides, dst_iterations,
+                     src_offset=0, dst_offset=0):
+        """Move segments * inner_bytes bytes from the source layout (at byte
+        src_offset of `src`) to the destination layout (at byte dst_offset of
+        `dst`); `src` and `dst` may be the same tensor.  Both layouts must lie
+        inside their tensors."""
+        u3 = lambda v: (ctypes.c_uint32 * 3)(*[int(x) for x in v])
+        nseg = int(src_iterations[0]) * int(src_iterations[1]) * int(src_iterations[2])
+        span = lambda st, it: inner_bytes + sum((int(i) - 1) * int(s) for s, i in zip(st, it))
+        if src_offset + span(src_strides, src_iterations) > src.numel() * src.element_size() or \
+                dst_offset + span(dst_strides, dst_iterations) > dst.numel() * dst.element_size():
+            raise ValueError("strided_copy: a layout reaches past its tensor")
+        sp = ctypes.c_void_p(_p(src).value + src_offset)
+        dp = ctypes.c_void_p(_p(dst).value + dst_offset)
+        _check(self._L.wafer_hip_strided_copy(self._bind(), sp, dp,
+                                              nseg * inner_bytes, inner_bytes, u3(src_strides), u3(src_iterations),
+                                              u3(dst_strides), u3(dst_iterations)))
+
+    def memset(self, dst, fmt, value, count):
+        bits = 1 if fmt == BOOL else {0: 8, 8: 8, 1: 16, 9: 16, 2: 16, 3: 16, 4: 32, 10: 32, 5: 32, 6: 32}.get(fmt, 64)
+        if (count * bits + 7) // 8 > dst.numel() * dst.element_size():
+            raise ValueError("memset: count exceeds the tensor")
+        _check(self._L.wafer_hip_memset(self._bind(), _p(dst), fmt, value, count))
+
+    def bit2fp(self, bits, dst, fmt, count):
+        if (count + 7) // 8 > bits.numel() * bits.element_size() or count > dst.numel():
+            raise ValueError("bit2fp: count exceeds a tensor")
+        _check(self._L.wafer_hip_bit2fp(self._bind(), _p(bits), _p(dst), fmt, count))
+
+    def mask_move(self, src, mask, dst, fmt):
+        if not (src.numel() == mask.numel() == dst.numel()):
+            raise ValueError("mask_move: element counts differ")
+        _check(self._L.wafer_hip_mask_move(self._bind(), _p(src), _p(mask), _p(dst), fmt, dst.numel()))
 
     def bias_add(self, x, bias, y, fmt=F32):
         cols = x.shape[-1]
