@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the gfx950 numeric backend on BASELINE.json's headline metric.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fa,fd,i8,mlp,llama,mv]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fa,fd,i8,mlp,llama,mv,cmp]
 
 One step = one launch of the hot path over one batch of synthetic, seeded
 input already resident in HBM.  The headline (`value`) is the FA prefill
@@ -288,6 +288,45 @@ def bench_mv(torch, hip, steps, warmup):
     }
 
 
+def bench_cmp(torch, hip, steps, warmup):
+    """Program-boundary comparator on a 256M-element bf16 pair (512 MiB each,
+    above the 256 MB last-level cache): the output gate (one statistics pass)
+    and the full error statistics (that pass plus the radix-selection passes
+    for the p99/p999 quantiles).  Both entries end with a host
+    synchronisation, so they are timed per call, host time included."""
+    n = 256 << 20
+    gen = torch.Generator(device="cuda").manual_seed(SEED)
+    x = torch.randn(n, device="cuda", generator=gen)
+    y = (x * (1 + 1e-3 * torch.randn(n, device="cuda", generator=gen))).to(torch.bfloat16)
+    x = x.to(torch.bfloat16)
+    a, e = (10, y.view(torch.uint8), (n,)), (10, x.view(torch.uint8), (n,))
+
+    def per_call(fn):
+        for _ in range(max(1, warmup // 5)):
+            fn()
+        torch.cuda.synchronize()
+        k = max(1, steps // 5)
+        t0 = time.perf_counter()
+        for _ in range(k):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / k
+
+    ms_gate = per_call(lambda: hip.compare_expected(a, e, 0.008, 0.006, (0.9999, 0.01)))
+    ms_elem = per_call(lambda: hip.compare_expected(a, e, 0.008, 0.006))
+    ms_stats = per_call(lambda: hip.compare_statistics(a, e, 0.008, 0.006))
+    gbs = 2 * n * 2 / (ms_gate * 1e-3) / 1e9
+    return {
+        "workload": "comparator gate (similarity policy) on a bf16 pair of 268,435,456 elements",
+        "metric": "GB/s", "ms": ms_gate, "value": gbs, "unit": "GB/s",
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK["hbm"], "unit": "GB/s",
+                     "frac": gbs / PEAK["hbm"], "traffic": None},
+        "elementwise_gate": {"ms": ms_elem, "value": 2 * n * 2 / (ms_elem * 1e-3) / 1e9, "unit": "GB/s"},
+        "statistics": {"workload": "full statistics incl. nearest-rank p99/p999 of |error| and ULP",
+                       "ms": ms_stats, "elements_per_s": n / (ms_stats * 1e-3)},
+    }
+
+
 def bench_copy(torch, steps, warmup):
     """A plain device copy of known size: the calibration kernel for the
     rocprofv3 FETCH_SIZE / WRITE_SIZE counters (reads and writes COPY_BYTES)."""
@@ -303,7 +342,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="fa,fd,i8,mlp,llama,mv", help="comma list of fa, fd, i8, mlp, llama, mv, copy")
+    ap.add_argument("--only", default="fa,fd,i8,mlp,llama,mv,cmp", help="comma list of fa, fd, i8, mlp, llama, mv, cmp, copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -334,6 +373,8 @@ def main() -> int:
         secondary.append(dict(name="llama_layer", **bench_llama(torch, hip, args.steps, args.warmup, with_cpu)))
     if "mv" in only:
         secondary.append(dict(name="movement", **bench_mv(torch, hip, args.steps, args.warmup)))
+    if "cmp" in only:
+        secondary.append(dict(name="comparator", **bench_cmp(torch, hip, args.steps, args.warmup)))
     if "copy" in only:
         secondary.append(dict(name="copy", **bench_copy(torch, args.steps, args.warmup)))
     hip.close()

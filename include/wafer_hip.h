@@ -292,6 +292,102 @@ int wafer_hip_mask_move(wafer_hip_context *ctx, const void *src,
                         const void *mask, void *dst, uint32_t format,
                         uint64_t element_count);
 
+/* ---- program-boundary comparison (output gate and error statistics) -------
+ * compareProgramTensorExpectedOutput and computeProgramTensorComparisonStatistics
+ * (lib/Wafer/Simulator/Invocation/ProgramTensorComparison.cpp:267-497;
+ * include/Wafer/Simulator/Invocation/ProgramTensorComparison.h:20-71) over
+ * device-resident compact row-major tensors.  The entries return WAFER_HIP_OK
+ * once the comparison ran; *verdict then holds WAFER_CMP_ACCEPTED or the
+ * reference's ProgramTensorComparisonErrorCode + 1, and `detail` (when given)
+ * the reference's diagnostic text.  Negative statuses are reserved for misuse
+ * of the ABI (null pointers, a byte count that disagrees with dtype and shape)
+ * and HIP failures. */
+
+/* ProgramElementType (include/Wafer/Frontend/ProgramElementType.h:17-32). */
+enum {
+  WAFER_DT_BOOL = 0, WAFER_DT_I8 = 1, WAFER_DT_U8 = 2, WAFER_DT_I16 = 3,
+  WAFER_DT_U16 = 4, WAFER_DT_I32 = 5, WAFER_DT_U32 = 6, WAFER_DT_I64 = 7,
+  WAFER_DT_U64 = 8, WAFER_DT_F16 = 9, WAFER_DT_BF16 = 10, WAFER_DT_F32 = 11,
+  WAFER_DT_TF32 = 12, WAFER_DT_F64 = 13
+};
+
+/* ProgramTensorComparisonErrorCode + 1 (ProgramTensorComparison.h:21-32). */
+enum {
+  WAFER_CMP_ACCEPTED = 0,
+  WAFER_CMP_INVALID_TOLERANCE = 1,
+  WAFER_CMP_DTYPE_MISMATCH = 2,
+  WAFER_CMP_SHAPE_MISMATCH = 3,
+  WAFER_CMP_BYTE_SIZE_MISMATCH = 4,
+  WAFER_CMP_UNSUPPORTED_FLOATING_DTYPE = 5,
+  WAFER_CMP_UNSUPPORTED_STATISTICS_DTYPE = 6,
+  WAFER_CMP_ACTUAL_NONFINITE = 7,
+  WAFER_CMP_EXPECTED_NONFINITE = 8,
+  WAFER_CMP_NUMERIC_MISMATCH = 9,
+  WAFER_CMP_RAW_MISMATCH = 10
+};
+
+/* A ProgramTensor (dtype, shape, compact bytes) whose bytes are in device
+ * memory; `bytes` must equal the element size times the shape product. */
+typedef struct wafer_hip_program_tensor {
+  uint32_t dtype;
+  uint32_t rank;
+  const int64_t *shape;
+  const void *data;
+  uint64_t bytes;
+} wafer_hip_program_tensor;
+
+/* ProgramTensorComparisonPolicy (ProgramTensorComparison.h:35-47). */
+typedef struct wafer_hip_comparison_policy {
+  double atol;
+  double rtol;
+  uint32_t has_similarity;
+  double minimum_cosine;
+  double maximum_relative_l2;
+} wafer_hip_comparison_policy;
+
+/* ProgramTensorComparisonStatistics (ProgramTensorComparison.h:55-71). */
+typedef struct wafer_hip_comparison_statistics {
+  uint64_t element_count;
+  uint64_t exact_element_count;
+  double exact_fraction;
+  double mean_absolute_error;
+  double p99_absolute_error;
+  double p999_absolute_error;
+  double maximum_absolute_error;
+  uint64_t elementwise_mismatch_count;
+  double cosine_similarity;
+  double relative_l2_error;
+  double mean_ulp_distance;
+  uint64_t p99_ulp_distance;
+  uint64_t p999_ulp_distance;
+  uint64_t maximum_ulp_distance;
+} wafer_hip_comparison_statistics;
+
+/* The output gate: F16 / BF16 / F32 elementwise (|a - e| <= atol + rtol |e|)
+ * or, with has_similarity, cosine >= minimum and relative L2 <= maximum over
+ * the whole tensor; other floating dtypes fail closed; integer and Bool
+ * storage compare byte for byte.  Replaces compareProgramTensorExpectedOutput
+ * (ProgramTensorComparison.cpp:267-387). */
+int wafer_hip_compare_expected(wafer_hip_context *ctx,
+                               const wafer_hip_program_tensor *actual,
+                               const wafer_hip_program_tensor *expected,
+                               const wafer_hip_comparison_policy *policy,
+                               uint32_t *verdict, char *detail,
+                               size_t detail_bytes);
+/* The error distribution of a finite F16 / BF16 / F32 pair: nearest-rank
+ * quantiles over all elements, sign-aware ULP distances (equal signed zeros
+ * at distance 0).  `policy` (may be NULL: atol = rtol = 0) sets only the
+ * diagnostic mismatch count.  Replaces computeProgramTensorComparisonStatistics
+ * (ProgramTensorComparison.cpp:389-497).  The ULP-distance sum is exact below
+ * 2^64 (any F16/BF16 tensor; F32 tensors below 2^32 elements). */
+int wafer_hip_compare_statistics(wafer_hip_context *ctx,
+                                 const wafer_hip_program_tensor *actual,
+                                 const wafer_hip_program_tensor *expected,
+                                 const wafer_hip_comparison_policy *policy,
+                                 uint32_t *verdict,
+                                 wafer_hip_comparison_statistics *out,
+                                 char *detail, size_t detail_bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -64,6 +64,10 @@ def _declare(L: ctypes.CDLL) -> None:
     L.oracle_memset.argtypes = [vp, i32, ctypes.c_uint32, i64]
     L.oracle_bit2fp.argtypes = [vp, vp, i32, i64]
     L.oracle_mask_move.argtypes = [vp, vp, vp, i32, i64]
+    d = ctypes.c_double
+    L.oracle_compare_floats.argtypes = [i32, vp, vp, i64, d, d, i32, d, d, ctypes.POINTER(d), ctypes.POINTER(d),
+                                        ctypes.POINTER(i64)]
+    L.oracle_compare_statistics.argtypes = [i32, vp, vp, i64, d, d, ctypes.POINTER(CmpStats), ctypes.POINTER(i64)]
     L.oracle_convert.argtypes = [i32, i32, vp, vp, i64]
     L.oracle_reduce.argtypes = [i32, i32, i32, vp, i32, vp, vp]
     L.oracle_attention_prefill.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, i32, i32, i32]
@@ -337,3 +341,98 @@ def mask_move(src, mask, dst, fmt):
     out = np.array(dst, copy=True)
     st = lib().oracle_mask_move(_p(src), _p(mask), _p(out), fmt, out.size)
     return st, out
+
+
+# ---- program-boundary comparison ---------------------------------------------
+# ProgramElementType (include/Wafer/Frontend/ProgramElementType.h:17-32)
+DT = dict(bool=0, i8=1, u8=2, i16=3, u16=4, i32=5, u32=6, i64=7, u64=8, f16=9, bf16=10, f32=11, tf32=12, f64=13)
+DT_NAME = {v: k for k, v in DT.items()}
+DT_BYTES = {0: 1, 1: 1, 2: 1, 3: 2, 4: 2, 5: 4, 6: 4, 7: 8, 8: 8, 9: 2, 10: 2, 11: 4, 12: 4, 13: 8}
+# ProgramTensorComparisonErrorCode + 1 (0: accepted)
+CMP = dict(accepted=0, invalid_tolerance=1, dtype_mismatch=2, shape_mismatch=3, byte_size_mismatch=4,
+           unsupported_floating_dtype=5, unsupported_statistics_dtype=6, actual_nonfinite=7,
+           expected_nonfinite=8, numeric_mismatch=9, raw_mismatch=10)
+
+
+class CmpStats(ctypes.Structure):
+    _fields_ = [("element_count", ctypes.c_uint64), ("exact_element_count", ctypes.c_uint64),
+                ("exact_fraction", ctypes.c_double), ("mean_absolute_error", ctypes.c_double),
+                ("p99_absolute_error", ctypes.c_double), ("p999_absolute_error", ctypes.c_double),
+                ("maximum_absolute_error", ctypes.c_double), ("elementwise_mismatch_count", ctypes.c_uint64),
+                ("cosine_similarity", ctypes.c_double), ("relative_l2_error", ctypes.c_double),
+                ("mean_ulp_distance", ctypes.c_double), ("p99_ulp_distance", ctypes.c_uint64),
+                ("p999_ulp_distance", ctypes.c_uint64), ("maximum_ulp_distance", ctypes.c_uint64)]
+
+
+def _policy_ok(atol, rtol, similarity):
+    """validateProgramTensorComparisonPolicy (ProgramTensorComparison.cpp:499-516)."""
+    import math
+    if not (math.isfinite(atol) and math.isfinite(rtol)) or atol < 0 or rtol < 0:
+        return False
+    if similarity is not None:
+        c, r = similarity
+        if not math.isfinite(c) or c < 0 or c > 1 or not math.isfinite(r) or r < 0:
+            return False
+    return True
+
+
+def _metadata(actual, expected):
+    """(dtype, shape, bytes) checks in the reference's order; tensors are
+    (dtype, shape, uint8 array)."""
+    if actual[0] != expected[0]:
+        return CMP["dtype_mismatch"]
+    if tuple(actual[1]) != tuple(expected[1]):
+        return CMP["shape_mismatch"]
+    if actual[2].size != expected[2].size:
+        return CMP["byte_size_mismatch"]
+    return None
+
+
+def compare_expected(actual, expected, atol, rtol, similarity=None):
+    """compareProgramTensorExpectedOutput (ProgramTensorComparison.cpp:267-387).
+    Returns (verdict, info): info is the raw first differing byte for a raw
+    mismatch, else the oracle's [scan end, mismatches, first, max_abs, max_ratio]
+    element indices plus cosine and relative L2."""
+    if not _policy_ok(atol, rtol, similarity):
+        return CMP["invalid_tolerance"], None
+    m = _metadata(actual, expected)
+    if m is not None:
+        return m, None
+    dt = actual[0]
+    if dt in (DT["tf32"], DT["f64"]):
+        return CMP["unsupported_floating_dtype"], None
+    a = np.ascontiguousarray(actual[2], dtype=np.uint8)
+    e = np.ascontiguousarray(expected[2], dtype=np.uint8)
+    if dt not in (DT["f16"], DT["bf16"], DT["f32"]):
+        diff = np.nonzero(a != e)[0]
+        return (CMP["raw_mismatch"], int(diff[0])) if diff.size else (CMP["accepted"], None)
+    n = a.size // DT_BYTES[dt]
+    info = (ctypes.c_int64 * 5)()
+    c, r = ctypes.c_double(), ctypes.c_double()
+    sim = similarity or (0.0, 0.0)
+    v = lib().oracle_compare_floats(dt, _p(a), _p(e), n, atol, rtol, int(similarity is not None), sim[0], sim[1],
+                                    ctypes.byref(c), ctypes.byref(r), info)
+    return v, dict(scan_end=info[0], mismatches=info[1], first=info[2], max_abs=info[3], max_ratio=info[4],
+                   cosine=c.value, relative_l2=r.value)
+
+
+def compare_statistics(actual, expected, atol=0.0, rtol=0.0):
+    """computeProgramTensorComparisonStatistics (ProgramTensorComparison.cpp:389-497).
+    Returns (verdict, stats dict or None)."""
+    if not _policy_ok(atol, rtol, None):
+        return CMP["invalid_tolerance"], None
+    m = _metadata(actual, expected)
+    if m is not None:
+        return m, None
+    dt = actual[0]
+    if dt not in (DT["f16"], DT["bf16"], DT["f32"]):
+        return CMP["unsupported_statistics_dtype"], None
+    a = np.ascontiguousarray(actual[2], dtype=np.uint8)
+    e = np.ascontiguousarray(expected[2], dtype=np.uint8)
+    out = CmpStats()
+    bad = ctypes.c_int64()
+    v = lib().oracle_compare_statistics(dt, _p(a), _p(e), a.size // DT_BYTES[dt], atol, rtol, ctypes.byref(out),
+                                        ctypes.byref(bad))
+    if v != 0:
+        return v, None
+    return 0, {k: getattr(out, k) for k, _ in CmpStats._fields_}

@@ -1091,3 +1091,167 @@ int oracle_mask_move(const void *src, const void *mask, void *dst, int format, i
   }
   return 0;
 }
+
+/* ---- program-boundary comparison --------------------------------------------
+ * compareProgramTensorExpectedOutput / computeProgramTensorComparisonStatistics
+ * (lib/Wafer/Simulator/Invocation/ProgramTensorComparison.cpp:267-497) for the
+ * floating formats, element by element in order with long double similarity
+ * accumulators (TensorSimilarity, :23-51), decodeBinaryFloat (:87-112),
+ * getUlpOrderKey / getUlpDistance (:147-162) and nearest-rank quantiles over
+ * sorted errors (:164-171).  The metadata checks (dtype, shape, bytes) are
+ * restated in oracle.py. */
+static int cmp_decode(int dtype, const void *p, int64_t i, double *v, uint32_t *bits) {
+  unsigned eb, fb;
+  int bias;
+  uint32_t b;
+  if (dtype == 11) {
+    b = ((const uint32_t *)p)[i];
+    eb = 8; fb = 23; bias = 127;
+  } else {
+    b = ((const uint16_t *)p)[i];
+    if (dtype == 9) { eb = 5; fb = 10; bias = 15; }
+    else { eb = 8; fb = 7; bias = 127; }
+  }
+  *bits = b;
+  const uint32_t fmask = (1u << fb) - 1u, emask = (1u << eb) - 1u;
+  const uint32_t frac = b & fmask, ex = (b >> fb) & emask;
+  const int neg = (b >> (fb + eb)) & 1u;
+  if (ex == emask) return 0;
+  double value;
+  if (ex == 0) value = ldexp((double)frac, 1 - bias - (int)fb);
+  else value = ldexp((double)((1u << fb) | frac), (int)ex - bias - (int)fb);
+  *v = neg ? -value : value;
+  return 1;
+}
+
+static uint64_t cmp_order_key(uint32_t bits, unsigned width) {
+  const uint64_t sign = (uint64_t)1 << (width - 1);
+  const uint64_t mag = (uint64_t)bits & (sign - 1);
+  return ((uint64_t)bits & sign) ? sign - mag : sign + mag;
+}
+
+static uint64_t cmp_ulp(int dtype, uint32_t ab, uint32_t eb, double a, double e) {
+  if (a == e) return 0;
+  const unsigned w = dtype == 11 ? 32 : 16;
+  const uint64_t ka = cmp_order_key(ab, w), ke = cmp_order_key(eb, w);
+  return ka >= ke ? ka - ke : ke - ka;
+}
+
+typedef struct {
+  long double dot, aa, bb, ee;
+} cmp_sim;
+
+static void sim_add(cmp_sim *s, double a, double b) {
+  const long double x = a, y = b;
+  s->dot += x * y;
+  s->aa += x * x;
+  s->bb += y * y;
+  s->ee += (x - y) * (x - y);
+}
+static double sim_cosine(const cmp_sim *s) {
+  if (s->aa == 0.0L || s->bb == 0.0L) return s->aa == s->bb ? 1.0 : 0.0;
+  long double c = s->dot / sqrtl(s->aa) / sqrtl(s->bb);
+  if (c < -1.0L) c = -1.0L;
+  if (c > 1.0L) c = 1.0L;
+  return (double)c;
+}
+static double sim_rel_l2(const cmp_sim *s) {
+  if (s->bb == 0.0L) return s->ee == 0.0L ? 0.0 : INFINITY;
+  return (double)sqrtl(s->ee / s->bb);
+}
+
+int oracle_compare_floats(int dtype, const void *actual, const void *expected, int64_t n, double atol,
+                          double rtol, int has_similarity, double minimum_cosine, double maximum_relative_l2,
+                          double *cosine_out, double *relative_l2_out, int64_t *info) {
+  cmp_sim sim = {0, 0, 0, 0};
+  int64_t mism = 0, first = -1, maxabs_i = -1, maxratio_i = -1;
+  double maxabs = 0, maxratio_abs = 0, maxratio_tol = 0;
+  for (int i = 0; i < 5; ++i) info[i] = -1;
+  if (has_similarity && n == 0) return 6;
+  for (int64_t i = 0; i < n; ++i) {
+    double a, e;
+    uint32_t ab, eb;
+    if (!cmp_decode(dtype, actual, i, &a, &ab)) { info[0] = i; return 7; }
+    if (!cmp_decode(dtype, expected, i, &e, &eb)) { info[0] = i; return 8; }
+    const double ad = fabs(a - e);
+    if (has_similarity) sim_add(&sim, a, e);
+    const double tol = atol + rtol * fabs(e);
+    if (!isfinite(tol)) { info[0] = i; return 1; }
+    if (ad <= tol) continue;
+    ++mism;
+    if (first < 0) first = i;
+    if (maxabs_i < 0 || ad > maxabs) { maxabs = ad; maxabs_i = i; }
+    const double ratio = tol == 0.0 ? INFINITY : ad / tol;
+    const double cur = maxratio_i < 0 ? -1.0 : (maxratio_tol == 0.0 ? INFINITY : maxratio_abs / maxratio_tol);
+    if (maxratio_i < 0 || ratio > cur) { maxratio_i = i; maxratio_abs = ad; maxratio_tol = tol; }
+  }
+  info[1] = mism; info[2] = first; info[3] = maxabs_i; info[4] = maxratio_i;
+  *cosine_out = sim_cosine(&sim);
+  *relative_l2_out = sim_rel_l2(&sim);
+  if (has_similarity)
+    return (*cosine_out >= minimum_cosine && *relative_l2_out <= maximum_relative_l2) ? 0 : 9;
+  return mism ? 9 : 0;
+}
+
+static int cmp_f64(const void *a, const void *b) {
+  const double x = *(const double *)a, y = *(const double *)b;
+  return x < y ? -1 : x > y;
+}
+
+static int64_t nearest_rank(double q, int64_t n) {
+  int64_t r = (int64_t)ceil(q * (double)n);
+  if (r > n) r = n;
+  if (r < 1) r = 1;
+  return r;
+}
+
+int oracle_compare_statistics(int dtype, const void *actual, const void *expected, int64_t n, double atol,
+                              double rtol, oracle_cmp_stats *out, int64_t *bad_element) {
+  *bad_element = -1;
+  memset(out, 0, sizeof *out);
+  if (n == 0) return 6;
+  double *abs_err = (double *)malloc((size_t)n * sizeof(double));
+  uint64_t *ulps = (uint64_t *)malloc((size_t)n * sizeof(uint64_t));
+  if (!abs_err || !ulps) { free(abs_err); free(ulps); return -1; }
+  cmp_sim sim = {0, 0, 0, 0};
+  long double abs_sum = 0, ulp_sum = 0;
+  int verdict = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    double a, e;
+    uint32_t ab, eb;
+    if (!cmp_decode(dtype, actual, i, &a, &ab)) { *bad_element = i; verdict = 7; break; }
+    if (!cmp_decode(dtype, expected, i, &e, &eb)) { *bad_element = i; verdict = 8; break; }
+    const double ad = fabs(a - e);
+    const double tol = atol + rtol * fabs(e);
+    if (!isfinite(tol)) { *bad_element = i; verdict = 1; break; }
+    out->elementwise_mismatch_count += ad > tol;
+    sim_add(&sim, a, e);
+    const uint64_t u = cmp_ulp(dtype, ab, eb, a, e);
+    if (ad == 0.0) ++out->exact_element_count;
+    abs_sum += ad;
+    ulp_sum += u;
+    abs_err[i] = ad;
+    ulps[i] = u;
+  }
+  if (verdict) {
+    memset(out, 0, sizeof *out);
+    free(abs_err); free(ulps);
+    return verdict;
+  }
+  qsort(abs_err, (size_t)n, sizeof(double), cmp_f64);
+  qsort(ulps, (size_t)n, sizeof(uint64_t), cmp_u64);
+  out->element_count = (uint64_t)n;
+  out->exact_fraction = (double)out->exact_element_count / (double)n;
+  out->mean_absolute_error = (double)(abs_sum / n);
+  out->p99_absolute_error = abs_err[nearest_rank(0.99, n) - 1];
+  out->p999_absolute_error = abs_err[nearest_rank(0.999, n) - 1];
+  out->maximum_absolute_error = abs_err[n - 1];
+  out->cosine_similarity = sim_cosine(&sim);
+  out->relative_l2_error = sim_rel_l2(&sim);
+  out->mean_ulp_distance = (double)(ulp_sum / n);
+  out->p99_ulp_distance = ulps[nearest_rank(0.99, n) - 1];
+  out->p999_ulp_distance = ulps[nearest_rank(0.999, n) - 1];
+  out->maximum_ulp_distance = ulps[n - 1];
+  free(abs_err); free(ulps);
+  return 0;
+}

@@ -115,6 +115,25 @@ int oracle_memset(uint8_t *dst, int format, uint32_t value, int64_t count);
 int oracle_bit2fp(const uint8_t *bits, void *dst, int format, int64_t count);
 int oracle_mask_move(const void *src, const void *mask, void *dst, int format, int64_t count);
 
+/* ---- program-boundary comparison ----------------------------------------- */
+typedef struct oracle_cmp_stats {
+  uint64_t element_count, exact_element_count;
+  double exact_fraction, mean_absolute_error, p99_absolute_error, p999_absolute_error,
+      maximum_absolute_error;
+  uint64_t elementwise_mismatch_count;
+  double cosine_similarity, relative_l2_error, mean_ulp_distance;
+  uint64_t p99_ulp_distance, p999_ulp_distance, maximum_ulp_distance;
+} oracle_cmp_stats;
+/* dtype: 9 F16, 10 BF16, 11 F32 (ProgramElementType).  Returns the verdict
+ * (0 accepted, ProgramTensorComparisonErrorCode + 1 otherwise); info[0..4] =
+ * element that ended the scan, mismatch count, first mismatch, largest-error
+ * mismatch, largest-ratio mismatch. */
+int oracle_compare_floats(int dtype, const void *actual, const void *expected, int64_t n, double atol,
+                          double rtol, int has_similarity, double minimum_cosine, double maximum_relative_l2,
+                          double *cosine_out, double *relative_l2_out, int64_t *info);
+int oracle_compare_statistics(int dtype, const void *actual, const void *expected, int64_t n, double atol,
+                              double rtol, oracle_cmp_stats *out, int64_t *bad_element);
+
 #ifdef __cplusplus
 }
 #endif

@@ -46,7 +46,35 @@ EXPORTS = (
     "wafer_hip_rope", "wafer_hip_bias_add", "wafer_hip_head_permute", "wafer_hip_buffer_alloc",
     "wafer_hip_buffer_free", "wafer_hip_copy_to_device", "wafer_hip_copy_to_host", "wafer_hip_convert_route",
     "wafer_hip_strided_copy", "wafer_hip_memset", "wafer_hip_bit2fp", "wafer_hip_mask_move",
+    "wafer_hip_compare_expected", "wafer_hip_compare_statistics",
 )
+
+# ProgramElementType codes (the comparator's dtypes) and verdicts
+# (ProgramTensorComparisonErrorCode + 1; 0 = accepted).
+DT = dict(bool=0, i8=1, u8=2, i16=3, u16=4, i32=5, u32=6, i64=7, u64=8, f16=9, bf16=10, f32=11, tf32=12, f64=13)
+CMP_NAMES = ("accepted", "invalid-tolerance", "dtype-mismatch", "shape-mismatch", "byte-size-mismatch",
+             "unsupported-floating-dtype", "unsupported-statistics-dtype", "actual-nonfinite", "expected-nonfinite",
+             "numeric-mismatch", "raw-mismatch")
+
+
+class ProgramTensorDesc(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_uint32), ("rank", ctypes.c_uint32), ("shape", ctypes.POINTER(ctypes.c_int64)),
+                ("data", ctypes.c_void_p), ("bytes", ctypes.c_uint64)]
+
+
+class ComparisonPolicy(ctypes.Structure):
+    _fields_ = [("atol", ctypes.c_double), ("rtol", ctypes.c_double), ("has_similarity", ctypes.c_uint32),
+                ("minimum_cosine", ctypes.c_double), ("maximum_relative_l2", ctypes.c_double)]
+
+
+class ComparisonStatistics(ctypes.Structure):
+    _fields_ = [("element_count", ctypes.c_uint64), ("exact_element_count", ctypes.c_uint64),
+                ("exact_fraction", ctypes.c_double), ("mean_absolute_error", ctypes.c_double),
+                ("p99_absolute_error", ctypes.c_double), ("p999_absolute_error", ctypes.c_double),
+                ("maximum_absolute_error", ctypes.c_double), ("elementwise_mismatch_count", ctypes.c_uint64),
+                ("cosine_similarity", ctypes.c_double), ("relative_l2_error", ctypes.c_double),
+                ("mean_ulp_distance", ctypes.c_double), ("p99_ulp_distance", ctypes.c_uint64),
+                ("p999_ulp_distance", ctypes.c_uint64), ("maximum_ulp_distance", ctypes.c_uint64)]
 
 
 class WaferHipError(RuntimeError):
@@ -110,6 +138,12 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wafer_hip_memset.argtypes = [vp, vp, u32, u32, u64]
     L.wafer_hip_bit2fp.argtypes = [vp, vp, vp, u32, u64]
     L.wafer_hip_mask_move.argtypes = [vp, vp, vp, vp, u32, u64]
+    pt = ctypes.POINTER(ProgramTensorDesc)
+    L.wafer_hip_compare_expected.argtypes = [vp, pt, pt, ctypes.POINTER(ComparisonPolicy), u32p, ctypes.c_char_p,
+                                             ctypes.c_size_t]
+    L.wafer_hip_compare_statistics.argtypes = [vp, pt, pt, ctypes.POINTER(ComparisonPolicy), u32p,
+                                               ctypes.POINTER(ComparisonStatistics), ctypes.c_char_p,
+                                               ctypes.c_size_t]
 
 
 def _check(status: int) -> None:
@@ -300,6 +334,46 @@ class Context:
         if not (src.numel() == mask.numel() == dst.numel()):
             raise ValueError("mask_move: element counts differ")
         _check(self._L.wafer_hip_mask_move(self._bind(), _p(src), _p(mask), _p(dst), fmt, dst.numel()))
+
+    @staticmethod
+    def _program_tensor(spec):
+        """(dtype, tensor[, shape]) -> (descriptor, shape array kept alive)."""
+        dtype, t = spec[0], spec[1]
+        shape = tuple(t.shape) if len(spec) < 3 else tuple(spec[2])
+        arr = (ctypes.c_int64 * max(len(shape), 1))(*[int(x) for x in shape])
+        data = _p(t) if t.numel() else ctypes.c_void_p(0)
+        return ProgramTensorDesc(dtype, len(shape), arr, data, t.numel() * t.element_size()), arr
+
+    @staticmethod
+    def _policy(atol, rtol, similarity):
+        c, r = similarity if similarity is not None else (0.0, 0.0)
+        return ComparisonPolicy(atol, rtol, 1 if similarity is not None else 0, c, r)
+
+    def compare_expected(self, actual, expected, atol, rtol, similarity=None):
+        """The output gate.  actual / expected: (dtype code, device tensor[,
+        shape]); similarity: (minimum cosine, maximum relative L2) or None.
+        Returns (verdict code, detail)."""
+        a, ka = self._program_tensor(actual)
+        e, ke = self._program_tensor(expected)
+        verdict = ctypes.c_uint32()
+        detail = ctypes.create_string_buffer(1024)
+        pol = self._policy(atol, rtol, similarity)
+        _check(self._L.wafer_hip_compare_expected(self._bind(), ctypes.byref(a), ctypes.byref(e), ctypes.byref(pol),
+                                                  ctypes.byref(verdict), detail, 1024))
+        return verdict.value, detail.value.decode()
+
+    def compare_statistics(self, actual, expected, atol=0.0, rtol=0.0):
+        """The error distribution.  Returns (verdict code, dict or None, detail)."""
+        a, ka = self._program_tensor(actual)
+        e, ke = self._program_tensor(expected)
+        verdict = ctypes.c_uint32()
+        out = ComparisonStatistics()
+        detail = ctypes.create_string_buffer(1024)
+        pol = self._policy(atol, rtol, None)
+        _check(self._L.wafer_hip_compare_statistics(self._bind(), ctypes.byref(a), ctypes.byref(e), ctypes.byref(pol),
+                                                    ctypes.byref(verdict), ctypes.byref(out), detail, 1024))
+        stats = {k: getattr(out, k) for k, _ in ComparisonStatistics._fields_} if verdict.value == 0 else None
+        return verdict.value, stats, detail.value.decode()
 
     def bias_add(self, x, bias, y, fmt=F32):
         cols = x.shape[-1]
