@@ -83,7 +83,9 @@ def test_seam_library_exports_and_fails_loudly_without_gpu():
         pytest.skip("seam not built")
     syms = subprocess.run(["nm", "-D", "-C", str(lib)], capture_output=True, text=True).stdout
     for name in ("wafer::model::HipTargetModelBackend::create", "wafer::model::HipTargetModelBackend::tryExecute",
-                 "wafer::model::PhysicalTensorDescriptor::create", "wafer::model::stringifyTargetModelKernelErrorCode"):
+                 "wafer::model::PhysicalTensorDescriptor::create", "wafer::model::stringifyTargetModelKernelErrorCode",
+                 "wafer::model::loadNpyTensorPayload", "wafer::model::parseNpyPayloadHeader",
+                 "wafer::model::decodeProgramNpyDescr", "wafer_npy_load", "wafer_npy_free"):
         assert name in syms, name
     import torch
 

@@ -277,3 +277,39 @@ def test_statistics_large_vs_torch(hip):
     assert st["relative_l2_error"] == pytest.approx(rel.item(), rel=1e-10)
     del x, y, av, ev, ad, ulp
     torch.cuda.empty_cache()
+
+
+def test_program_boundary_npy_gate(hip, tmp_path):
+    # the reference's board flow at the program boundary: the FA output and a
+    # torch float32 reference written as .npy (bf16 as '|V2'), loaded by the
+    # C++ loader, gated on the GPU with the attention policy
+    # (test/Board/PyTorch/wafer_pytorch_board_cases.py:31-33)
+    from vibe_compiler_amd import program_io
+
+    say("npy gate")
+    g = torch.Generator(device="cuda").manual_seed(3)
+    q, k, v = (torch.randn((1, 4, 256, 128), device="cuda", generator=g).to(torch.bfloat16) for _ in range(3))
+    o = torch.empty_like(q)
+    scale = 1 / math.sqrt(128)
+    hip.attention_prefill(q, k, v, o, scale, causal=True)
+    s = (q.float() @ k.float().transpose(-1, -2).contiguous()) * scale
+    mask = torch.ones(256, 256, device="cuda", dtype=torch.bool).tril()
+    ref = torch.softmax(s.masked_fill(~mask, float("-inf")), dim=-1) @ v.float()
+
+    def save(t, path):
+        bits = t.to(torch.bfloat16).view(torch.int16).cpu().numpy().view(np.dtype("|V2"))
+        np.save(path, bits)
+    save(o, tmp_path / "actual.npy")
+    save(ref, tmp_path / "expected.npy")
+    policy = (0.008, 0.006)
+    v_, detail = program_io.compare_npy(hip, torch, tmp_path / "actual.npy", tmp_path / "expected.npy", *policy,
+                                        similarity=(0.9999, 0.01))
+    assert v_ == ACC, detail
+    v_, st, _ = program_io.compare_npy(hip, torch, tmp_path / "actual.npy", tmp_path / "expected.npy", *policy,
+                                       statistics=True)
+    assert v_ == ACC and st["cosine_similarity"] >= 0.9999 and st["relative_l2_error"] <= 0.01
+    bad = o.clone()
+    bad[0, 1, 7, :] += 1.0
+    save(bad, tmp_path / "bad.npy")
+    v_, detail = program_io.compare_npy(hip, torch, tmp_path / "bad.npy", tmp_path / "expected.npy", *policy)
+    assert v_ == NUMERIC and "first={element=%d " % (1 * 256 * 128 + 7 * 128) in detail
