@@ -89,6 +89,22 @@ int wafer_hip_copy_to_host(wafer_hip_context *ctx, void *dst, const void *src,
  * field (include/Wafer/Simulator/Kernel/TargetModelKernel.h:144-182). */
 const char *wafer_hip_implementation(void);
 
+/* The execution environment a qualification record binds: the analogue of
+ * OneDNNExecutionEnvironment's identity fields
+ * (include/Wafer/Simulator/OneDNN/OneDNNQualification.h:132-229 records its
+ * digest).  Strings are NUL-terminated. */
+typedef struct wafer_hip_environment_info {
+  char gcn_arch_name[64];   /* e.g. "gfx950:sramecc+:xnack-" */
+  char device_name[128];
+  int32_t compute_units;
+  int32_t hip_runtime_version;
+  int32_t driver_version;
+  int32_t warp_size;
+  uint64_t global_memory_bytes;
+  uint64_t lds_bytes_per_block;
+} wafer_hip_environment_info;
+int wafer_hip_environment(wafer_hip_context *ctx, wafer_hip_environment_info *out);
+
 /* ---- per-command GEMM (formal semantics, bit-exact) ----------------------
  * Replaces wafer_tx81_gemm_oriented (runtime/crt/include/wafer_tx81_crt.h:44-49)
  * as executed by the formal lane, executeGemm

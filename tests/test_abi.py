@@ -85,7 +85,10 @@ def test_seam_library_exports_and_fails_loudly_without_gpu():
     for name in ("wafer::model::HipTargetModelBackend::create", "wafer::model::HipTargetModelBackend::tryExecute",
                  "wafer::model::PhysicalTensorDescriptor::create", "wafer::model::stringifyTargetModelKernelErrorCode",
                  "wafer::model::loadNpyTensorPayload", "wafer::model::parseNpyPayloadHeader",
-                 "wafer::model::decodeProgramNpyDescr", "wafer_npy_load", "wafer_npy_free"):
+                 "wafer::model::decodeProgramNpyDescr", "wafer_npy_load", "wafer_npy_free",
+                 "wafer::model::validateHipBackend", "wafer::model::loadVerifiedHipQualificationRecord",
+                 "wafer::model::executeQualifiedHip", "wafer::model::captureHipExecutionEnvironment",
+                 "wafer_sha256_digest", "wafer_canonical_json"):
         assert name in syms, name
     import torch
 

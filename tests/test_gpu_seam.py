@@ -19,3 +19,20 @@ def test_seam_requests_match_oracle():
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "PASSED" in r.stdout
+
+
+QUALIFY = ROOT / "tests" / "seam" / "_build" / "qualify_check"
+
+
+@pytest.mark.gpu
+def test_qualification_records(tmp_path):
+    """Evidence records (vibe_compiler_amd/seam/qualification.h): validation
+    writes a record only for output bytes equal to the formal lane's; the
+    verified record qualifies exactly its problem on exactly its environment;
+    tampered records, other payloads and other environments are refused."""
+    assert QUALIFY.exists(), "build first: make -C tests/seam"
+    print("qualify_check", flush=True)
+    r = subprocess.run([str(QUALIFY), str(tmp_path)], capture_output=True, text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "ALL OK" in r.stdout

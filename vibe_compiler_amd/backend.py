@@ -46,7 +46,7 @@ EXPORTS = (
     "wafer_hip_rope", "wafer_hip_bias_add", "wafer_hip_head_permute", "wafer_hip_buffer_alloc",
     "wafer_hip_buffer_free", "wafer_hip_copy_to_device", "wafer_hip_copy_to_host", "wafer_hip_convert_route",
     "wafer_hip_strided_copy", "wafer_hip_memset", "wafer_hip_bit2fp", "wafer_hip_mask_move",
-    "wafer_hip_compare_expected", "wafer_hip_compare_statistics",
+    "wafer_hip_compare_expected", "wafer_hip_compare_statistics", "wafer_hip_environment",
 )
 
 # ProgramElementType codes (the comparator's dtypes) and verdicts

@@ -100,6 +100,26 @@ extern "C" const char *wafer_hip_implementation(void) {
          "managed elementwise/convert/reduce, Cx/NCx codec, fused regions";
 }
 
+extern "C" int wafer_hip_environment(wafer_hip_context *ctx, wafer_hip_environment_info *out) {
+  WAFER_CHECK_CTX(ctx);
+  if (!out) return fail(WAFER_HIP_E_INVALID_FIELD, "environment: null output");
+  memset(out, 0, sizeof *out);
+  hipDeviceProp_t prop;
+  WAFER_TRY(check_hip(hipGetDeviceProperties(&prop, ctx->device), "hipGetDeviceProperties"));
+  strncpy(out->gcn_arch_name, prop.gcnArchName, sizeof out->gcn_arch_name - 1);
+  strncpy(out->device_name, prop.name, sizeof out->device_name - 1);
+  out->compute_units = prop.multiProcessorCount;
+  out->warp_size = prop.warpSize;
+  out->global_memory_bytes = prop.totalGlobalMem;
+  out->lds_bytes_per_block = prop.sharedMemPerBlock;
+  int v = 0;
+  WAFER_TRY(check_hip(hipRuntimeGetVersion(&v), "hipRuntimeGetVersion"));
+  out->hip_runtime_version = v;
+  WAFER_TRY(check_hip(hipDriverGetVersion(&v), "hipDriverGetVersion"));
+  out->driver_version = v;
+  return WAFER_HIP_OK;
+}
+
 // ---- device buffers for host-side callers ---------------------------------
 // The seam adapter moves TargetModelNumericTensor storage through these, so
 // it needs nothing but this ABI.  Copies are ordered on the context's stream

@@ -228,6 +228,10 @@ public:
   Expected<TargetModelManagedReferenceResult> execute(const TargetModelReduceRequest &request,
                                                       FormalNumericWorkBudget scalarBudget) const override;
 
+  // The C ABI context the backend drives (for the qualification records'
+  // environment capture and case materialisation).
+  wafer_hip_context *context() const { return ctx; }
+
 private:
   explicit HipTargetModelBackend(wafer_hip_context *ctx) : ctx(ctx) {}
   wafer_hip_context *ctx;
