@@ -58,6 +58,21 @@ constexpr int KPITCH = D + 8;     // LDS row pitch of K tiles (elements): 272 B
 constexpr int VPITCH = BK + 8;    // LDS row pitch of V^T tiles (elements): 144 B
 constexpr int THREADS = 512;
 
+// Lazy rescaling: the exponentials use a reference max that moves only when
+// some row's running max exceeds it by more than 2^RESCALE_LOG2 (P <= 2^8).
+constexpr float RESCALE_LOG2 = 8.0f;
+
+// x combined with the value of lane ^ 32 (v_permlane32_swap exchanges the
+// upper half of one register with the lower half of the other)
+__device__ inline float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // V^T LDS column p of a 64-key block holds key swap23(p): bits 2 and 3 of
 // the key index swapped, so the 8 keys one lane feeds into one PV MFMA are
 // contiguous (the 32x32 accumulator layout puts rows 8(r/4) + 4g + r%4 in a
@@ -144,7 +159,9 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     }
   };
 
-  float m_raw = -__builtin_inff();
+  // running max of the raw scores, the reference max the exponentials use
+  // (and its scaled value, 0 while the reference is -inf), and the sum of P
+  float m_run = -__builtin_inff(), m_ref = -__builtin_inff(), mc_ref = 0.0f;
   float l_sum = 0.0f;
   f32x16 acc_o[4];
 #pragma unroll
@@ -181,28 +198,34 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[t][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_raw, mx);
-    const float mc = (m_new == -__builtin_inff()) ? 0.0f : m_new * c;
-    const float alpha = __builtin_amdgcn_exp2f(m_raw * c - mc);
+    mx = xor32_max(mx);
+    const float m_new = fmaxf(m_run, mx);
+    m_run = m_new;
+    // move the reference max (and rescale acc and l by alpha) only when a
+    // row's running max has grown by more than 2^RESCALE_LOG2 over it
+    const bool grow = m_new != -__builtin_inff() &&
+                      (m_ref == -__builtin_inff() || m_new * c > mc_ref + RESCALE_LOG2);
+    if (__any(grow)) {
+      const float mc = (m_new == -__builtin_inff()) ? 0.0f : m_new * c;
+      const float alpha = (m_ref == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(mc_ref - mc);
+      l_sum *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha;
+      m_ref = m_new;
+      mc_ref = mc;
+    }
     float rs = 0.0f;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][r], c, -mc));
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][r], c, -mc_ref));
         sacc[t][r] = p;
         rs += p;
       }
-    rs += __shfl_xor(rs, 32);
-    l_sum = l_sum * alpha + rs;
-    m_raw = m_new;
-    if (!__all(alpha == 1.0f)) {
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha;
-    }
+    l_sum += xor32_sum(rs);
     // P^T operands: (t, hf) covers S^T rows t*32 + hf*16 + [0,16); the
     // lane's 8 values are accumulator rows hf*8 + [0,8) of tile t.
     bf16x8 pb[2][2];
@@ -265,17 +288,18 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) xacc[((slot * 4 + dt) * 16 + r) * 64 + lane] = acc_o[dt][r];
-    xml[slot * 64 + lane] = m_raw;
+    xml[slot * 64 + lane] = m_ref;
     xml[256 + slot * 64 + lane] = l_sum;
   }
   __syncthreads();
   if (half == 1) return;
   {
+    // each state is (acc, l) relative to its reference max
     const float m1 = xml[slot * 64 + lane], l1 = xml[256 + slot * 64 + lane];
-    const float m = fmaxf(m_raw, m1);
+    const float m = fmaxf(m_ref, m1);
     const float e = (m == -__builtin_inff()) ? 0.0f : m * c;
-    const float s0 = __builtin_amdgcn_exp2f(m_raw * c - e);
-    const float s1 = __builtin_amdgcn_exp2f(m1 * c - e);
+    const float s0 = (m_ref == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m_ref * c - e);
+    const float s1 = (m1 == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m1 * c - e);
     l_sum = l_sum * s0 + l1 * s1;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
