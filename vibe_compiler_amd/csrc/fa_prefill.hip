@@ -15,35 +15,45 @@
 //
 // Mapping onto CDNA4:
 //  * a workgroup (8 waves) serves two 64-query blocks of one (batch, head):
-//    block i and block n-1-i of the causal triangle, so every workgroup does
-//    the same amount of work (i+1 + n-i key blocks) and one launch of
-//    heads*n/2 workgroups fills the CUs evenly with no cross-workgroup merge;
-//  * wave w: group g = w>>2 (0: the late block, 1: the early block), query
-//    tile w&1 (32 queries), key half (w>>1)&1.  The two key halves sweep the
-//    even and the odd 64-key blocks; each SIMD holds one late-block and one
-//    early-block wave, so all SIMDs carry equal work and one wave's softmax
-//    VALU work overlaps the other's MFMAs;
+//    block n-1-i (phase A) and then block i (phase B) of the causal
+//    triangle, so every workgroup does the same amount of work (n-i + i+1
+//    key blocks) and one launch of heads*n/2 workgroups fills the CUs evenly
+//    with no cross-workgroup merge;
+//  * wave w: query tile w&3 (16 queries of the current block), key half
+//    w>>2 (the even or the odd 64-key blocks).  All 8 waves work on the same
+//    query block, so each SIMD always carries two equally long chains whose
+//    MFMA and VALU work interleave; at the end of a phase the two key halves
+//    of a query tile merge through LDS;
 //  * scores are computed transposed, S^T = K . Q^T, on
-//    v_mfma_f32_32x32x16_bf16 (A = 32 keys x 16 d from LDS, B = Q^T kept in
-//    VGPRs), so each lane's accumulator column is one query: row max / sum /
-//    alpha are lane-local plus one xor-32 exchange;
-//  * the output is accumulated transposed as well, O^T = V^T . P^T: the
-//    rescale by alpha is lane-local and P^T feeds the MFMA B operand from the
-//    score registers after RNE narrowing (v_cvt_pk_bf16_f32).  The rescale is
-//    skipped when alpha == 1 for the whole wave (x * 1 == x exactly);
-//  * K tiles sit row-major in LDS, V tiles transposed (d-major) with keys
-//    permuted inside every 16-key group so the 8 keys one lane needs for one
-//    MFMA are contiguous (one ds_read_b128); per key half double-buffered in
-//    LDS and staged global -> VGPR two iterations ahead; both query blocks of a
-//    workgroup read the same tiles for their common key prefix;
+//    v_mfma_f32_16x16x32_bf16 (A = 16 keys x 32 d from LDS, B = Q^T kept in
+//    VGPRs): each lane holds 16 scores of one query, the 4 lanes of a query
+//    combine with permlane16/permlane32 swaps;
+//  * the output is accumulated transposed as well, O^T = V^T . P^T: P^T feeds
+//    the MFMA B operand straight from the score registers after RNE narrowing
+//    (v_cvt_pk_bf16_f32), and the V^T operand comes from row-major V in LDS
+//    through the transposing read ds_read_b64_tr_b16 (within each 16-lane
+//    group, lane i receives element i%4 of the 4-element vectors at the
+//    addresses of lanes 4e + i/4, e = 0..3);
+//  * K and V blocks move global -> LDS by buffer_load ... lds (no staging
+//    registers): two stages, the next block's DMA overlapping the current
+//    block's compute.  Rows are 256 bytes with 16-byte chunks XOR-swizzled
+//    by 2 (row & 7), which keeps the ds_read_b128 K reads and the
+//    transposed V reads free of bank conflicts (measured: 128 banks per
+//    half-wave for b128 reads, 64 for b64 reads);
+//  * lazy rescale: the exponentials are taken against a per-query reference
+//    max that moves only when a score exceeds it by more than 2^8 in the
+//    log2 domain; the common path computes no block max at all (a lane sum
+//    of P above 2^8 detects every such block);
 //  * consecutive workgroup ids walk (batch*head), so each head's workgroups
 //    land on one XCD (ids are dealt round-robin over the 8 XCDs) and share
 //    its L2.
 //
 // Arithmetic note: ExpLp(S*scale - m) is evaluated as
-// exp2(fma(s_raw, scale*log2e, -m_raw*scale*log2e)) (one rounding fewer than
+// exp2(fma(s_raw, scale*log2e, -m_ref*scale*log2e)) (one rounding fewer than
 // the reference's mul, sub, mul chain); the difference is below 1 ulp of the
-// f32 argument and far inside the attention tolerance.
+// f32 argument and far inside the attention tolerance.  With the lazy
+// reference P <= 2^8 and its bf16 rounding point differs from the
+// reference's, with the same relative bound.
 #include "common.h"
 
 #include <type_traits>
@@ -54,13 +64,19 @@ namespace {
 constexpr int D = 128;
 constexpr int QB = 64;            // queries per query block
 constexpr int BK = 64;            // keys per KV block
-constexpr int KPITCH = D + 8;     // LDS row pitch of K tiles (elements): 272 B
-constexpr int VPITCH = BK + 8;    // LDS row pitch of V^T tiles (elements): 144 B
 constexpr int THREADS = 512;
 
 // Lazy rescaling: the exponentials use a reference max that moves only when
-// some row's running max exceeds it by more than 2^RESCALE_LOG2 (P <= 2^8).
+// some query's max exceeds it by more than 2^RESCALE_LOG2 (P <= 2^8).
 constexpr float RESCALE_LOG2 = 8.0f;
+constexpr float RESCALE_BOUND = 256.0f;  // 2^RESCALE_LOG2
+// __builtin_amdgcn_sched_group_barrier instruction classes
+constexpr int SG_MFMA = 0x008, SG_DS_READ = 0x100;
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+// "no reference yet": finite, so exp2(fma(s, c, -NOREF)) is +inf for a
+// visible score and 0 for a masked one (never NaN), and exp2(NOREF - x) == 0
+constexpr float NOREF = -0x1p100f;
 
 // x combined with the value of lane ^ 32 (v_permlane32_swap exchanges the
 // upper half of one register with the lower half of the other)
@@ -73,19 +89,24 @@ __device__ inline float xor32_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// V^T LDS column p of a 64-key block holds key swap23(p): bits 2 and 3 of
-// the key index swapped, so the 8 keys one lane feeds into one PV MFMA are
-// contiguous (the 32x32 accumulator layout puts rows 8(r/4) + 4g + r%4 in a
-// lane) and one ds_read_b128 fetches them.
-__device__ inline int swap23(int p) { return (p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1); }
+__device__ inline float xor16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float xor16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 template <bool CAUSAL>
 __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, uint16_t *__restrict__ O, int q_heads, int kv_heads,
     int q_len, int kv_len, float c, int bh_count, int n_qblocks) {
-  __shared__ __align__(16) uint16_t sK[2][2][BK * KPITCH];  // [half][buf]
-  __shared__ __align__(16) uint16_t sV[2][2][D * VPITCH];
+  // two stages of [K half 0 | K half 1 | V half 0 | V half 1], 16 KiB each:
+  // rows of 256 bytes (64 keys x 128 d), 16-byte chunk ch of row r stored at
+  // chunk position ch ^ swz(r)
+  __shared__ __align__(1024) uint16_t sbuf[2][4][BK * D];
 
   const int bid = blockIdx.x;
   const int pair = bid / bh_count;
@@ -99,229 +120,259 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int grp = wave >> 2, tile = wave & 1, half = (wave >> 1) & 1;
-  const int l32 = lane & 31, g = lane >> 5;
-  // causal: pair the early block `pair` with the late block n-1-pair
-  const int qb_lo = CAUSAL ? pair : 2 * pair;
-  const int qb_hi = CAUSAL ? n_qblocks - 1 - pair : 2 * pair + 1;
-  const int qb = grp == 0 ? qb_hi : qb_lo;
-  const int q0 = qb * QB + tile * 32;
-  const int my_q = q0 + l32;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qt = wave & 3, half = wave >> 2;
+  const int l16 = lane & 15, g = lane >> 4;
+  // phase A serves the late query block, phase B the early one
+  const int qb_a = CAUSAL ? n_qblocks - 1 - pair : 2 * pair + 1;
+  const int qb_b = CAUSAL ? pair : 2 * pair;
   const int kv_blocks = kv_len / BK;
-  const int nk_hi = CAUSAL ? min(kv_blocks, qb_hi + 1) : kv_blocks;
-  const int nk_mine = CAUSAL ? min(kv_blocks, qb + 1) : kv_blocks;
+  const int nk_a = CAUSAL ? min(kv_blocks, qb_a + 1) : kv_blocks;
+  const int nk_b = CAUSAL ? min(kv_blocks, qb_b + 1) : kv_blocks;
+  const int ta = (nk_a + 1) / 2, niter = ta + (nk_b + 1) / 2;
 
-  // Q^T as the MFMA B operand: lane holds query l32, d = s*16 + g*8 + [0,8).
-  bf16x8 qreg[8];
+  // Q^T as the MFMA B operand: lane holds query l16, d = 32 s + 8 g + [0,8)
+  bf16x8 qreg[4];
+  int q0 = qb_a * QB + qt * 16;
+  auto load_q = [&]() __attribute__((always_inline)) {
 #pragma unroll
-  for (int s = 0; s < 8; ++s)
-    qreg[s] = *(const bf16x8 *)(Qp + (size_t)my_q * D + s * 16 + g * 8);
-  // (the Q loads are drained in the prologue below, together with the first
-  // K/V block: without an explicit drain the waitcnt pass ties Q's registers
-  // to the in-loop prefetch loads and stalls every iteration on them)
-
-  // global -> VGPR staging: the 4 waves of a key half load that half's
-  // block (K: 16 lanes per 256-byte key row; V: 4 consecutive keys per lane,
-  // so the V^T stores of 16 lanes fill one 128-byte LDS row segment without
-  // bank conflicts).  Two register slots keep the loads two iterations ahead
-  // of their use.
-  const int ltid = (((wave & 1) | ((wave >> 2) << 1)) << 6) | lane;  // 0..255 within the half
-  const int k_row = ltid >> 4, k_col = (ltid & 15) * 8;               // rows k_row + 16 i
-  const int v_kg = ltid & 15, v_dc = ltid >> 4;                       // keys 4 v_kg + i, d 8 v_dc
-  const int v_pos = swap23(4 * v_kg);
-  u32x4 kst[2][4], vst[2][4];
-  auto gload = [&](int kb, auto slot) __attribute__((always_inline)) {
-    const uint16_t *kp = Kp + (size_t)(kb * BK) * D;
-    const uint16_t *vp = Vp + (size_t)(kb * BK) * D;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      kst[slot][i] = *(const u32x4 *)(kp + (size_t)(k_row + 16 * i) * D + k_col);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      vst[slot][i] = *(const u32x4 *)(vp + (size_t)(4 * v_kg + i) * D + 8 * v_dc);
+    for (int s = 0; s < 4; ++s)
+      qreg[s] = *(const bf16x8 *)(Qp + (size_t)(q0 + l16) * D + s * 32 + g * 8);
   };
-  auto sstore = [&](int buf, auto slot) __attribute__((always_inline)) {
-    uint16_t *sk = sK[half][buf];
-    uint16_t *sv = sV[half][buf];
+  load_q();
+
+  // global -> LDS by buffer_load ... lds: the 4 waves of a key half move that
+  // half's K and V blocks, 4 + 4 instructions of 1 KiB (4 rows) per wave.
+  // Instruction j of wave qt writes rows 16 qt + 4 j + lane/16, chunk
+  // position lane%16, so lane loads global chunk (lane%16) ^ swz(row), with
+  // swz(row) = 2 (row & 7) = 8 (j & 1) + 2 (lane >> 4), which keeps the K
+  // fragment reads (ds_read_b128) and the transposed V reads
+  // (ds_read_b64_tr_b16) free of bank conflicts.
+  const __amdgpu_buffer_rsrc_t krsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void *)Kp, 0, (int)(kv_len * D * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void *)Vp, 0, (int)(kv_len * D * 2), 0x00020000);
+  uint32_t dma_off[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *(u32x4 *)&sk[(k_row + 16 * i) * KPITCH + k_col] = kst[slot][i];
+  for (int j = 0; j < 4; ++j)
+    dma_off[j] = (uint32_t)((16 * qt + 4 * j + (lane >> 4)) * 256 + (((lane & 15) ^ (8 * (j & 1) + 2 * (lane >> 4))) << 4));
+  // key block of iteration t for this half (t clamped to the last iteration,
+  // the block to the phase's last block: loads past the end are harmless)
+  auto block_of = [&](int t) __attribute__((always_inline)) {
+    t = min(t, niter - 1);
+    return t < ta ? min(2 * t + half, nk_a - 1) : min(2 * (t - ta) + half, nk_b - 1);
+  };
+  auto dma = [&](int kb, int buf) __attribute__((always_inline)) {
+    const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane(kb * BK * D * 2);
+    uint16_t *dk = sbuf[buf][half] + qt * 4 * 512;
+    uint16_t *dv = sbuf[buf][2 + half] + qt * 4 * 512;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const uint32_t a0 = vst[slot][0][w], a1 = vst[slot][1][w], a2 = vst[slot][2][w], a3 = vst[slot][3][w];
-      u32x2 lo, hi;
-      lo[0] = __builtin_amdgcn_perm(a1, a0, 0x05040100u);
-      lo[1] = __builtin_amdgcn_perm(a3, a2, 0x05040100u);
-      hi[0] = __builtin_amdgcn_perm(a1, a0, 0x07060302u);
-      hi[1] = __builtin_amdgcn_perm(a3, a2, 0x07060302u);
-      *(u32x2 *)&sv[(8 * v_dc + 2 * w) * VPITCH + v_pos] = lo;
-      *(u32x2 *)&sv[(8 * v_dc + 2 * w + 1) * VPITCH + v_pos] = hi;
-    }
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krsrc, (__attribute__((address_space(3))) void *)(dk + j * 512), 16,
+                                               dma_off[j], so, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrsrc, (__attribute__((address_space(3))) void *)(dv + j * 512), 16,
+                                               dma_off[j], so, 0, 0);
   };
 
-  // running max of the raw scores, the reference max the exponentials use
-  // (and its scaled value, 0 while the reference is -inf), and the sum of P
-  float m_run = -__builtin_inff(), m_ref = -__builtin_inff(), mc_ref = 0.0f;
-  float l_sum = 0.0f;
-  f32x16 acc_o[4];
+  // LDS read offsets (bytes within a 16 KiB block), per lane:
+  //  K (A operand of S^T = K.Q^T, k-step s, key tile kt): row kt*16 + l16,
+  //    chunk 4 s + g, swz = 2 (l16 & 7)  ->  k_off[s] + kt * 4096
+  //  V^T (A operand of O^T = V^T.P^T via ds_read_b64_tr_b16, k-step s, key
+  //    half hh, d tile dt): lane reads row 32 s + 16 hh + 4 g + l16/4,
+  //    d 16 dt + 4 (l16 % 4) (chunk 2 dt + (l16/2) % 2, byte 8 (l16 % 2));
+  //    swz = 8 (g % 2) + 2 (l16 / 4)  ->  v_off[dt] + (32 s + 16 hh) * 256
+  uint32_t k_off[4], v_off[8];
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int s = 0; s < 4; ++s) k_off[s] = (uint32_t)(l16 * 256 + (((4 * s + g) ^ (2 * (l16 & 7))) << 4));
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc_o[dt][r] = 0.0f;
+  for (int dt = 0; dt < 8; ++dt)
+    v_off[dt] = (uint32_t)((4 * g + (l16 >> 2)) * 256 +
+                           (((2 * dt + ((l16 >> 1) & 1)) ^ (8 * (g & 1) + 2 * (l16 >> 2))) << 4) + 8 * (l16 & 1));
 
-  // one 64-key block: S^T = K.Q^T, online-softmax update, O^T += V^T.P^T
-  auto compute = [&](int kb, const uint16_t *sk, const uint16_t *sv) __attribute__((always_inline)) {
-    f32x16 sacc[2];
+  // per lane: the scaled reference max of query l16 (shared by the 4 lanes
+  // of the query; NOREF until the query has seen a visible key) and this
+  // lane's partial sum of P
+  float mc_ref = NOREF;
+  float l_part = 0.0f;
+  f32x4 acc_o[8];  // O^T rows dt*16 + 4 g + [0,4), column query l16
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+  for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[t][r] = 0.0f;
-    // the two key tiles alternate so consecutive MFMAs are independent
+    for (int j = 0; j < 4; ++j) acc_o[dt][j] = 0.0f;
+
+  // one 64-key block: S^T = K.Q^T, online-softmax update, O^T += V^T.P^T.
+  // The exponentials are taken against the current reference first; a lane
+  // sum above 2^RESCALE_LOG2 (implied by any P above it, and by every
+  // visible score while there is no reference) sends the wave to the exact
+  // update: block max, reference moved if some query's max exceeds it by
+  // more than 2^RESCALE_LOG2, state rescaled, exponentials recomputed.
+  auto compute = [&](int kb, const char *sk, const char *sv) __attribute__((always_inline)) {
+    f32x4 sacc[4];  // S^T rows kt*16 + 4 g + [0,4)
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
+    for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const bf16x8 a = *(const bf16x8 *)&sk[(t * 32 + l32) * KPITCH + s * 16 + g * 8];
-        sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[s], sacc[t], 0, 0, 0);
+      for (int j = 0; j < 4; ++j) sacc[kt][j] = 0.0f;
+    bf16x8 kf[4][4], vf[2][8];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) kf[s][kt] = *(const bf16x8 *)(sk + k_off[s] + kt * 4096);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+        sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[s][kt], qreg[s], sacc[kt], 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_v4i16 *)(sv + v_off[dt] + (32 * s) * 256));
+        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_v4i16 *)(sv + v_off[dt] + (32 * s + 16) * 256));
+        vf[s][dt] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
+    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 16, 0);
+    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 16, 0);
+    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 32, 0);
     if (CAUSAL && kb * BK + BK - 1 > q0) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kb * BK + t * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-          if (key > my_q) sacc[t][r] = -__builtin_inff();
-        }
+        for (int j = 0; j < 4; ++j)
+          if (kb * BK + kt * 16 + 4 * g + j > q0 + l16) sacc[kt][j] = -__builtin_inff();
     }
-    float mx = sacc[0][0];
+    f32x4 p[4];
+    float rs[4];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[t][r]);
-    mx = xor32_max(mx);
-    const float m_new = fmaxf(m_run, mx);
-    m_run = m_new;
-    // move the reference max (and rescale acc and l by alpha) only when a
-    // row's running max has grown by more than 2^RESCALE_LOG2 over it
-    const bool grow = m_new != -__builtin_inff() &&
-                      (m_ref == -__builtin_inff() || m_new * c > mc_ref + RESCALE_LOG2);
-    if (__any(grow)) {
-      const float mc = (m_new == -__builtin_inff()) ? 0.0f : m_new * c;
-      const float alpha = (m_ref == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(mc_ref - mc);
-      l_sum *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha;
-      m_ref = m_new;
-      mc_ref = mc;
+      for (int j = 0; j < 4; ++j) p[kt][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][j], c, -mc_ref));
+      rs[kt] = (p[kt][0] + p[kt][1]) + (p[kt][2] + p[kt][3]);
     }
-    float rs = 0.0f;
+    float rsum = (rs[0] + rs[1]) + (rs[2] + rs[3]);
+    if (__builtin_expect(__any(rsum > RESCALE_BOUND), 0)) {
+      float mx = -__builtin_inff();
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int kt = 0; kt < 4; ++kt)
+        mx = fmaxf(mx, fmaxf(fmaxf(sacc[kt][0], sacc[kt][1]), fmaxf(sacc[kt][2], sacc[kt][3])));
+      mx = xor16_max(xor32_max(mx));
+      const float mc_new = mx * c;
+      if (mx != -__builtin_inff() && mc_new > mc_ref + RESCALE_LOG2) {
+        const float alpha = __builtin_amdgcn_exp2f(mc_ref - mc_new);  // 0 from NOREF
+        l_part *= alpha;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][r], c, -mc_ref));
-        sacc[t][r] = p;
-        rs += p;
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc_o[dt][j] *= alpha;
+        mc_ref = mc_new;
       }
-    l_sum += xor32_sum(rs);
-    // P^T operands: (t, hf) covers S^T rows t*32 + hf*16 + [0,16); the
-    // lane's 8 values are accumulator rows hf*8 + [0,8) of tile t.
-    bf16x8 pb[2][2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
+        for (int j = 0; j < 4; ++j) p[kt][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][j], c, -mc_ref));
+        rs[kt] = (p[kt][0] + p[kt][1]) + (p[kt][2] + p[kt][3]);
+      }
+      rsum = (rs[0] + rs[1]) + (rs[2] + rs[3]);
+    }
+    l_part += rsum;
+    // P^T operand of k-step s: slots 8 g + [0,4) are keys 32 s + 4 g + [0,4)
+    // (tile 2 s), slots 8 g + [4,8) keys 32 s + 16 + 4 g + [0,4) (tile 2 s + 1)
+    bf16x8 pb[2];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pb[t][hf][e] = (__bf16)sacc[t][hf * 8 + e];
+    for (int s = 0; s < 2; ++s)
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int j = 0; j < 4; ++j) {
+        pb[s][j] = (__bf16)p[2 * s][j];
+        pb[s][4 + j] = (__bf16)p[2 * s + 1][j];
+      }
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
+    for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-          const bf16x8 va = *(const bf16x8 *)&sv[(dt * 32 + l32) * VPITCH + t * 32 + hf * 16 + g * 8];
-          acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[t][hf], acc_o[dt], 0, 0, 0);
-        }
+      for (int dt = 0; dt < 8; ++dt)
+        acc_o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[s][dt], pb[s], acc_o[dt], 0, 0, 0);
   };
 
-  // Pipeline (per key half; iteration i works on block 2 i + half):
-  //   LDS buffer i%2 holds iteration i's block; register slot (i+1)%2 holds
-  //   iteration i+1's block, loaded one iteration earlier; iteration i loads
-  //   iteration i+2's block into slot i%2, computes, stores slot (i+1)%2 into
-  //   LDS buffer (i+1)%2, and meets the other waves at one barrier.  Loads
-  //   and stores are unconditional (block index clamped to the last block)
-  //   so the waitcnt pass counts them exactly and waits only for the older
-  //   slot.
-  const int niter = (nk_hi + 1) / 2;
-  const int last = nk_hi - 1;
-  gload(min(half, last), std::integral_constant<int, 0>{});
-  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): Q and the first block
-  sstore(0, std::integral_constant<int, 0>{});
-  gload(min(half + 2, last), std::integral_constant<int, 1>{});
-  __syncthreads();
-
-  auto step = [&](int i, auto slot) __attribute__((always_inline)) {
-    constexpr int P = decltype(slot)::value;  // == i % 2
-    const int kb = 2 * i + half;
-    gload(min(kb + 4, last), std::integral_constant<int, P>{});
-    const bool active = (kb < nk_mine) && (!CAUSAL || kb * BK <= q0 + 31);
-    if (active) compute(kb, sK[half][P], sV[half][P]);
-    if (i + 1 < niter) {
-      sstore(P ^ 1, std::integral_constant<int, P ^ 1>{});
-      __syncthreads();
+  // The two key halves of one query tile merge through LDS (`xr`, free at
+  // the call), then the even half normalises and writes the query tile.
+  auto finish = [&](float *xr) __attribute__((always_inline)) {
+    float *xacc = xr;               // [qt][dt][j][lane]: 32 KiB
+    float *xml = xr + 4 * 32 * 64;  // mc_ref [qt][lane], l_part [qt][lane]
+    if (half == 1) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xacc[((qt * 8 + dt) * 4 + j) * 64 + lane] = acc_o[dt][j];
+      xml[qt * 64 + lane] = mc_ref;
+      xml[256 + qt * 64 + lane] = l_part;
+    }
+    __syncthreads();
+    if (half == 0) {
+      // each state is (acc, l) relative to its scaled reference max; a state
+      // that never saw a visible key (NOREF) has l == 0 and acc == 0
+      const float m1 = xml[qt * 64 + lane], l1 = xml[256 + qt * 64 + lane];
+      const float e = fmaxf(mc_ref, m1);
+      const float s0 = __builtin_amdgcn_exp2f(mc_ref - e);
+      const float s1 = __builtin_amdgcn_exp2f(m1 - e);
+      const float lp = l_part * s0 + l1 * s1;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc_o[dt][j] = acc_o[dt][j] * s0 + xacc[((qt * 8 + dt) * 4 + j) * 64 + lane] * s1;
+      const float l = xor16_sum(xor32_sum(lp));
+      // finalize: coefficient = Recip(l) (0 for an empty row), out = bf16(acc * coef)
+      const float coef = (l == 0.0f) ? 0.0f : 1.0f / l;
+      uint16_t *orow = O + ((size_t)bh * q_len + q0 + l16) * D + 4 * g;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        u32x2 packed;
+        packed[0] = (uint32_t)f32_to_bf16(acc_o[dt][0] * coef) | ((uint32_t)f32_to_bf16(acc_o[dt][1] * coef) << 16);
+        packed[1] = (uint32_t)f32_to_bf16(acc_o[dt][2] * coef) | ((uint32_t)f32_to_bf16(acc_o[dt][3] * coef) << 16);
+        *(u32x2 *)(orow + dt * 16) = packed;
+      }
     }
   };
-  for (int i = 0; i < niter; i += 2) {
-    step(i, std::integral_constant<int, 0>{});
-    if (i + 1 < niter) step(i + 1, std::integral_constant<int, 1>{});
-  }
 
-  // ---- merge the odd-block half into the even-block half through LDS ----
+  // Pipeline (iteration t works on block_of(t) of each half): stage t%2
+  // holds iteration t's blocks.  Iteration t starts the DMA of iteration
+  // t+1's blocks into stage (t+1)%2 (read last in iteration t-1, before the
+  // barrier that ended it), computes from stage t%2, waits for its own DMA
+  // and meets the other waves at one barrier.  After the last iteration of
+  // phase A stage t%2 is free until the next DMA: the halves merge there and
+  // phase B starts with a fresh state.
+  dma(block_of(0), 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // Q and the first blocks
   __syncthreads();
-  float *xacc = (float *)&sK[0][0][0];  // [grp*2+tile][dt][r][lane], 64 KiB
-  float *xml = (float *)&sV[0][0][0];   // m [slot][lane], l [slot][lane]
-  const int slot = grp * 2 + tile;
-  if (half == 1) {
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) xacc[((slot * 4 + dt) * 16 + r) * 64 + lane] = acc_o[dt][r];
-    xml[slot * 64 + lane] = m_ref;
-    xml[256 + slot * 64 + lane] = l_sum;
-  }
-  __syncthreads();
-  if (half == 1) return;
-  {
-    // each state is (acc, l) relative to its reference max
-    const float m1 = xml[slot * 64 + lane], l1 = xml[256 + slot * 64 + lane];
-    const float m = fmaxf(m_ref, m1);
-    const float e = (m == -__builtin_inff()) ? 0.0f : m * c;
-    const float s0 = (m_ref == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m_ref * c - e);
-    const float s1 = (m1 == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m1 * c - e);
-    l_sum = l_sum * s0 + l1 * s1;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        acc_o[dt][r] = acc_o[dt][r] * s0 + xacc[((slot * 4 + dt) * 16 + r) * 64 + lane] * s1;
-  }
 
-  // finalize: coefficient = Recip(l) (0 for an empty row), out = bf16(acc * coef)
-  const float coef = (l_sum == 0.0f) ? 0.0f : 1.0f / l_sum;
-  uint16_t *orow = O + ((size_t)bh * q_len + my_q) * D;
+  auto step = [&](int t, auto slot) __attribute__((always_inline)) {
+    constexpr int P = decltype(slot)::value;  // == t % 2
+    if (t + 1 < niter) dma(block_of(t + 1), P ^ 1);
+    const int kb = t < ta ? 2 * t + half : 2 * (t - ta) + half;
+    if (kb < (t < ta ? nk_a : nk_b))
+      compute(kb, (const char *)sbuf[P][half], (const char *)sbuf[P][2 + half]);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t == ta - 1) {
+      finish((float *)&sbuf[P][0][0]);  // 64 KiB, free until the next DMA
+      __syncthreads();                  // merge reads done before that DMA
+      q0 = qb_b * QB + qt * 16;
+      load_q();
+      mc_ref = NOREF;
+      l_part = 0.0f;
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+      for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-    for (int rq = 0; rq < 4; ++rq) {
-      u32x2 packed;
-      packed[0] = (uint32_t)f32_to_bf16(acc_o[dt][4 * rq + 0] * coef) |
-                  ((uint32_t)f32_to_bf16(acc_o[dt][4 * rq + 1] * coef) << 16);
-      packed[1] = (uint32_t)f32_to_bf16(acc_o[dt][4 * rq + 2] * coef) |
-                  ((uint32_t)f32_to_bf16(acc_o[dt][4 * rq + 3] * coef) << 16);
-      *(u32x2 *)(orow + dt * 32 + 8 * rq + 4 * g) = packed;
+        for (int j = 0; j < 4; ++j) acc_o[dt][j] = 0.0f;
     }
+  };
+  for (int t = 0; t < niter; t += 2) {
+    step(t, std::integral_constant<int, 0>{});
+    if (t + 1 < niter) step(t + 1, std::integral_constant<int, 1>{});
+  }
+  finish((float *)&sbuf[0][0][0]);
 }
 
 }  // namespace
@@ -350,6 +401,8 @@ extern "C" int wafer_hip_attention_prefill(wafer_hip_context *ctx, uint32_t form
   if (causal && kv_len < q_len)
     return fail(WAFER_HIP_E_UNSUPPORTED, "attention_prefill: causal needs kv_len >= q_len");
   if (!(scale > 0.0f)) return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill: scale must be positive");
+  if ((uint64_t)kv_len * D * 2 > 0x7fffffffull)  // 32-bit buffer offsets of one head's K/V
+    return fail(WAFER_HIP_E_UNSUPPORTED, "attention_prefill: kv_len too large (max 8388607)");
   if ((uint64_t)batch * q_heads * (q_len / (2 * QB)) > 0x7fffffffull)
     return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill: grid too large");
   WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
