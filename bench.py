@@ -10,7 +10,8 @@ algorithmic (causal, visible-pair) work; FD decode (config 2), the int8 GEMM
 (config 3), the fp32 MLP block (config 0) and the decoder layer (config 4)
 are reported in `secondary`,
 each with its own roofline fraction and CPU baseline.  Timing: W untimed
-launches, then exactly K launches captured into one HIP graph and replayed
+launches, then exactly K launches captured into one HIP graph, replayed
+untimed for SETTLE_S seconds so the GPU clocks settle, and replayed once
 between two HIP events on the stream the kernels run on (the backend binds
 torch's current stream at each call, the capture stream during capture).
 
@@ -67,14 +68,21 @@ def traffic_for(kernel: str):
         return None
 
 
+SETTLE_S = 0.3  # untimed replays before the timed one: the GPU's clocks
+                # take tens of milliseconds of sustained load to settle
+
+
 def timed(torch, fn, steps: int, warmup: int) -> float:
     """Average milliseconds per step over exactly `steps` steps.
 
     The W warmup steps run eagerly (they also size the backend's workspace).
-    The K timed steps are captured once into a HIP graph and replayed between
-    two HIP events on the replay stream, so the figure is the GPU's time for
-    K back-to-back steps, free of the Python binding's per-call host cost
-    (a C++ caller of the C ABI does not pay it)."""
+    The K timed steps are captured once into a HIP graph; the graph is
+    replayed untimed for at least SETTLE_S seconds (the clocks of an idle
+    GPU ramp up over tens of milliseconds of load; a short warmup times the
+    ramp, not the kernel), then one replay is timed between two HIP events
+    on the replay stream, so the figure is the GPU's time for K back-to-back
+    steps, free of the Python binding's per-call host cost (a C++ caller of
+    the C ABI does not pay it)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -88,6 +96,10 @@ def timed(torch, fn, steps: int, warmup: int) -> float:
     torch.cuda.current_stream().wait_stream(side)
     graph.replay()  # untimed: first replay uploads the graph
     torch.cuda.synchronize()
+    t_end = time.perf_counter() + SETTLE_S
+    while time.perf_counter() < t_end:
+        graph.replay()
+        torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()

@@ -71,7 +71,7 @@ constexpr int THREADS = 512;
 constexpr float RESCALE_LOG2 = 8.0f;
 constexpr float RESCALE_BOUND = 256.0f;  // 2^RESCALE_LOG2
 // __builtin_amdgcn_sched_group_barrier instruction classes
-constexpr int SG_MFMA = 0x008, SG_DS_READ = 0x100;
+constexpr int SG_MFMA = 0x008, SG_VMEM = 0x010, SG_DS_READ = 0x100;
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 // "no reference yet": finite, so exp2(fma(s, c, -NOREF)) is +inf for a
@@ -162,14 +162,17 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     t = min(t, niter - 1);
     return t < ta ? min(2 * t + half, nk_a - 1) : min(2 * (t - ta) + half, nk_b - 1);
   };
-  auto dma = [&](int kb, int buf) __attribute__((always_inline)) {
+  auto dma_k = [&](int kb, int buf) __attribute__((always_inline)) {
     const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane(kb * BK * D * 2);
     uint16_t *dk = sbuf[buf][half] + qt * 4 * 512;
-    uint16_t *dv = sbuf[buf][2 + half] + qt * 4 * 512;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(krsrc, (__attribute__((address_space(3))) void *)(dk + j * 512), 16,
                                                dma_off[j], so, 0, 0);
+  };
+  auto dma_v = [&](int kb, int buf) __attribute__((always_inline)) {
+    const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane(kb * BK * D * 2);
+    uint16_t *dv = sbuf[buf][2 + half] + qt * 4 * 512;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(vrsrc, (__attribute__((address_space(3))) void *)(dv + j * 512), 16,
@@ -208,7 +211,11 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
   // visible score while there is no reference) sends the wave to the exact
   // update: block max, reference moved if some query's max exceeds it by
   // more than 2^RESCALE_LOG2, state rescaled, exponentials recomputed.
-  auto compute = [&](int kb, const char *sk, const char *sv) __attribute__((always_inline)) {
+  // `kdma` / `vdma` issue the next blocks' K / V moves: K's after this
+  // block's QK fragments and MFMAs are queued, V's one instruction per 4 PV
+  // MFMAs (a DMA issue stalls the wave; between queued MFMAs it costs
+  // little).
+  auto compute = [&](int kb, const char *sk, const char *sv, auto &&kdma, auto &&vdma) __attribute__((always_inline)) {
     f32x4 sacc[4];  // S^T rows kt*16 + 4 g + [0,4)
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
@@ -234,9 +241,11 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
             (lds_v4i16 *)(sv + v_off[dt] + (32 * s + 16) * 256));
         vf[s][dt] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
+    kdma();
     __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 16, 0);
     __builtin_amdgcn_sched_group_barrier(SG_MFMA, 16, 0);
     __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 32, 0);
+    __builtin_amdgcn_sched_group_barrier(SG_VMEM, 4, 0);
     if (CAUSAL && kb * BK + BK - 1 > q0) {
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
@@ -293,6 +302,12 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt)
         acc_o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[s][dt], pb[s], acc_o[dt], 0, 0, 0);
+    vdma();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 4, 1);
+      __builtin_amdgcn_sched_group_barrier(SG_VMEM, 1, 1);
+    }
   };
 
   // The two key halves of one query tile merge through LDS (`xr`, free at
@@ -337,22 +352,31 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
   };
 
   // Pipeline (iteration t works on block_of(t) of each half): stage t%2
-  // holds iteration t's blocks.  Iteration t starts the DMA of iteration
-  // t+1's blocks into stage (t+1)%2 (read last in iteration t-1, before the
-  // barrier that ended it), computes from stage t%2, waits for its own DMA
-  // and meets the other waves at one barrier.  After the last iteration of
+  // holds iteration t's blocks.  Iteration t moves iteration t+1's blocks
+  // into stage (t+1)%2 (read last in iteration t-1, before the barrier that
+  // ended it) while it computes from stage t%2, waits for its own moves and
+  // meets the other waves at one barrier.  After the last iteration of
   // phase A stage t%2 is free until the next DMA: the halves merge there and
   // phase B starts with a fresh state.
-  dma(block_of(0), 0);
+  dma_k(block_of(0), 0);
+  dma_v(block_of(0), 0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // Q and the first blocks
   __syncthreads();
 
   auto step = [&](int t, auto slot) __attribute__((always_inline)) {
     constexpr int P = decltype(slot)::value;  // == t % 2
-    if (t + 1 < niter) dma(block_of(t + 1), P ^ 1);
+    // the next blocks' moves (after the last iteration a clamped, unused
+    // block: unconditional, so they can sit between the MFMAs)
+    auto kdma = [&]() __attribute__((always_inline)) { dma_k(block_of(t + 1), P ^ 1); };
+    auto vdma = [&]() __attribute__((always_inline)) { dma_v(block_of(t + 1), P ^ 1); };
     const int kb = t < ta ? 2 * t + half : 2 * (t - ta) + half;
-    if (kb < (t < ta ? nk_a : nk_b))
-      compute(kb, (const char *)sbuf[P][half], (const char *)sbuf[P][2 + half]);
+    if (kb < (t < ta ? nk_a : nk_b)) {
+      compute(kb, (const char *)sbuf[P][half], (const char *)sbuf[P][2 + half], kdma, vdma);
+    } else {
+      asm volatile("" ::: "memory");  // keeps the moves from being hoisted out of compute
+      kdma();
+      vdma();
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (t == ta - 1) {
