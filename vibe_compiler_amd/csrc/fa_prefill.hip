@@ -310,45 +310,57 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     }
   };
 
-  // The two key halves of one query tile merge through LDS (`xr`, free at
-  // the call), then the even half normalises and writes the query tile.
-  auto finish = [&](float *xr) __attribute__((always_inline)) {
-    float *xacc = xr;               // [qt][dt][j][lane]: 32 KiB
-    float *xml = xr + 4 * 32 * 64;  // mc_ref [qt][lane], l_part [qt][lane]
-    if (half == 1) {
+  // The two key halves of one query tile merge by a reduce-scatter through
+  // LDS (`xr`, free at the call): half h keeps d tiles 4 h .. 4 h + 3,
+  // hands the other four to its partner, merges the partner's four into its
+  // own, normalises and writes them.  Exchange layout: 16-byte vectors,
+  // [qt][writer half][tile][lane] (1 KiB rows: b128 without conflicts), then
+  // the (reference max, lane sum) pairs.  Each state is (acc, l) relative to
+  // its scaled reference max; a state that never saw a visible key (NOREF)
+  // has l == 0 and acc == 0.
+  auto lds_barrier = [&]() __attribute__((always_inline)) {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // LDS only: stores stay in flight
+  };
+  auto finish_h = [&](float *xr, bool last, auto half_c) __attribute__((always_inline)) {
+    constexpr int H = decltype(half_c)::value;  // == half, so every tile index is static
+    f32x4 *xacc = (f32x4 *)xr;                  // [qt][half][4][lane]: 32 KiB
+    float *xml = xr + 4 * 2 * 4 * 64 * 4;       // [qt][half][2][lane]
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
+    for (int i = 0; i < 4; ++i) xacc[((qt * 2 + H) * 4 + i) * 64 + lane] = acc_o[4 * (1 - H) + i];
+    xml[((qt * 2 + H) * 2 + 0) * 64 + lane] = mc_ref;
+    xml[((qt * 2 + H) * 2 + 1) * 64 + lane] = l_part;
+    lds_barrier();
+    const float m1 = xml[((qt * 2 + (1 - H)) * 2 + 0) * 64 + lane];
+    const float l1 = xml[((qt * 2 + (1 - H)) * 2 + 1) * 64 + lane];
+    const float e = fmaxf(mc_ref, m1);
+    const float s0 = __builtin_amdgcn_exp2f(mc_ref - e);
+    const float s1 = __builtin_amdgcn_exp2f(m1 - e);
+    const float l = xor16_sum(xor32_sum(l_part * s0 + l1 * s1));
+    // finalize: coefficient = Recip(l) (0 for an empty row), out = bf16(acc * coef)
+    const float coef = (l == 0.0f) ? 0.0f : 1.0f / l;
+    uint16_t *orow = O + ((size_t)bh * q_len + q0 + l16) * D + 4 * g;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xacc[((qt * 8 + dt) * 4 + j) * 64 + lane] = acc_o[dt][j];
-      xml[qt * 64 + lane] = mc_ref;
-      xml[256 + qt * 64 + lane] = l_part;
+    for (int i = 0; i < 4; ++i) {
+      const int dt = 4 * H + i;
+      const f32x4 o = xacc[((qt * 2 + (1 - H)) * 4 + i) * 64 + lane];
+      f32x4 r;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r[j] = (acc_o[dt][j] * s0 + o[j] * s1) * coef;
+      u32x2 packed;
+      packed[0] = (uint32_t)f32_to_bf16(r[0]) | ((uint32_t)f32_to_bf16(r[1]) << 16);
+      packed[1] = (uint32_t)f32_to_bf16(r[2]) | ((uint32_t)f32_to_bf16(r[3]) << 16);
+      *(u32x2 *)(orow + dt * 16) = packed;
     }
-    __syncthreads();
-    if (half == 0) {
-      // each state is (acc, l) relative to its scaled reference max; a state
-      // that never saw a visible key (NOREF) has l == 0 and acc == 0
-      const float m1 = xml[qt * 64 + lane], l1 = xml[256 + qt * 64 + lane];
-      const float e = fmaxf(mc_ref, m1);
-      const float s0 = __builtin_amdgcn_exp2f(mc_ref - e);
-      const float s1 = __builtin_amdgcn_exp2f(m1 - e);
-      const float lp = l_part * s0 + l1 * s1;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc_o[dt][j] = acc_o[dt][j] * s0 + xacc[((qt * 8 + dt) * 4 + j) * 64 + lane] * s1;
-      const float l = xor16_sum(xor32_sum(lp));
-      // finalize: coefficient = Recip(l) (0 for an empty row), out = bf16(acc * coef)
-      const float coef = (l == 0.0f) ? 0.0f : 1.0f / l;
-      uint16_t *orow = O + ((size_t)bh * q_len + q0 + l16) * D + 4 * g;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        u32x2 packed;
-        packed[0] = (uint32_t)f32_to_bf16(acc_o[dt][0] * coef) | ((uint32_t)f32_to_bf16(acc_o[dt][1] * coef) << 16);
-        packed[1] = (uint32_t)f32_to_bf16(acc_o[dt][2] * coef) | ((uint32_t)f32_to_bf16(acc_o[dt][3] * coef) << 16);
-        *(u32x2 *)(orow + dt * 16) = packed;
-      }
-    }
+    if (!last) lds_barrier();  // exchange reads done before the buffers are reused
+    // a distinct marker per half: keeps the two copies from being merged
+    // into one tail that would index acc_o at run time (and spill it)
+    asm volatile("; fa merge tail %0" ::"n"(H));
+  };
+  auto finish = [&](float *xr, bool last) __attribute__((always_inline)) {
+    if (half == 0)  // wave-uniform
+      finish_h(xr, last, std::integral_constant<int, 0>{});
+    else
+      finish_h(xr, last, std::integral_constant<int, 1>{});
   };
 
   // Pipeline (iteration t works on block_of(t) of each half): stage t%2
@@ -380,8 +392,7 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (t == ta - 1) {
-      finish((float *)&sbuf[P][0][0]);  // 64 KiB, free until the next DMA
-      __syncthreads();                  // merge reads done before that DMA
+      finish((float *)&sbuf[P][0][0], false);  // 64 KiB, free until the next DMA
       q0 = qb_b * QB + qt * 16;
       load_q();
       mc_ref = NOREF;
@@ -396,7 +407,7 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     step(t, std::integral_constant<int, 0>{});
     if (t + 1 < niter) step(t + 1, std::integral_constant<int, 1>{});
   }
-  finish((float *)&sbuf[0][0][0]);
+  finish((float *)&sbuf[0][0][0], true);
 }
 
 }  // namespace
