@@ -153,9 +153,11 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmArgs args) {
     // the buffer of stage kt-1 for the next issue; the asm keeps the compiler
     // from moving LDS accesses across it
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE) : "memory");
-    issue(kt + NS - 1);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
+      // the DMA issues (which stall the wave) go after the first k-step's
+      // fragment reads and MFMAs are queued
+      if (ks == 1) issue(kt + NS - 1);
       const int chunk = ks * 2 + g;
       u32x4 fa[WTM], fb[WTN];
 #pragma unroll
