@@ -309,6 +309,25 @@ def test_fa_prefill_vs_oracle(hip, B, oracle, Bn, Hq, Hkv, S, causal):
     attention_gate(got, oracle.bf16_to_f32(ref).reshape(ref.shape), what="FA vs oracle")
 
 
+@pytest.mark.parametrize("Bn,Hq,Hkv,Sq,Skv,causal", [(1, 4, 2, 256, 448, True), (2, 2, 2, 128, 320, False),
+                                                     (1, 2, 1, 384, 640, True)])
+def test_fa_prefill_longer_kv_vs_oracle(hip, B, oracle, Bn, Hq, Hkv, Sq, Skv, causal):
+    """kv_len above q_len (a cached prefix): an odd number of 64-key blocks, so
+    the two key halves of a phase get unequal block counts; causal masking is
+    aligned at key 0 (key j visible to query i iff j <= i), as in the oracle."""
+    say("fa prefill longer kv", Bn, Hq, Hkv, Sq, Skv, causal)
+    rng = np.random.default_rng(Sq * 7 + Skv + causal)
+    D = 128
+    q = _bf16_randn(oracle, rng, (Bn, Hq, Sq, D))
+    k, v = (_bf16_randn(oracle, rng, (Bn, Hkv, Skv, D)) for _ in range(2))
+    scale = 1.0 / math.sqrt(D)
+    ref = oracle.attention_prefill(q, k, v, scale, causal=causal, block_k=64)
+    o = torch.zeros((Bn, Hq, Sq, D), dtype=torch.int16, device="cuda")
+    hip.attention_prefill(u16(q), u16(k), u16(v), o, scale, causal=causal)
+    got = oracle.bf16_to_f32(from_u16(o)).reshape(o.shape)
+    attention_gate(got, oracle.bf16_to_f32(ref).reshape(ref.shape), what="FA (longer kv) vs oracle")
+
+
 def test_fa_prefill_baseline_config(hip, B, oracle):
     """[1,16,2048,128] bf16 causal.  All heads against a
     torch float32 attention on the GPU (independent check); two heads
