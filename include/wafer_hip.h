@@ -197,8 +197,9 @@ int wafer_hip_unpack(wafer_hip_context *ctx, uint32_t format, uint32_t layout,
  * acc = acc*alpha + bf16(P).V, out = narrow(acc * (1/l)).
  * q [batch, q_heads, q_len, head_dim], k/v [batch, kv_heads, kv_len, head_dim],
  * o like q; q_heads % kv_heads == 0 (GQA: q head h reads kv head
- * h / (q_heads/kv_heads)).  Causal: query i sees key j iff j <= i.
- * format BF16; head_dim 128; q_len a multiple of 128, kv_len of 64. */
+ * h / (q_heads/kv_heads)).  Causal: query i sees key j iff j <= i (and
+ * j < kv_len).  format BF16; head_dim 128; any q_len, kv_len >= 1 (kv_len up
+ * to 8388607). */
 int wafer_hip_attention_prefill(wafer_hip_context *ctx, uint32_t format,
                                 const void *q, const void *k, const void *v,
                                 void *o, uint32_t batch, uint32_t q_heads,

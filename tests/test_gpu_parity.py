@@ -328,6 +328,34 @@ def test_fa_prefill_longer_kv_vs_oracle(hip, B, oracle, Bn, Hq, Hkv, Sq, Skv, ca
     attention_gate(got, oracle.bf16_to_f32(ref).reshape(ref.shape), what="FA (longer kv) vs oracle")
 
 
+@pytest.mark.parametrize("Bn,Hq,Hkv,Sq,Skv,causal", [(1, 2, 2, 200, 200, True), (1, 3, 1, 77, 77, True),
+                                                     (2, 2, 2, 130, 250, False), (1, 1, 1, 1, 1, True),
+                                                     (1, 2, 1, 300, 100, True), (1, 1, 1, 64, 1000, False),
+                                                     (1, 2, 2, 1000, 1000, True), (1, 2, 1, 17, 33, False)])
+def test_fa_prefill_ragged_vs_oracle(hip, B, oracle, Bn, Hq, Hkv, Sq, Skv, causal):
+    """Lengths that are not multiples of the 64-query / 64-key blocks: partial
+    last query block (rows past q_len computed on a clamped row and never
+    stored), partial last key block (zero-filled by the block's buffer range
+    and masked), an odd number of query blocks (the middle block served alone),
+    single-token sequences, and causal with kv_len below q_len (key j visible
+    to query i iff j <= i and j < kv_len)."""
+    say("fa prefill ragged", Bn, Hq, Hkv, Sq, Skv, causal)
+    rng = np.random.default_rng(Sq * 13 + Skv * 3 + causal)
+    D = 128
+    q = _bf16_randn(oracle, rng, (Bn, Hq, Sq, D))
+    k, v = (_bf16_randn(oracle, rng, (Bn, Hkv, Skv, D)) for _ in range(2))
+    scale = 1.0 / math.sqrt(D)
+    ref = oracle.attention_prefill(q, k, v, scale, causal=causal, block_k=64)
+    # a canary row after the output: the kernel must not write past q_len
+    n_out = Bn * Hq * Sq * D
+    buf = torch.full((n_out + D,), 0x1234, dtype=torch.int16, device="cuda")
+    hip.attention_prefill(u16(q), u16(k), u16(v), buf[:n_out].view(Bn, Hq, Sq, D), scale, causal=causal)
+    oh = host(buf)
+    got = oracle.bf16_to_f32(oh[:n_out].copy().view(np.uint16)).reshape(Bn, Hq, Sq, D)
+    attention_gate(got, oracle.bf16_to_f32(ref).reshape(ref.shape), what="FA (ragged) vs oracle")
+    assert (oh[n_out:] == 0x1234).all()
+
+
 def test_fa_prefill_baseline_config(hip, B, oracle):
     """[1,16,2048,128] bf16 causal.  All heads against a
     torch float32 attention on the GPU (independent check); two heads

@@ -17,8 +17,11 @@
 //  * a workgroup (8 waves) serves two 64-query blocks of one (batch, head):
 //    block n-1-i (phase A) and then block i (phase B) of the causal
 //    triangle, so every workgroup does the same amount of work (n-i + i+1
-//    key blocks) and one launch of heads*n/2 workgroups fills the CUs evenly
-//    with no cross-workgroup merge;
+//    key blocks) and one launch of heads*ceil(n/2) workgroups fills the CUs
+//    evenly with no cross-workgroup merge (an odd n leaves the middle block
+//    alone in its workgroup).  Partial last blocks: padding queries load a
+//    clamped row and are not stored; keys past kv_len read as zero (each
+//    block's buffer resource is sized to its rows) and are masked;
 //  * wave w: query tile w&3 (16 queries of the current block), key half
 //    w>>2 (the even or the odd 64-key blocks).  All 8 waves work on the same
 //    query block, so each SIMD always carries two equally long chains whose
@@ -123,21 +126,25 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qt = wave & 3, half = wave >> 2;
   const int l16 = lane & 15, g = lane >> 4;
-  // phase A serves the late query block, phase B the early one
-  const int qb_a = CAUSAL ? n_qblocks - 1 - pair : 2 * pair + 1;
-  const int qb_b = CAUSAL ? pair : 2 * pair;
-  const int kv_blocks = kv_len / BK;
+  // phase A serves the late query block n-1-pair, phase B the early one
+  // `pair` (none when they coincide: the middle block of an odd count).  The
+  // last query block and the last key block may be partial.
+  const int qb_a = n_qblocks - 1 - pair;
+  const int qb_b = pair;
+  const int kv_blocks = (kv_len + BK - 1) / BK;
   const int nk_a = CAUSAL ? min(kv_blocks, qb_a + 1) : kv_blocks;
-  const int nk_b = CAUSAL ? min(kv_blocks, qb_b + 1) : kv_blocks;
+  const int nk_b = qb_b < qb_a ? (CAUSAL ? min(kv_blocks, qb_b + 1) : kv_blocks) : 0;
   const int ta = (nk_a + 1) / 2, niter = ta + (nk_b + 1) / 2;
 
   // Q^T as the MFMA B operand: lane holds query l16, d = 32 s + 8 g + [0,8)
+  // (rows past q_len load the last row and are never stored)
   bf16x8 qreg[4];
   int q0 = qb_a * QB + qt * 16;
   auto load_q = [&]() __attribute__((always_inline)) {
+    const int row = min(q0 + l16, q_len - 1);
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      qreg[s] = *(const bf16x8 *)(Qp + (size_t)(q0 + l16) * D + s * 32 + g * 8);
+      qreg[s] = *(const bf16x8 *)(Qp + (size_t)row * D + s * 32 + g * 8);
   };
   load_q();
 
@@ -148,10 +155,13 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
   // swz(row) = 2 (row & 7) = 8 (j & 1) + 2 (lane >> 4), which keeps the K
   // fragment reads (ds_read_b128) and the transposed V reads
   // (ds_read_b64_tr_b16) free of bank conflicts.
-  const __amdgpu_buffer_rsrc_t krsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void *)Kp, 0, (int)(kv_len * D * 2), 0x00020000);
-  const __amdgpu_buffer_rsrc_t vrsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void *)Vp, 0, (int)(kv_len * D * 2), 0x00020000);
+  // One buffer resource per block, based at the block and sized to its rows
+  // (the hardware range check covers the lane offset, not the scalar one), so
+  // rows of a partial last block past kv_len read as zero.
+  auto block_rsrc = [&](const uint16_t *base, int kb) __attribute__((always_inline)) {
+    const int rows = min(BK, kv_len - kb * BK);
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(base + (size_t)kb * BK * D), 0, rows * D * 2, 0x00020000);
+  };
   uint32_t dma_off[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j)
@@ -163,20 +173,20 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     return t < ta ? min(2 * t + half, nk_a - 1) : min(2 * (t - ta) + half, nk_b - 1);
   };
   auto dma_k = [&](int kb, int buf) __attribute__((always_inline)) {
-    const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane(kb * BK * D * 2);
+    const __amdgpu_buffer_rsrc_t rsrc = block_rsrc(Kp, __builtin_amdgcn_readfirstlane(kb));
     uint16_t *dk = sbuf[buf][half] + qt * 4 * 512;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(krsrc, (__attribute__((address_space(3))) void *)(dk + j * 512), 16,
-                                               dma_off[j], so, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)(dk + j * 512), 16,
+                                               dma_off[j], 0, 0, 0);
   };
   auto dma_v = [&](int kb, int buf) __attribute__((always_inline)) {
-    const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane(kb * BK * D * 2);
+    const __amdgpu_buffer_rsrc_t rsrc = block_rsrc(Vp, __builtin_amdgcn_readfirstlane(kb));
     uint16_t *dv = sbuf[buf][2 + half] + qt * 4 * 512;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrsrc, (__attribute__((address_space(3))) void *)(dv + j * 512), 16,
-                                               dma_off[j], so, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)(dv + j * 512), 16,
+                                               dma_off[j], 0, 0, 0);
   };
 
   // LDS read offsets (bytes within a 16 KiB block), per lane:
@@ -246,12 +256,15 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     __builtin_amdgcn_sched_group_barrier(SG_MFMA, 16, 0);
     __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 32, 0);
     __builtin_amdgcn_sched_group_barrier(SG_VMEM, 4, 0);
-    if (CAUSAL && kb * BK + BK - 1 > q0) {
+    // key kb*BK + kt*16 + 4 g + j is visible to query q0 + l16 iff it is
+    // below kv_len and (causal) not past the query
+    if ((CAUSAL && kb * BK + BK - 1 > q0) || kb * BK + BK > kv_len) {
+      const int lim = CAUSAL ? min(q0 + l16, kv_len - 1) : kv_len - 1;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          if (kb * BK + kt * 16 + 4 * g + j > q0 + l16) sacc[kt][j] = -__builtin_inff();
+          if (kb * BK + kt * 16 + 4 * g + j > lim) sacc[kt][j] = -__builtin_inff();
     }
     f32x4 p[4];
     float rs[4];
@@ -349,7 +362,7 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
       u32x2 packed;
       packed[0] = (uint32_t)f32_to_bf16(r[0]) | ((uint32_t)f32_to_bf16(r[1]) << 16);
       packed[1] = (uint32_t)f32_to_bf16(r[2]) | ((uint32_t)f32_to_bf16(r[3]) << 16);
-      *(u32x2 *)(orow + dt * 16) = packed;
+      if (q0 + l16 < q_len) *(u32x2 *)(orow + dt * 16) = packed;
     }
     if (!last) lds_barrier();  // exchange reads done before the buffers are reused
     // a distinct marker per half: keeps the two copies from being merged
@@ -391,7 +404,7 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (t == ta - 1) {
+    if (t == ta - 1 && niter > ta) {
       finish((float *)&sbuf[P][0][0], false);  // 64 KiB, free until the next DMA
       q0 = qb_b * QB + qt * 16;
       load_q();
@@ -431,20 +444,17 @@ extern "C" int wafer_hip_attention_prefill(wafer_hip_context *ctx, uint32_t form
     return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill: empty dimension");
   if (q_heads % kv_heads != 0)
     return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill: q_heads % kv_heads != 0");
-  if (q_len % (2 * QB) != 0 || kv_len % BK != 0)
-    return fail(WAFER_HIP_E_UNSUPPORTED, "attention_prefill: q_len must be a multiple of 128 and kv_len of 64");
-  if (causal && kv_len < q_len)
-    return fail(WAFER_HIP_E_UNSUPPORTED, "attention_prefill: causal needs kv_len >= q_len");
   if (!(scale > 0.0f)) return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill: scale must be positive");
   if ((uint64_t)kv_len * D * 2 > 0x7fffffffull)  // 32-bit buffer offsets of one head's K/V
     return fail(WAFER_HIP_E_UNSUPPORTED, "attention_prefill: kv_len too large (max 8388607)");
-  if ((uint64_t)batch * q_heads * (q_len / (2 * QB)) > 0x7fffffffull)
+  const uint64_t n_qblocks64 = (q_len + QB - 1) / QB;
+  if ((uint64_t)batch * q_heads * ((n_qblocks64 + 1) / 2) > 0x7fffffffull)
     return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill: grid too large");
   WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
-  const int n_qblocks = (int)(q_len / QB);
+  const int n_qblocks = (int)n_qblocks64;
   const int bh_count = (int)(batch * q_heads);
   const float c = scale * 0x1.715476p+0f;
-  dim3 grid((unsigned)(bh_count * (n_qblocks / 2)));
+  dim3 grid((unsigned)(bh_count * ((n_qblocks + 1) / 2)));  // one workgroup per pair of query blocks
   if (causal)
     hipLaunchKernelGGL(fa_prefill_bf16_d128<true>, grid, dim3(THREADS), 0, ctx->stream,
                        (const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)v, (uint16_t *)o,
