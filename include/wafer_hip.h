@@ -124,8 +124,8 @@ int wafer_hip_gemm(wafer_hip_context *ctx, const void *lhs, const void *rhs,
  * The throughput path for large region-level GEMMs.  Same operand meaning as
  * wafer_hip_gemm with lhs Normal; the MFMA accumulation order differs from
  * the formal k-order, so results match the formal lane within tolerance.
- * out_format F32 or the input format.  m, n multiples of 256 / 128 and k a
- * multiple of 64 are served; other shapes return WAFER_HIP_E_UNSUPPORTED. */
+ * out_format F32 or the input format.  Any m, n; k a multiple of 32 (64-byte
+ * K stages); other k return WAFER_HIP_E_UNSUPPORTED. */
 int wafer_hip_gemm_mfma(wafer_hip_context *ctx, const void *lhs,
                         const void *rhs, void *dst, uint32_t m, uint32_t k,
                         uint32_t n, uint32_t in_format, uint32_t out_format,
@@ -139,7 +139,8 @@ int wafer_hip_gemm_mfma(wafer_hip_context *ctx, const void *lhs,
  * y = bf16_RNE(f32_RNE(f32_RNE(acc) * scale[n])) (int32_fp32 route, CT Mul,
  * fp32_bf16 route; lib/Wafer/Target/TargetFormat.cpp:174,192).
  * a [m,k] i8, b [k,n] i8 (Transpose: [n,k]), scale [n] f32, y [m,n] bf16;
- * acc_out [m,n] i32 may be NULL.  k <= 133152 keeps |acc| < 2^31. */
+ * acc_out [m,n] i32 may be NULL.  Any m, n; k a multiple of 64 and at most
+ * 131071 (|acc| <= k*128*128 < 2^31); other k are rejected. */
 int wafer_hip_gemm_i8(wafer_hip_context *ctx, const int8_t *a, const int8_t *b,
                       const float *scale, int32_t *acc_out, uint16_t *y,
                       uint32_t m, uint32_t k, uint32_t n,

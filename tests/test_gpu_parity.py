@@ -262,6 +262,30 @@ def test_i8_gemm_baseline_size_rows(hip, B, oracle):
     assert np.array_equal(accg.astype(np.int64).sum(0), colsum)
 
 
+@pytest.mark.parametrize("m,k,n,rt", [(100, 192, 130, 0), (1, 64, 1, 1), (300, 128, 257, 0), (129, 256, 200, 1),
+                                      (257, 64, 128, 0), (130, 320, 384, 1), (64, 128, 1000, 0)])
+def test_i8_gemm_ragged_bit_exact(hip, B, oracle, m, k, n, rt):
+    """m, n that the 128x128 tiles do not divide (the last tile row / column
+    re-reads its last real operand row and stores only real outputs), and the
+    bounds-checked re-layout for n that the tiled transpose does not divide.
+    Outputs live in flat buffers with a canary tail that must stay intact."""
+    say("i8 gemm ragged", m, k, n, rt)
+    rng = np.random.default_rng(3 * m + 5 * k + 7 * n + rt)
+    a = rng.integers(-128, 128, size=(m, k), dtype=np.int64).astype(np.int8)
+    b = rng.integers(-128, 128, size=(k, n), dtype=np.int64).astype(np.int8)
+    bb = np.ascontiguousarray(b.T) if rt else b
+    scale = rng.uniform(0.001, 0.01, size=n).astype(np.float32)
+    acc_ref, y_ref = oracle.gemm_i8(a, bb, scale, m, k, n, rhs_t=bool(rt))
+    pad = 4096
+    acc = torch.full((m * n + pad,), 0x5A5A5A5A, dtype=torch.int32, device="cuda")
+    y = torch.full((m * n + pad,), 0x1234, dtype=torch.int16, device="cuda")
+    hip.gemm_i8(dev(a), dev(bb), dev(scale), y, m, k, n, acc_out=acc, rhs_t=bool(rt))
+    ga, gy = host(acc), host(y).view(np.uint16)
+    assert np.array_equal(ga[:m * n].reshape(m, n), acc_ref)
+    assert np.array_equal(gy[:m * n].reshape(m, n), y_ref)
+    assert np.all(ga[m * n:] == 0x5A5A5A5A) and np.all(gy[m * n:] == 0x1234)
+
+
 # ------------------------------------------------------------------ MFMA bf16 GEMM
 @pytest.mark.parametrize("m,k,n,rt,fmt", [(256, 512, 256, 0, 3), (128, 256, 384, 1, 3), (512, 1024, 512, 0, 2),
                                           (1024, 4096, 1024, 1, 3)])
@@ -287,6 +311,38 @@ def test_mfma_gemm_vs_formal(hip, B, oracle, m, k, n, rt, fmt):
     gf = oracle.to_float(fmt, gn).reshape(m, n)
     rel = np.linalg.norm(gf - ref) / np.linalg.norm(ref)
     assert rel <= 2e-3 and np.abs(gf - ref).max() <= 2e-2 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("m,k,n,rt,fmt", [(100, 96, 130, 0, 3), (1, 32, 1, 1, 2), (300, 256, 257, 1, 3),
+                                          (77, 512, 384, 0, 2), (200, 160, 72, 0, 3), (513, 64, 129, 1, 3)])
+def test_mfma_gemm_ragged_vs_formal(hip, B, oracle, m, k, n, rt, fmt):
+    """m, n that the 128x128 tiles do not divide, with canary tails after the
+    outputs; same tolerances as the aligned cases."""
+    say("mfma gemm ragged", m, k, n, rt, fmt)
+    rng = np.random.default_rng(11 * m + 13 * k + n + rt)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = (rng.standard_normal((k, n)) / math.sqrt(k)).astype(np.float32)
+    if fmt == B.BF16:
+        ah, bh = oracle.f32_to_bf16(a).reshape(a.shape), oracle.f32_to_bf16(b).reshape(b.shape)
+    else:
+        ah, bh = a.astype(np.float16).view(np.uint16), b.astype(np.float16).view(np.uint16)
+    bt = np.ascontiguousarray(bh.T) if rt else bh
+    ref = oracle.gemm_formal(fmt, oracle.F32, ah, bt, m, k, n, rhs_t=bool(rt)).reshape(m, n)
+    pad = 2048
+    out = torch.full((m * n + pad,), 7.5, dtype=torch.float32, device="cuda")
+    hip.gemm_mfma(u16(ah), u16(bt), out, m, k, n, in_fmt=fmt, out_fmt=B.F32, rhs_t=bool(rt))
+    go = host(out)
+    got = go[:m * n].reshape(m, n)
+    rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert rel <= 1e-5 and np.abs(got - ref).max() <= 1e-4 * np.abs(ref).max()
+    assert np.all(go[m * n:] == 7.5)
+    outn = torch.full((m * n + pad,), 0x1234, dtype=torch.int16, device="cuda")
+    hip.gemm_mfma(u16(ah), u16(bt), outn, m, k, n, in_fmt=fmt, out_fmt=fmt, rhs_t=bool(rt))
+    gn = host(outn).view(np.uint16)
+    gf = oracle.to_float(fmt, gn[:m * n]).reshape(m, n)
+    rel = np.linalg.norm(gf - ref) / np.linalg.norm(ref)
+    assert rel <= 2e-3 and np.abs(gf - ref).max() <= 2e-2 * np.abs(ref).max()
+    assert np.all(gn[m * n:] == 0x1234)
 
 
 # ------------------------------------------------------------------ attention
@@ -599,8 +655,15 @@ def test_invalid_arguments_fail_without_launch(hip, B):
     assert e.value.status == -3  # head_dim 16 is not served
     with pytest.raises(B.WaferHipError):
         hip.gemm(t, t, t, 0, 1, 1)
-    with pytest.raises(B.WaferHipError):
+    with pytest.raises(ValueError):  # operands smaller than the shape: caught before the C call
         hip.gemm_i8(t, t, t, t, 100, 64, 128)
+    big = torch.zeros(4096, dtype=torch.int16, device="cuda")
+    with pytest.raises(B.WaferHipError) as e:
+        hip.gemm_i8(big, big, big, big, 1, 100, 1)
+    assert e.value.status == -3  # k not a multiple of one 64-byte stage
+    with pytest.raises(B.WaferHipError) as e:
+        hip.gemm_mfma(big, big, big, 1, 40, 1)
+    assert e.value.status == -3
 
 
 def test_split_state_counters_rearm(hip, B, oracle):

@@ -162,6 +162,18 @@ def _p(t):
     return ctypes.c_void_p(t.data_ptr())
 
 
+def _fits(what, *pairs):
+    """Raise before any launch when a tensor is smaller than its operand:
+    the C ABI takes bare pointers and cannot check extents itself."""
+    for t, nbytes in pairs:
+        if t is not None and t.numel() * t.element_size() < nbytes:
+            raise ValueError(f"{what}: a tensor holds {t.numel() * t.element_size()} bytes, "
+                             f"the shape needs {nbytes}")
+
+
+_GEMM_ESIZE = {F16: 2, BF16: 2, F32: 4}
+
+
 def _shape(shape):
     arr = (ctypes.c_int64 * max(len(shape), 1))(*[int(s) for s in shape])
     return arr, len(shape)
@@ -214,15 +226,21 @@ class Context:
     # ---- per-command lane ------------------------------------------------------
     def gemm(self, lhs, rhs, dst, m, k, n, batch=1, in_fmt=F32, out_fmt=F32, psum=None,
              lhs_t=False, rhs_t=False):
+        ei, eo = _GEMM_ESIZE.get(in_fmt), _GEMM_ESIZE.get(out_fmt)
+        if ei and eo:  # other formats are rejected by the library before any launch
+            _fits("gemm", (lhs, batch * m * k * ei), (rhs, batch * k * n * ei), (dst, batch * m * n * eo),
+                  (psum, batch * m * n * 4))
         _check(self._L.wafer_hip_gemm(self._bind(), _p(lhs), _p(rhs), _p(dst), _p(psum), m, k, n,
                                       batch, in_fmt, out_fmt, F32 if psum is not None else PSUM_DISABLED,
                                       int(lhs_t), int(rhs_t)))
 
     def gemm_mfma(self, lhs, rhs, dst, m, k, n, in_fmt=BF16, out_fmt=F32, rhs_t=False):
+        _fits("gemm_mfma", (lhs, m * k * 2), (rhs, k * n * 2), (dst, m * n * (4 if out_fmt == F32 else 2)))
         _check(self._L.wafer_hip_gemm_mfma(self._bind(), _p(lhs), _p(rhs), _p(dst), m, k, n, in_fmt,
                                            out_fmt, int(rhs_t)))
 
     def gemm_i8(self, a, b, scale, y, m, k, n, acc_out=None, rhs_t=False):
+        _fits("gemm_i8", (a, m * k), (b, k * n), (scale, n * 4), (y, m * n * 2), (acc_out, m * n * 4))
         _check(self._L.wafer_hip_gemm_i8(self._bind(), _p(a), _p(b), _p(scale), _p(acc_out), _p(y),
                                          m, k, n, int(rhs_t)))
 

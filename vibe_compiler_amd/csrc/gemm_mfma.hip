@@ -67,10 +67,14 @@ struct GemmArgs {
   int32_t *acc_out;    // int8 only, optional [M, N]
   const float *scale;  // int8 only, [N]
   int m, n, kbytes;    // K in bytes
-  int tiles_n;         // N / BN
+  int tiles_m, tiles_n;  // ceil(M / BM), ceil(N / BN)
 };
 
-template <int KIND, int BM, int BN, int OUT>
+// TAIL: the grid's last tile row / column may hold fewer than BM / BN rows /
+// columns.  Those tiles load their last real A row (Bt row) again in place of
+// the missing ones, so every load stays inside the operands, and store only
+// the outputs that exist.
+template <int KIND, int BM, int BN, int OUT, bool TAIL>
 __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmArgs args) {
   // 8 waves as 2 (M) x 4 (N); each wave owns a (BM/2) x (BN/4) sub-tile
   constexpr int NT = 512, WM = 2, WN = 4;
@@ -80,7 +84,7 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmArgs args) {
 
   // XCD-aware tile order: ids are dealt round-robin over 8 XCDs; the ids one
   // XCD receives cover a 4 x 8 block of output tiles when the grid allows it.
-  const int tiles_m = args.m / BM, tiles_n = args.tiles_n;
+  const int tiles_m = args.tiles_m, tiles_n = args.tiles_n;
   int tm, tn;
   {
     const int bid = blockIdx.x;
@@ -129,6 +133,9 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmArgs args) {
   const uint8_t *abase = args.a + (size_t)m0 * kb;
   const uint8_t *bbase = args.bt + (size_t)n0 * kb;
   const int dma_row = lane >> 2, dma_pos = lane & 3;
+  // last row of the tile that exists in A / Bt (BM - 1 / BN - 1 unless TAIL)
+  const int last_a = TAIL ? min(BM, args.m - m0) - 1 : BM - 1;
+  const int last_b = TAIL ? min(BN, args.n - n0) - 1 : BN - 1;
   auto issue = [&](int kt) __attribute__((always_inline)) {
     const int st = kt % NS;
     const uint32_t koff = (uint32_t)min(kt, nkt - 1) * BKB;
@@ -138,7 +145,8 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmArgs args) {
       const bool is_a = ins < A_INSTR;
       const int row = (is_a ? ins : ins - A_INSTR) * 16 + dma_row;
       const int chunk = swz(row, dma_pos);  // swz is an involution on the chunk index
-      const uint8_t *src = (is_a ? abase : bbase) + (row * kb32 + koff + chunk * 16);
+      const int src_row = TAIL ? min(row, is_a ? last_a : last_b) : row;
+      const uint8_t *src = (is_a ? abase : bbase) + (src_row * kb32 + koff + chunk * 16);
       u32x4 *dst = is_a ? &sA[st][(ins * 16) * 4] : &sB[st][((ins - A_INSTR) * 16) * 4];
       __builtin_amdgcn_global_load_lds((const void *)src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
     }
@@ -185,11 +193,13 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmArgs args) {
 #pragma unroll
     for (int j = 0; j < WTN; ++j) {
       const int col = n0 + wn * (BN / WN) + j * 32 + l32;
+      const bool col_ok = !TAIL || col < args.n;
       float sc = 0.0f;
-      if (OUT == OUT_I8_DEQUANT) sc = args.scale[col];
+      if (OUT == OUT_I8_DEQUANT && col_ok) sc = args.scale[col];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (TAIL && !(col_ok && row < args.m)) continue;
         const size_t o = (size_t)row * args.n + col;
         if (OUT == OUT_F32) {
           ((float *)args.y)[o] = (float)acc[i][j][r];
@@ -282,16 +292,40 @@ __global__ __launch_bounds__(128) void transpose_b16_kernel(const uint16_t *__re
   }
 }
 
+// Re-layout for an N that the tiled kernels above do not divide (their
+// 16-byte row loads also need N * element bytes to be a multiple of 16): a
+// 32 x 32 element tile through LDS with every access bounds-checked.
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_any_kernel(const T *__restrict__ src, T *__restrict__ dst,
+                                                            int K, int N) {
+  __shared__ T tile[32][33];
+  const int k0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+#pragma unroll
+  for (int i = ty; i < 32; i += 8)
+    if (k0 + i < K && n0 + tx < N) tile[i][tx] = src[(size_t)(k0 + i) * N + n0 + tx];
+  __syncthreads();
+#pragma unroll
+  for (int i = ty; i < 32; i += 8)
+    if (n0 + i < N && k0 + tx < K) dst[(size_t)(n0 + i) * K + k0 + tx] = tile[tx][i];
+}
+
 template <int KIND, int OUT>
-int launch_gemm(hipStream_t st, GemmArgs args, int ctas_256) {
-  if (args.m % 256 == 0 && args.n % 256 == 0 && ctas_256 >= 192) {
+int launch_gemm(hipStream_t st, GemmArgs args) {
+  // 256x256 tiles only where they divide the output and still fill the chip
+  if (args.m % 256 == 0 && args.n % 256 == 0 && (args.m / 256) * (args.n / 256) >= 192) {
+    args.tiles_m = args.m / 256;
     args.tiles_n = args.n / 256;
-    dim3 grid((args.m / 256) * args.tiles_n);
-    hipLaunchKernelGGL((gemm_nt_kernel<KIND, 256, 256, OUT>), grid, dim3(512), 0, st, args);
+    hipLaunchKernelGGL((gemm_nt_kernel<KIND, 256, 256, OUT, false>), dim3(args.tiles_m * args.tiles_n),
+                       dim3(512), 0, st, args);
   } else {
-    args.tiles_n = args.n / 128;
-    dim3 grid((args.m / 128) * args.tiles_n);
-    hipLaunchKernelGGL((gemm_nt_kernel<KIND, 128, 128, OUT>), grid, dim3(512), 0, st, args);
+    args.tiles_m = (args.m + 127) / 128;
+    args.tiles_n = (args.n + 127) / 128;
+    const dim3 grid(args.tiles_m * args.tiles_n);
+    if (args.m % 128 == 0 && args.n % 128 == 0)
+      hipLaunchKernelGGL((gemm_nt_kernel<KIND, 128, 128, OUT, false>), grid, dim3(512), 0, st, args);
+    else
+      hipLaunchKernelGGL((gemm_nt_kernel<KIND, 128, 128, OUT, true>), grid, dim3(512), 0, st, args);
   }
   return launch_status("gemm_nt_kernel");
 }
@@ -299,10 +333,22 @@ int launch_gemm(hipStream_t st, GemmArgs args, int ctas_256) {
 int relayout_rhs(wafer_hip_context *ctx, const void *rhs, uint32_t k, uint32_t n, int esize,
                  const uint8_t **bt) {
   const size_t need = (size_t)k * n * esize;
+  // the transposes put K blocks of 32 or more on grid y (at most 65535)
+  if ((k + 31) / 32 > 65535)
+    return fail(WAFER_HIP_E_INVALID_FIELD, "gemm: k above 2097120 with a [K,N] rhs; pass the [N,K] form");
   WAFER_TRY(ensure_workspace(ctx, &ctx->relayout, &ctx->relayout_bytes, need));
-  // check_shape guarantees n % 128 == 0 and k a multiple of 64 (int8) or
-  // 32 (16-bit), so every tile is full
-  if (esize == 1)
+  // check_shape guarantees k a multiple of 64 (int8) or 32 (16-bit); the
+  // tiled kernels also need n a multiple of their 128 / 64 columns
+  const int tile_n = esize == 1 ? 128 : 64;
+  if (n % tile_n) {
+    const dim3 grid((n + 31) / 32, (k + 31) / 32);
+    if (esize == 1)
+      hipLaunchKernelGGL(transpose_any_kernel<uint8_t>, grid, dim3(256), 0, ctx->stream, (const uint8_t *)rhs,
+                         (uint8_t *)ctx->relayout, (int)k, (int)n);
+    else
+      hipLaunchKernelGGL(transpose_any_kernel<uint16_t>, grid, dim3(256), 0, ctx->stream, (const uint16_t *)rhs,
+                         (uint16_t *)ctx->relayout, (int)k, (int)n);
+  } else if (esize == 1)
     hipLaunchKernelGGL(transpose_i8_kernel, dim3(n / 128, k / 64), dim3(128), 0, ctx->stream,
                        (const uint8_t *)rhs, (uint8_t *)ctx->relayout, (int)k, (int)n);
   else
@@ -315,9 +361,11 @@ int relayout_rhs(wafer_hip_context *ctx, const void *rhs, uint32_t k, uint32_t n
 
 int check_shape(uint32_t m, uint32_t k, uint32_t n, int esize, const char *what) {
   if (m == 0 || k == 0 || n == 0) return fail(WAFER_HIP_E_INVALID_FIELD, std::string(what) + ": empty dimension");
-  if (m % 128 || n % 128 || ((uint64_t)k * esize) % BKB)
-    return fail(WAFER_HIP_E_UNSUPPORTED,
-                std::string(what) + ": needs m, n multiples of 128 and k*elem_bytes a multiple of 64");
+  if (((uint64_t)k * esize) % BKB)
+    return fail(WAFER_HIP_E_UNSUPPORTED, std::string(what) + ": needs k*elem_bytes a multiple of 64");
+  // m, n are kernel ints; the grid is one dimension of 128x128 tiles
+  if (m > 0x7fffffffu || n > 0x7fffffffu || (uint64_t)((m + 127) / 128) * ((n + 127) / 128) > 0x7fffffffull)
+    return fail(WAFER_HIP_E_INVALID_FIELD, std::string(what) + ": output too large");
   // in-tile offsets (row * k * esize over 256 rows) are 32-bit
   if ((uint64_t)m * k * esize > 0x7fffffffffull || (uint64_t)k * esize >= (1u << 24))
     return fail(WAFER_HIP_E_INVALID_FIELD, std::string(what) + ": operand too large (k * element bytes must be below 16 MiB)");
@@ -344,14 +392,13 @@ extern "C" int wafer_hip_gemm_mfma(wafer_hip_context *ctx, const void *lhs, cons
   WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
   const uint8_t *bt = (const uint8_t *)rhs;
   if (rhs_orientation == WAFER_GEMM_NORMAL) WAFER_TRY(relayout_rhs(ctx, rhs, k, n, 2, &bt));
-  GemmArgs args{(const uint8_t *)lhs, bt, dst, nullptr, nullptr, (int)m, (int)n, (int)(k * 2), 0};
-  const int ctas = (int)((m / 256) * (n / 256));
+  GemmArgs args{(const uint8_t *)lhs, bt, dst, nullptr, nullptr, (int)m, (int)n, (int)(k * 2), 0, 0};
   const bool f32 = out_format == WAFER_FMT_F32;
   if (in_format == WAFER_FMT_BF16)
-    return f32 ? launch_gemm<KIND_BF16, OUT_F32>(ctx->stream, args, ctas)
-               : launch_gemm<KIND_BF16, OUT_NARROW>(ctx->stream, args, ctas);
-  return f32 ? launch_gemm<KIND_F16, OUT_F32>(ctx->stream, args, ctas)
-             : launch_gemm<KIND_F16, OUT_NARROW>(ctx->stream, args, ctas);
+    return f32 ? launch_gemm<KIND_BF16, OUT_F32>(ctx->stream, args)
+               : launch_gemm<KIND_BF16, OUT_NARROW>(ctx->stream, args);
+  return f32 ? launch_gemm<KIND_F16, OUT_F32>(ctx->stream, args)
+             : launch_gemm<KIND_F16, OUT_NARROW>(ctx->stream, args);
 }
 
 extern "C" int wafer_hip_gemm_i8(wafer_hip_context *ctx, const int8_t *a, const int8_t *b,
@@ -365,6 +412,6 @@ extern "C" int wafer_hip_gemm_i8(wafer_hip_context *ctx, const int8_t *a, const 
   WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
   const uint8_t *bt = (const uint8_t *)b;
   if (rhs_orientation == WAFER_GEMM_NORMAL) WAFER_TRY(relayout_rhs(ctx, b, k, n, 1, &bt));
-  GemmArgs args{(const uint8_t *)a, bt, y, acc_out, scale, (int)m, (int)n, (int)k, 0};
-  return launch_gemm<KIND_I8, OUT_I8_DEQUANT>(ctx->stream, args, (int)((m / 256) * (n / 256)));
+  GemmArgs args{(const uint8_t *)a, bt, y, acc_out, scale, (int)m, (int)n, (int)k, 0, 0};
+  return launch_gemm<KIND_I8, OUT_I8_DEQUANT>(ctx->stream, args);
 }
