@@ -2,6 +2,7 @@
 """Benchmark of the gfx950 numeric backend on BASELINE.json's headline metric.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fa,fd,i8,mlp,llama,mv,cmp]
+                  (also: copy = counter calibration, vendor = ROCm library kernels for context)
 
 One step = one launch of the hot path over one batch of synthetic, seeded
 input already resident in HBM.  The headline (`value`) is the FA prefill
@@ -339,6 +340,53 @@ def bench_cmp(torch, hip, steps, warmup):
     }
 
 
+def bench_vendor(torch, hip, steps, warmup):
+    """ROCm's own kernels on the same shapes, timed the same way, as context
+    for the roofline fractions (not part of the headline): torch SDPA
+    restricted to its flash / memory-efficient backends (never the math path)
+    for config 1, hipBLASLt through torch.matmul for a bf16 4096^3 GEMM next
+    to this backend's MFMA GEMM, and torch._int_mm for the int8 4096^3
+    product (int32 out, no dequant) next to this backend's int8 GEMM with the
+    rhs already in [N,K] form."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    import torch.nn.functional as F
+    from vibe_compiler_amd.backend import BF16
+
+    gen = torch.Generator(device="cuda").manual_seed(SEED)
+    out = {}
+
+    def record(name, fn, work, unit):
+        try:
+            ms = timed(torch, fn, steps, warmup)
+            out[name] = {"ms": ms, "value": work / (ms * 1e-3) / 1e12, "unit": unit}
+        except Exception as e:  # a backend the installed torch does not offer
+            out[name] = {"error": f"{type(e).__name__}: {str(e)[:160]}"}
+
+    q, k, v = (rnd_bf16(torch, gen, FA_SHAPE) for _ in range(3))
+    scale = 1.0 / math.sqrt(FA_SHAPE[3])
+    for name, be in (("sdpa_flash", SDPBackend.FLASH_ATTENTION), ("sdpa_efficient", SDPBackend.EFFICIENT_ATTENTION)):
+        def fa_fn(be=be):
+            with sdpa_kernel([be]):
+                F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=scale)
+        record(name, fa_fn, FA_FLOPS, "TFLOP/s")
+    del q, k, v
+    n = I8_N
+    a = rnd_bf16(torch, gen, (n, n))
+    b = rnd_bf16(torch, gen, (n, n))
+    bt = b.t().contiguous()
+    y = torch.empty((n, n), dtype=torch.bfloat16, device="cuda")
+    record("hipblaslt_bf16_mm", lambda: torch.matmul(a, b), I8_OPS, "TFLOP/s")
+    record("wafer_bf16_mfma_nt", lambda: hip.gemm_mfma(a, bt, y, n, n, n, in_fmt=BF16, out_fmt=BF16, rhs_t=True),
+           I8_OPS, "TFLOP/s")
+    ai = torch.randint(-127, 128, (n, n), device="cuda", generator=gen, dtype=torch.int8)
+    bi = torch.randint(-127, 128, (n, n), device="cuda", generator=gen, dtype=torch.int8)
+    bit = bi.t().contiguous()
+    sc = torch.rand(n, device="cuda", generator=gen) * 0.009 + 0.001
+    record("torch_int_mm", lambda: torch._int_mm(ai, bi), I8_OPS, "TOP/s")
+    record("wafer_i8_nt", lambda: hip.gemm_i8(ai, bit, sc, y, n, n, n, rhs_t=True), I8_OPS, "TOP/s")
+    return {"workload": "ROCm library kernels on config 1 and 4096^3 GEMM shapes (context only)", **out}
+
+
 def bench_copy(torch, steps, warmup):
     """A plain device copy of known size: the calibration kernel for the
     rocprofv3 FETCH_SIZE / WRITE_SIZE counters (reads and writes COPY_BYTES)."""
@@ -354,7 +402,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="fa,fd,i8,mlp,llama,mv,cmp", help="comma list of fa, fd, i8, mlp, llama, mv, cmp, copy")
+    ap.add_argument("--only", default="fa,fd,i8,mlp,llama,mv,cmp", help="comma list of fa, fd, i8, mlp, llama, mv, cmp, copy, vendor")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -389,6 +437,8 @@ def main() -> int:
         secondary.append(dict(name="comparator", **bench_cmp(torch, hip, args.steps, args.warmup)))
     if "copy" in only:
         secondary.append(dict(name="copy", **bench_copy(torch, args.steps, args.warmup)))
+    if "vendor" in only:
+        secondary.append(dict(name="vendor", **bench_vendor(torch, hip, args.steps, args.warmup)))
     hip.close()
 
     line = {

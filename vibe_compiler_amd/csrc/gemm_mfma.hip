@@ -10,7 +10,9 @@
 // when the 256 grid would leave CUs idle); each wave owns (BM/2) x (BN/4),
 // two waves per SIMD.  64-byte K slices of A and Bt go global -> LDS directly
 // (global_load_lds_dwordx4, no VGPR round trip) into a ring of 4 stage
-// buffers, issued 3 stages ahead; one barrier per stage.  LDS rows are 64 B
+// buffers, issued 3 stages ahead; one barrier per stage, placed between the
+// stage's two k-steps so that each k-step's fragment reads overlap the
+// previous k-step's MFMAs.  LDS rows are 64 B
 // with the 16-byte chunk index XOR-swizzled by ((row >> 2) & 3), so any 16
 // consecutive rows read at one chunk hit 16 distinct bank groups
 // (conflict-free ds_read_b128; SQ_LDS_BANK_CONFLICT reads 0).  A normal
@@ -152,37 +154,75 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmArgs args) {
     }
   };
 
+  auto read_frags = [&](int buf, int ks, u32x4 (&fa)[WTM], u32x4 (&fb)[WTN]) __attribute__((always_inline)) {
+    const int chunk = ks * 2 + g;
+#pragma unroll
+    for (int i = 0; i < WTM; ++i) {
+      const int row = wm * (BM / WM) + i * 32 + l32;
+      fa[i] = sA[buf][row * 4 + swz(row, chunk)];
+    }
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) {
+      const int row = wn * (BN / WN) + j * 32 + l32;
+      fb[j] = sB[buf][row * 4 + swz(row, chunk)];
+    }
+  };
+  auto mfmas = [&](const u32x4 (&fa)[WTM], const u32x4 (&fb)[WTN]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < WTM; ++i)
+#pragma unroll
+      for (int j = 0; j < WTN; ++j) acc[i][j] = mfma<KIND>(fa[i], fb[j], acc[i][j]);
+  };
+
+  // Software pipeline over the two k-steps of a stage, with the stage
+  // barrier between them: the fragment reads of one k-step are issued
+  // between the MFMAs of the previous one, so LDS latency hides behind
+  // matrix work.  sched_barrier fences keep the compiler from moving MFMAs
+  // across the barrier; sched_group_barrier pins the interleave (masks:
+  // 0x008 MFMA, 0x100 LDS read, 0x010 VMEM, which covers the DMA issues).
+  constexpr int NR = WTM + WTN, NV = PER_WAVE;  // fragment reads per k-step, DMA issues per stage
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s) issue(s);
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE) : "memory");
+  u32x4 fa0[WTM], fb0[WTN], fa1[WTM], fb1[WTN];
+  read_frags(0, 0, fa0, fb0);
   for (int kt = 0; kt < nkt; ++kt) {
     const int buf = kt % NS;
-    // own loads of stage kt done (the NS-2 later stages may stay in flight),
-    // then the barrier makes every wave's stage-kt data visible and frees
-    // the buffer of stage kt-1 for the next issue; the asm keeps the compiler
-    // from moving LDS accesses across it
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE) : "memory");
+    // phase 1: k-step 1's fragment reads, then the stage's DMA issues (an
+    // issue stalls the wave), each after one of k-step 0's MFMAs
+    read_frags(buf, 1, fa1, fb1);
+    mfmas(fa0, fb0);
+    // into buffer (kt - 1) % NS, which every wave finished reading before
+    // the last barrier
+    issue(kt + NS - 1);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      // the DMA issues (which stall the wave) go after the first k-step's
-      // fragment reads and MFMAs are queued
-      if (ks == 1) issue(kt + NS - 1);
-      const int chunk = ks * 2 + g;
-      u32x4 fa[WTM], fb[WTN];
-#pragma unroll
-      for (int i = 0; i < WTM; ++i) {
-        const int row = wm * (BM / WM) + i * 32 + l32;
-        fa[i] = sA[buf][row * 4 + swz(row, chunk)];
-      }
-#pragma unroll
-      for (int j = 0; j < WTN; ++j) {
-        const int row = wn * (BN / WN) + j * 32 + l32;
-        fb[j] = sB[buf][row * 4 + swz(row, chunk)];
-      }
-#pragma unroll
-      for (int i = 0; i < WTM; ++i)
-#pragma unroll
-        for (int j = 0; j < WTN; ++j) acc[i][j] = mfma<KIND>(fa[i], fb[j], acc[i][j]);
+    for (int r = 0; r < NR; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    // this wave's stage-(kt+1) loads have landed (the NS-2 later stages may
+    // stay in flight) and its reads of stage kt are complete; after the
+    // barrier stage kt+1 is visible to every wave and buffer kt % NS is free
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE) : "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    // phase 2: stage kt+1's k-step 0 fragment reads between k-step 1's
+    // MFMAs (past the last stage they read a clamped copy, unused)
+    read_frags((kt + 1) % NS, 0, fa0, fb0);
+    mfmas(fa1, fb1);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+    __builtin_amdgcn_sched_barrier(0);
   }
   // the clamped tail loads are still in flight: drain before the LDS goes away
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
