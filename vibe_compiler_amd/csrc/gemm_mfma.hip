@@ -8,21 +8,21 @@
 //   int8:     v_mfma_i32_32x32x32_i8          (32 elements = 32 B of K/step)
 // A workgroup of 8 waves (2 x 4) computes a BMxBN tile (256x256, or 128x128
 // when the 256 grid would leave CUs idle); each wave owns (BM/2) x (BN/4),
-// two waves per SIMD.  64-byte K slices of A and Bt go global -> LDS directly
-// (global_load_lds_dwordx4, no VGPR round trip) into a ring of 4 stage
-// buffers, issued 3 stages ahead; one barrier per stage, placed between the
-// stage's two k-steps so that each k-step's fragment reads overlap the
-// previous k-step's MFMAs.  LDS rows are 64 B
-// with the 16-byte chunk index XOR-swizzled by ((row >> 2) & 3), so any 16
-// consecutive rows read at one chunk hit 16 distinct bank groups
-// (conflict-free ds_read_b128; SQ_LDS_BANK_CONFLICT reads 0).  A normal
+// two waves per SIMD.  K slices of A and Bt (128 bytes per stage when K
+// allows, else 64) go global -> LDS directly (global_load_lds_dwordx4, no
+// VGPR round trip) into a ring of stage buffers filling 128 KiB (2 stages
+// of 128-byte slices for 256x256 tiles, else 4), issued NS-1 stages ahead;
+// one barrier per stage, placed before the stage's last k-step so that each
+// k-step's fragment reads overlap the previous k-step's MFMAs.  The 16-byte
+// chunks of each LDS row are XOR-swizzled so that the rows one fragment
+// read touches hit distinct bank groups (conflict-free ds_read_b128).  A normal
 // (K-major) rhs is first re-laid out to Bt by a transpose kernel into
 // context scratch.  Workgroup ids are mapped so that the 32 tiles served by
 // one XCD form a 4x8 block of the output, bounding that XCD's L2 working set.
 //
 // int8 semantics (no reference implementation exists; the closed form on the
 // reference's conversion routes): acc = sum_k int32(a)*int32(b) exactly
-// (|acc| <= k*127*128 < 2^31 for k <= 131071), y = bf16_RNE(f32_RNE(
+// (|acc| <= k*128*128 < 2^31 for k <= 131071), y = bf16_RNE(f32_RNE(
 // f32_RNE(acc) * scale[n])) -- int32_fp32 route, CT Mul, fp32_bf16 route
 // (lib/Wafer/Target/TargetFormat.cpp:174,192).  Integer sums are
 // order-independent, so the result is bit-exact.
@@ -32,9 +32,7 @@ namespace wafer {
 namespace {
 
 enum { KIND_BF16 = 0, KIND_F16 = 1, KIND_I8 = 2 };
-constexpr int BKB = 64;  // bytes of K per LDS stage (2 MFMA steps)
-
-__device__ inline int swz(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
+constexpr int BKB = 64;  // K bytes must be a multiple of the smaller LDS stage
 
 template <int KIND> struct Acc;
 template <> struct Acc<KIND_BF16> { typedef f32x16 T; };
@@ -76,13 +74,23 @@ struct GemmArgs {
 // columns.  Those tiles load their last real A row (Bt row) again in place of
 // the missing ones, so every load stays inside the operands, and store only
 // the outputs that exist.
-template <int KIND, int BM, int BN, int OUT, bool TAIL>
+template <int KIND, int BM, int BN, int OUT, bool TAIL, int SB>
 __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmArgs args) {
   // 8 waves as 2 (M) x 4 (N); each wave owns a (BM/2) x (BN/4) sub-tile
   constexpr int NT = 512, WM = 2, WN = 4;
   constexpr int WTM = BM / WM / 32, WTN = BN / WN / 32;  // 32x32 MFMA tiles per wave
-  __shared__ __align__(16) u32x4 sA[4][BM * 4];
-  __shared__ __align__(16) u32x4 sB[4][BN * 4];
+  // SB bytes of K per stage (2 or 4 MFMA k-steps); NS stages fill 128 KiB
+  constexpr int CH = SB / 16, KS = SB / 32;
+  constexpr int NS = (128 * 1024) / ((BM + BN) * SB) < 4 ? (128 * 1024) / ((BM + BN) * SB) : 4;
+  static_assert(NS >= 2, "at least two stages");
+  __shared__ __align__(16) u32x4 sA[NS][BM * CH];
+  __shared__ __align__(16) u32x4 sB[NS][BN * CH];
+  // 16-byte chunk c of row r sits at position swz(r, c) (an involution in c):
+  // 16 consecutive rows read at one chunk hit 16 distinct 16-byte bank
+  // groups, and so do 32 consecutive rows for 128-byte rows
+  auto swz = [](int row, int chunk) __attribute__((always_inline)) {
+    return SB == 64 ? chunk ^ ((row >> 2) & 3) : chunk ^ (((row >> 1) ^ (row >> 4)) & 7);
+  };
 
   // XCD-aware tile order: ids are dealt round-robin over 8 XCDs; the ids one
   // XCD receives cover a 4 x 8 block of output tiles when the grid allows it.
@@ -94,13 +102,11 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmArgs args) {
     if (total % 256 == 0 && tiles_m % 4 == 0 && tiles_n % 8 == 0) {
       const int group = bid / 256, inner = bid % 256;  // 256 tiles per round
       const int xcd = inner % 8, j = inner / 8;        // 32 tiles per XCD
-      const int gm = tiles_m / 4, gn = tiles_n / 8;    // 4x8 blocks in the grid
-      const int blocks_per_round = 8;
-      const int blk = group * blocks_per_round + xcd;  // which 4x8 block
+      const int gn = tiles_n / 8;                      // 4x8 blocks across the grid
+      const int blk = group * 8 + xcd;                 // which 4x8 block
       const int bm = blk / gn, bn = blk % gn;
       tm = bm * 4 + j / 8;
       tn = bn * 8 + j % 8;
-      (void)gm;
     } else {
       tm = bid / tiles_n;
       tn = bid % tiles_n;
@@ -122,107 +128,119 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmArgs args) {
 
   // Direct-to-LDS staging: NS stage buffers in a ring, loads issued NS-1
   // stages ahead with global_load_lds_dwordx4 (no VGPR round trip).  One
-  // instruction fills 1 KiB = 16 rows x 4 chunks of a stage buffer: lane l
-  // writes LDS chunk position (l & 3) of row (l >> 2), so it loads the global
-  // chunk that the XOR swizzle maps there.
-  constexpr int NS = 4;
-  constexpr int A_INSTR = BM / 16, B_INSTR = BN / 16;      // 1 KiB DMA per instruction
+  // instruction fills 1 KiB = 1024/SB rows x CH chunks of a stage buffer:
+  // lane l writes LDS chunk position l % CH of row l / CH, so it loads the
+  // global chunk that the swizzle maps there.
+  constexpr int RPI = 1024 / SB;                           // rows per instruction
+  constexpr int A_INSTR = BM / RPI, B_INSTR = BN / RPI;
   constexpr int PER_WAVE = (A_INSTR + B_INSTR) / (NT / 64);
   static_assert((A_INSTR + B_INSTR) % (NT / 64) == 0, "DMA instructions must split evenly over the waves");
   const uint32_t kb32 = (uint32_t)args.kbytes;
-  const int nkt = args.kbytes / BKB;
+  const int nkt = args.kbytes / SB;
   const size_t kb = (size_t)args.kbytes;
   const uint8_t *abase = args.a + (size_t)m0 * kb;
   const uint8_t *bbase = args.bt + (size_t)n0 * kb;
-  const int dma_row = lane >> 2, dma_pos = lane & 3;
+  const int dma_row = lane / CH, dma_pos = lane % CH;
   // last row of the tile that exists in A / Bt (BM - 1 / BN - 1 unless TAIL)
   const int last_a = TAIL ? min(BM, args.m - m0) - 1 : BM - 1;
   const int last_b = TAIL ? min(BN, args.n - n0) - 1 : BN - 1;
-  auto issue = [&](int kt) __attribute__((always_inline)) {
+  // instructions q0 .. q1-1 of this wave's PER_WAVE for stage kt
+  auto issue = [&](int kt, int q0, int q1) __attribute__((always_inline)) {
     const int st = kt % NS;
-    const uint32_t koff = (uint32_t)min(kt, nkt - 1) * BKB;
+    const uint32_t koff = (uint32_t)min(kt, nkt - 1) * SB;
 #pragma unroll
-    for (int q = 0; q < PER_WAVE; ++q) {
+    for (int q = q0; q < q1; ++q) {
       const int ins = wave * PER_WAVE + q;  // 0 .. A_INSTR + B_INSTR - 1
       const bool is_a = ins < A_INSTR;
-      const int row = (is_a ? ins : ins - A_INSTR) * 16 + dma_row;
-      const int chunk = swz(row, dma_pos);  // swz is an involution on the chunk index
+      const int row = (is_a ? ins : ins - A_INSTR) * RPI + dma_row;
+      const int chunk = swz(row, dma_pos);
       const int src_row = TAIL ? min(row, is_a ? last_a : last_b) : row;
       const uint8_t *src = (is_a ? abase : bbase) + (src_row * kb32 + koff + chunk * 16);
-      u32x4 *dst = is_a ? &sA[st][(ins * 16) * 4] : &sB[st][((ins - A_INSTR) * 16) * 4];
+      u32x4 *dst = is_a ? &sA[st][(ins * RPI) * CH] : &sB[st][((ins - A_INSTR) * RPI) * CH];
       __builtin_amdgcn_global_load_lds((const void *)src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
     }
   };
 
-  auto read_frags = [&](int buf, int ks, u32x4 (&fa)[WTM], u32x4 (&fb)[WTN]) __attribute__((always_inline)) {
+  u32x4 fa[2][WTM], fb[2][WTN];  // fragments of two k-steps
+  auto read_frags = [&](int buf, int ks, int f) __attribute__((always_inline)) {
     const int chunk = ks * 2 + g;
 #pragma unroll
     for (int i = 0; i < WTM; ++i) {
       const int row = wm * (BM / WM) + i * 32 + l32;
-      fa[i] = sA[buf][row * 4 + swz(row, chunk)];
+      fa[f][i] = sA[buf][row * CH + swz(row, chunk)];
     }
 #pragma unroll
     for (int j = 0; j < WTN; ++j) {
       const int row = wn * (BN / WN) + j * 32 + l32;
-      fb[j] = sB[buf][row * 4 + swz(row, chunk)];
+      fb[f][j] = sB[buf][row * CH + swz(row, chunk)];
     }
   };
-  auto mfmas = [&](const u32x4 (&fa)[WTM], const u32x4 (&fb)[WTN]) __attribute__((always_inline)) {
+  auto mfmas = [&](int f) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < WTM; ++i)
 #pragma unroll
-      for (int j = 0; j < WTN; ++j) acc[i][j] = mfma<KIND>(fa[i], fb[j], acc[i][j]);
+      for (int j = 0; j < WTN; ++j) acc[i][j] = mfma<KIND>(fa[f][i], fb[f][j], acc[i][j]);
   };
 
-  // Software pipeline over the two k-steps of a stage, with the stage
-  // barrier between them: the fragment reads of one k-step are issued
-  // between the MFMAs of the previous one, so LDS latency hides behind
-  // matrix work.  sched_barrier fences keep the compiler from moving MFMAs
-  // across the barrier; sched_group_barrier pins the interleave (masks:
-  // 0x008 MFMA, 0x100 LDS read, 0x010 VMEM, which covers the DMA issues).
-  constexpr int NR = WTM + WTN, NV = PER_WAVE;  // fragment reads per k-step, DMA issues per stage
+  // Software pipeline over the KS k-steps of a stage, with the stage barrier
+  // before the last one: each k-step's fragment reads are issued between
+  // the MFMAs of the previous one, so LDS latency hides behind matrix work.
+  // The stage's DMA issues ride in the first k-steps.  sched_barrier fences
+  // keep the compiler from moving MFMAs across the barrier; sched_group_barrier
+  // pins the interleave (masks: 0x008 MFMA, 0x100 LDS read, 0x010 VMEM,
+  // which covers the DMA issues).
+  constexpr int NR = WTM + WTN;                  // fragment reads per k-step
+  constexpr int DKS = KS > 2 ? KS - 2 : 1;       // k-steps that carry DMA issues
+  constexpr int NV = (PER_WAVE + DKS - 1) / DKS;  // DMA issues per such k-step
 #pragma unroll
-  for (int s = 0; s < NS - 1; ++s) issue(s);
+  for (int s = 0; s < NS - 1; ++s) issue(s, 0, PER_WAVE);
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE) : "memory");
-  u32x4 fa0[WTM], fb0[WTN], fa1[WTM], fb1[WTN];
-  read_frags(0, 0, fa0, fb0);
+  read_frags(0, 0, 0);
   for (int kt = 0; kt < nkt; ++kt) {
     const int buf = kt % NS;
-    // phase 1: k-step 1's fragment reads, then the stage's DMA issues (an
-    // issue stalls the wave), each after one of k-step 0's MFMAs
-    read_frags(buf, 1, fa1, fb1);
-    mfmas(fa0, fb0);
-    // into buffer (kt - 1) % NS, which every wave finished reading before
-    // the last barrier
-    issue(kt + NS - 1);
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
+    for (int ks = 0; ks < KS; ++ks) {
+      const int cur = ks & 1;
+      if (ks < KS - 1) {
+        read_frags(buf, ks + 1, cur ^ 1);
+        mfmas(cur);
+        // into buffer (kt - 1) % NS, which every wave finished reading
+        // before the last barrier
+        if (ks < DKS) issue(kt + NS - 1, min(ks * NV, PER_WAVE), min((ks + 1) * NV, PER_WAVE));
 #pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    // this wave's stage-(kt+1) loads have landed (the NS-2 later stages may
-    // stay in flight) and its reads of stage kt are complete; after the
-    // barrier stage kt+1 is visible to every wave and buffer kt % NS is free
-    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE) : "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    // phase 2: stage kt+1's k-step 0 fragment reads between k-step 1's
-    // MFMAs (past the last stage they read a clamped copy, unused)
-    read_frags((kt + 1) % NS, 0, fa0, fb0);
-    mfmas(fa1, fb1);
+        for (int r = 0; r < NR; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          if (ks < DKS && r < NV) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+        }
+        if (ks < DKS && NV > NR) {
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          for (int v = NR; v < NV; ++v) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+          }
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        // this wave's stage-(kt+1) loads have landed (the NS-2 later stages
+        // may stay in flight) and its reads of stage kt are complete; after
+        // the barrier stage kt+1 is visible to every wave and buffer kt % NS
+        // is free
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE) : "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        // stage kt+1's first fragments (past the last stage a clamped copy, unused)
+        read_frags((kt + 1) % NS, 0, cur ^ 1);
+        mfmas(cur);
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
-    __builtin_amdgcn_sched_barrier(0);
   }
   // the clamped tail loads are still in flight: drain before the LDS goes away
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -350,24 +368,30 @@ __global__ __launch_bounds__(256) void transpose_any_kernel(const T *__restrict_
     if (n0 + i < N && k0 + tx < K) dst[(size_t)(n0 + i) * K + k0 + tx] = tile[tx][i];
 }
 
-template <int KIND, int OUT>
-int launch_gemm(hipStream_t st, GemmArgs args) {
+template <int KIND, int OUT, int SB>
+int launch_gemm_sb(hipStream_t st, GemmArgs args) {
   // 256x256 tiles only where they divide the output and still fill the chip
   if (args.m % 256 == 0 && args.n % 256 == 0 && (args.m / 256) * (args.n / 256) >= 192) {
     args.tiles_m = args.m / 256;
     args.tiles_n = args.n / 256;
-    hipLaunchKernelGGL((gemm_nt_kernel<KIND, 256, 256, OUT, false>), dim3(args.tiles_m * args.tiles_n),
+    hipLaunchKernelGGL((gemm_nt_kernel<KIND, 256, 256, OUT, false, SB>), dim3(args.tiles_m * args.tiles_n),
                        dim3(512), 0, st, args);
   } else {
     args.tiles_m = (args.m + 127) / 128;
     args.tiles_n = (args.n + 127) / 128;
     const dim3 grid(args.tiles_m * args.tiles_n);
     if (args.m % 128 == 0 && args.n % 128 == 0)
-      hipLaunchKernelGGL((gemm_nt_kernel<KIND, 128, 128, OUT, false>), grid, dim3(512), 0, st, args);
+      hipLaunchKernelGGL((gemm_nt_kernel<KIND, 128, 128, OUT, false, SB>), grid, dim3(512), 0, st, args);
     else
-      hipLaunchKernelGGL((gemm_nt_kernel<KIND, 128, 128, OUT, true>), grid, dim3(512), 0, st, args);
+      hipLaunchKernelGGL((gemm_nt_kernel<KIND, 128, 128, OUT, true, SB>), grid, dim3(512), 0, st, args);
   }
   return launch_status("gemm_nt_kernel");
+}
+
+template <int KIND, int OUT>
+int launch_gemm(hipStream_t st, GemmArgs args) {
+  // 128-byte K stages where K allows (half the stage barriers per FLOP)
+  return args.kbytes % 128 == 0 ? launch_gemm_sb<KIND, OUT, 128>(st, args) : launch_gemm_sb<KIND, OUT, 64>(st, args);
 }
 
 int relayout_rhs(wafer_hip_context *ctx, const void *rhs, uint32_t k, uint32_t n, int esize,
