@@ -279,18 +279,19 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmArgs args) {
 // N, an in-register byte (or half-word) transpose with v_perm, a dword tile
 // in LDS, and 16-byte stores along K, so both HBM sides move whole lines.
 //
-// int8: a 128-thread block moves a 64 (k) x 128 (n) tile.  Thread (k4, n16)
-// loads rows 4 k4 .. 4 k4 + 3 at bytes 16 n16 .. +15; each output dword is
-// the 4 k-bytes of one column.
-__global__ __launch_bounds__(128) void transpose_i8_kernel(const uint8_t *__restrict__ src,
+// int8: a 256-thread block moves a 128 (k) x 128 (n) tile.  Thread
+// (kq, n16) loads rows 4 kq .. 4 kq + 3 at bytes 16 n16 .. +15 (8 lanes
+// cover one 128-byte row segment); each transposed dword is the 4 k-bytes of
+// one column.  Stores: 8 lanes write one whole 128-byte row of Bt.
+__global__ __launch_bounds__(256) void transpose_i8_kernel(const uint8_t *__restrict__ src,
                                                            uint8_t *__restrict__ dst, int K, int N) {
-  __shared__ uint32_t T[128][17];  // [n][k / 4], padded
-  const int k0 = blockIdx.y * 64, n0 = blockIdx.x * 128;
-  const int tid = threadIdx.x, k4 = tid & 15, n16 = tid >> 4;
+  __shared__ __align__(16) uint32_t T[128][32];  // [n][k / 4], 16-byte chunks swizzled
+  const int k0 = blockIdx.y * 128, n0 = blockIdx.x * 128;
+  const int tid = threadIdx.x, n16 = tid & 7, kq = tid >> 3;
   u32x4 r[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    r[i] = *(const u32x4 *)(src + (size_t)(k0 + 4 * k4 + i) * N + n0 + 16 * n16);
+    r[i] = *(const u32x4 *)(src + (size_t)(k0 + 4 * kq + i) * N + n0 + 16 * n16);
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     // rows a0..a3 hold columns 4w..4w+3; out[c] = bytes c of a0, a1, a2, a3
@@ -300,22 +301,21 @@ __global__ __launch_bounds__(128) void transpose_i8_kernel(const uint8_t *__rest
     const uint32_t t23l = __builtin_amdgcn_perm(a3, a2, 0x05010400u);
     const uint32_t t23h = __builtin_amdgcn_perm(a3, a2, 0x07030602u);
     const int n = 16 * n16 + 4 * w;
-    T[n + 0][k4] = __builtin_amdgcn_perm(t23l, t01l, 0x05040100u);
-    T[n + 1][k4] = __builtin_amdgcn_perm(t23l, t01l, 0x07060302u);
-    T[n + 2][k4] = __builtin_amdgcn_perm(t23h, t01h, 0x05040100u);
-    T[n + 3][k4] = __builtin_amdgcn_perm(t23h, t01h, 0x07060302u);
+    // 16-byte chunk kq/4 of row n sits at chunk (kq/4) ^ (n/16): the rows
+    // one write instruction touches are 16 apart, so their chunks differ
+    const int kx = (((kq >> 2) ^ n16) << 2) | (kq & 3);
+    T[n + 0][kx] = __builtin_amdgcn_perm(t23l, t01l, 0x05040100u);
+    T[n + 1][kx] = __builtin_amdgcn_perm(t23l, t01l, 0x07060302u);
+    T[n + 2][kx] = __builtin_amdgcn_perm(t23h, t01h, 0x05040100u);
+    T[n + 3][kx] = __builtin_amdgcn_perm(t23h, t01h, 0x07060302u);
   }
   __syncthreads();
-  // thread tid writes row n0 + tid of Bt: 64 bytes of k
-  uint8_t *d = dst + (size_t)(n0 + tid) * K + k0;
+  // pass p: lanes 8 q .. 8 q + 7 write row n = 32 p + tid / 8 of Bt, 16 bytes each
+  const int j = tid & 7;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    u32x4 v;
-    v[0] = T[tid][4 * q + 0];
-    v[1] = T[tid][4 * q + 1];
-    v[2] = T[tid][4 * q + 2];
-    v[3] = T[tid][4 * q + 3];
-    *(u32x4 *)(d + 16 * q) = v;
+  for (int p = 0; p < 4; ++p) {
+    const int n = 32 * p + (tid >> 3);
+    *(u32x4 *)(dst + (size_t)(n0 + n) * K + k0 + 16 * j) = *(const u32x4 *)&T[n][4 * (j ^ (n >> 4))];
   }
 }
 
@@ -402,9 +402,10 @@ int relayout_rhs(wafer_hip_context *ctx, const void *rhs, uint32_t k, uint32_t n
     return fail(WAFER_HIP_E_INVALID_FIELD, "gemm: k above 2097120 with a [K,N] rhs; pass the [N,K] form");
   WAFER_TRY(ensure_workspace(ctx, &ctx->relayout, &ctx->relayout_bytes, need));
   // check_shape guarantees k a multiple of 64 (int8) or 32 (16-bit); the
-  // tiled kernels also need n a multiple of their 128 / 64 columns
-  const int tile_n = esize == 1 ? 128 : 64;
-  if (n % tile_n) {
+  // tiled kernels need n a multiple of their 128 / 64 columns and (int8) k a
+  // multiple of 128
+  const bool tiled = esize == 1 ? (n % 128 == 0 && k % 128 == 0) : n % 64 == 0;
+  if (!tiled) {
     const dim3 grid((n + 31) / 32, (k + 31) / 32);
     if (esize == 1)
       hipLaunchKernelGGL(transpose_any_kernel<uint8_t>, grid, dim3(256), 0, ctx->stream, (const uint8_t *)rhs,
@@ -413,7 +414,7 @@ int relayout_rhs(wafer_hip_context *ctx, const void *rhs, uint32_t k, uint32_t n
       hipLaunchKernelGGL(transpose_any_kernel<uint16_t>, grid, dim3(256), 0, ctx->stream, (const uint16_t *)rhs,
                          (uint16_t *)ctx->relayout, (int)k, (int)n);
   } else if (esize == 1)
-    hipLaunchKernelGGL(transpose_i8_kernel, dim3(n / 128, k / 64), dim3(128), 0, ctx->stream,
+    hipLaunchKernelGGL(transpose_i8_kernel, dim3(n / 128, k / 128), dim3(256), 0, ctx->stream,
                        (const uint8_t *)rhs, (uint8_t *)ctx->relayout, (int)k, (int)n);
   else
     hipLaunchKernelGGL(transpose_b16_kernel, dim3(n / 64, k / 32), dim3(128), 0, ctx->stream,
