@@ -1,0 +1,82 @@
+"""GPU tests of the MFMA GEMM's fused SwiGLU epilogue.
+
+The fused entry is held bit for bit against the unfused sequence it
+replaces, run through the same library on the same inputs:
+
+  wafer_hip_gemm_mfma_swiglu == two wafer_hip_gemm_mfma (bf16 out, gate and
+      up) followed by wafer_hip_silu_mul.
+
+Both sides accumulate the same products in the same MFMA order, so the
+narrowed products are identical and the region arithmetic is the same
+function; any difference is a bug in the epilogue (a wrong column pairing, a
+dropped rounding point, a tail store).  The unfused GEMM itself is held to
+the formal lane in test_gpu_parity.py.  Shapes cover the 256x256 tiles with
+and without ragged m / feature tails and the decoder layer's own shape.
+"""
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def hip():
+    from vibe_compiler_amd import backend
+
+    ctx = backend.Context(0)
+    yield ctx
+    ctx.close()
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch
+
+    return torch
+
+
+def _rnd(torch, gen, *shape, std=1.0):
+    return (torch.randn(*shape, generator=gen, device="cuda") * std).to(torch.bfloat16)
+
+
+def _same_bits(torch, a, b):
+    return torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("m,k,f", [
+    (1024, 4096, 14336),  # decoder layer gate/up (256x256 tiles)
+    (256, 512, 512),
+    (200, 256, 96),       # ragged m and a feature count that leaves a partial 256-column tile
+    (64, 128, 32),        # one 32-feature group
+])
+def test_gemm_swiglu_bit_exact(hip, torch, m, k, f):
+    from vibe_compiler_amd import backend as B
+
+    gen = torch.Generator(device="cuda").manual_seed(20260803 + m + k + f)
+    h, wg, wu = _rnd(torch, gen, m, k), _rnd(torch, gen, f, k, std=0.05), _rnd(torch, gen, f, k, std=0.05)
+    gate = torch.empty(m, f, dtype=torch.bfloat16, device="cuda")
+    up = torch.empty_like(gate)
+    ref = torch.empty_like(gate)
+    hip.gemm_mfma(h, wg, gate, m, k, f, out_fmt=B.BF16, rhs_t=True)
+    hip.gemm_mfma(h, wu, up, m, k, f, out_fmt=B.BF16, rhs_t=True)
+    hip.silu_mul(gate, up, ref)
+    wgu = torch.empty(2 * f, k, dtype=torch.bfloat16, device="cuda")
+    hip.interleave_gate_up(wg, wu, wgu)
+    # canary past the output: a tail store beyond m*f would change it
+    buf = torch.full((m * f + 64,), 1.5, dtype=torch.bfloat16, device="cuda")
+    hip.gemm_mfma_swiglu(h, wgu, buf[: m * f].view(m, f), m, k, f)
+    torch.cuda.synchronize()
+    # the packing itself: 64-row groups of 32 gate rows then 32 up rows
+    g4 = wgu.view(f // 32, 2, 32, k)
+    assert torch.equal(g4[:, 0].reshape(f, k), wg) and torch.equal(g4[:, 1].reshape(f, k), wu)
+    assert _same_bits(torch, buf[: m * f].view(m, f), ref)
+    assert torch.all(buf[m * f:] == 1.5)
+
+
+def test_fused_entries_reject_unsupported(hip, torch):
+    from vibe_compiler_amd import backend as B
+
+    t = torch.zeros(64 * 64, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(B.WaferHipError):
+        hip.gemm_mfma_swiglu(t, t, t, 8, 64, 16)  # features not a multiple of 32
+    with pytest.raises(B.WaferHipError):
+        hip.gemm_mfma_swiglu(t, t, t, 8, 64, 32, in_fmt=B.F16)  # bf16 only

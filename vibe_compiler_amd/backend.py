@@ -39,7 +39,7 @@ STATUS = {0: "ok", -1: "InvalidCommandField", -2: "WorkBudgetExceeded",
 EXPORTS = (
     "wafer_hip_context_create", "wafer_hip_context_destroy", "wafer_hip_set_stream",
     "wafer_hip_synchronize", "wafer_hip_last_error", "wafer_hip_implementation",
-    "wafer_hip_gemm", "wafer_hip_gemm_mfma", "wafer_hip_gemm_i8", "wafer_hip_elementwise",
+    "wafer_hip_gemm", "wafer_hip_gemm_mfma", "wafer_hip_gemm_mfma_swiglu", "wafer_hip_gemm_i8", "wafer_hip_elementwise",
     "wafer_hip_convert", "wafer_hip_reduce", "wafer_hip_physical_bytes", "wafer_hip_pack",
     "wafer_hip_unpack", "wafer_hip_attention_prefill", "wafer_hip_attention_decode",
     "wafer_hip_rmsnorm", "wafer_hip_softmax", "wafer_hip_silu_mul", "wafer_hip_gelu_tanh",
@@ -112,6 +112,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wafer_hip_synchronize.argtypes = [vp]
     L.wafer_hip_gemm.argtypes = [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32, u32, u32]
     L.wafer_hip_gemm_mfma.argtypes = [vp, vp, vp, vp, u32, u32, u32, u32, u32, u32]
+    L.wafer_hip_gemm_mfma_swiglu.argtypes = [vp, vp, vp, vp, u32, u32, u32, u32]
     L.wafer_hip_gemm_i8.argtypes = [vp, vp, vp, vp, vp, vp, u32, u32, u32, u32]
     L.wafer_hip_elementwise.argtypes = [vp, u32, u32, vp, vp, vp, u64]
     L.wafer_hip_convert.argtypes = [vp, u32, u32, vp, vp, u64]
@@ -238,6 +239,25 @@ class Context:
         _fits("gemm_mfma", (lhs, m * k * 2), (rhs, k * n * 2), (dst, m * n * (4 if out_fmt == F32 else 2)))
         _check(self._L.wafer_hip_gemm_mfma(self._bind(), _p(lhs), _p(rhs), _p(dst), m, k, n, in_fmt,
                                            out_fmt, int(rhs_t)))
+
+    def gemm_mfma_swiglu(self, lhs, rhs_gu, dst, m, k, features, in_fmt=BF16):
+        """dst [m, features] = silu_mul(gate, up) of the gate/up products, with
+        rhs_gu [2*features, k] in 64-row groups (32 gate rows, then the 32 up
+        rows of the same features); see interleave_gate_up."""
+        _fits("gemm_mfma_swiglu", (lhs, m * k * 2), (rhs_gu, 2 * features * k * 2), (dst, m * features * 2))
+        _check(self._L.wafer_hip_gemm_mfma_swiglu(self._bind(), _p(lhs), _p(rhs_gu), _p(dst), m, k, features,
+                                                  in_fmt))
+
+    def interleave_gate_up(self, w_gate, w_up, w_gu):
+        """Packs the [features, k] gate and up weights (16-bit) into the
+        [2*features, k] operand of gemm_mfma_swiglu with two strided copies."""
+        features, k = w_gate.shape
+        if features % 32 or tuple(w_up.shape) != (features, k) or w_gu.numel() != 2 * features * k:
+            raise ValueError("interleave_gate_up: shapes")
+        blk = 32 * k * w_gate.element_size()
+        for part, w in enumerate((w_gate, w_up)):
+            self.strided_copy(w, w_gu, blk, (blk, 0, 0), (features // 32, 1, 1), (2 * blk, 0, 0),
+                              (features // 32, 1, 1), dst_offset=part * blk)
 
     def gemm_i8(self, a, b, scale, y, m, k, n, acc_out=None, rhs_t=False):
         _fits("gemm_i8", (a, m * k), (b, k * n), (scale, n * 4), (y, m * n * 2), (acc_out, m * n * 4))

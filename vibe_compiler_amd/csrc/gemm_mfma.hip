@@ -58,7 +58,11 @@ __device__ inline i32x16 mfma<KIND_I8>(u32x4 a, u32x4 b, i32x16 c) {
 }
 
 // Epilogue selectors.
-enum { OUT_F32 = 0, OUT_NARROW = 1, OUT_I8_DEQUANT = 2 };
+// OUT_SWIGLU (bf16 only): the rhs rows come in 64-row groups, 32 gate rows
+// then the 32 up rows of the same features, and y[m, f] =
+// bf16(silu_mul(bf16(gate), bf16(up))) over N/2 features (the narrowed
+// products, then the silu_mul region).
+enum { OUT_F32 = 0, OUT_NARROW = 1, OUT_I8_DEQUANT = 2, OUT_SWIGLU = 3 };
 
 struct GemmArgs {
   const uint8_t *a;    // [M, K] elements, K-contiguous
@@ -245,7 +249,97 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmArgs args) {
   // the clamped tail loads are still in flight: drain before the LDS goes away
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+  // Staged epilogue (16-bit outputs of full tiles): each wave narrows its
+  // sub-tile into LDS as row-major [OR][OC] 16-bit values (16-byte chunks of
+  // a row XOR-swizzled by (row / 4) % CPR, so the two row groups of one
+  // ds_write_b16 land in distinct banks), then reads it back 16 bytes per
+  // lane and stores whole 16-byte row segments (64 lanes cover 1 KiB of
+  // consecutive rows) instead of scattered 2-byte stores.  Waves 0-3 stage
+  // in sA, 4-7 in sB, after a barrier that retires every wave's fragment
+  // reads and stage moves.
+  if constexpr (OUT != OUT_F32) {
+    constexpr int OR = BM / WM;                                     // rows per wave
+    constexpr int OC = OUT == OUT_SWIGLU ? BN / WN / 2 : BN / WN;   // output columns per wave
+    constexpr int CPR = OC * 2 / 16;                                // 16-byte chunks per row
+    static_assert(4 * OR * OC * 2 <= NS * BM * CH * 16 && 4 * OR * OC * 2 <= NS * BN * CH * 16,
+                  "a wave's staged sub-tile fits its quarter of sA / sB");
+    const int ldy = OUT == OUT_SWIGLU ? args.n / 2 : args.n;
+    const bool staged = !TAIL && ldy % 8 == 0 && (((uintptr_t)args.y) & 15) == 0 &&
+                        (OUT != OUT_I8_DEQUANT || args.acc_out == nullptr);
+    if (staged) {
+      __syncthreads();
+      char *stage = (char *)(wave < 4 ? &sA[0][0] : &sB[0][0]) + (wave & 3) * (OR * OC * 2);
+      auto put = [&](int row, int col, uint16_t v) __attribute__((always_inline)) {
+        const int sw = (row >> 2) & (CPR - 1);
+        *(uint16_t *)(stage + row * (CPR * 16) + (((col >> 3) ^ sw) << 4) + (col & 7) * 2) = v;
+      };
+      if constexpr (OUT == OUT_SWIGLU) {
+        static_assert(KIND == KIND_BF16, "the fused epilogue serves bf16");
+#pragma unroll
+        for (int i = 0; i < WTM; ++i)
+#pragma unroll
+          for (int jp = 0; jp < WTN / 2; ++jp)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const float gv = bf16_to_f32(f32_to_bf16((float)acc[i][2 * jp][r]));
+              const float uv = bf16_to_f32(f32_to_bf16((float)acc[i][2 * jp + 1][r]));
+              put(i * 32 + 8 * (r >> 2) + 4 * g + (r & 3), jp * 32 + l32, f32_to_bf16(silu_mul_1(gv, uv)));
+            }
+      } else {
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) {
+          float sc = 0.0f;
+          if (OUT == OUT_I8_DEQUANT) sc = args.scale[n0 + wn * (BN / WN) + j * 32 + l32];
+#pragma unroll
+          for (int i = 0; i < WTM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              uint16_t v;
+              if (OUT == OUT_NARROW)
+                v = KIND == KIND_F16 ? f32_to_f16((float)acc[i][j][r]) : f32_to_bf16((float)acc[i][j][r]);
+              else
+                v = f32_to_bf16((float)(int32_t)acc[i][j][r] * sc);
+              put(i * 32 + 8 * (r >> 2) + 4 * g + (r & 3), j * 32 + l32, v);
+            }
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's own sub-tile
+      const int col0 = OUT == OUT_SWIGLU ? (n0 + wn * (BN / WN)) / 2 : n0 + wn * (BN / WN);
+      uint16_t *ybase = (uint16_t *)args.y + (size_t)(m0 + wm * OR) * ldy + col0;
+#pragma unroll
+      for (int q = 0; q < OR * CPR / 64; ++q) {
+        const int idx = q * 64 + lane, row = idx / CPR, c = idx % CPR;
+        const u32x4 v = *(const u32x4 *)(stage + row * (CPR * 16) + ((c ^ ((row >> 2) & (CPR - 1))) << 4));
+        *(u32x4 *)(ybase + (size_t)row * ldy + c * 8) = v;
+      }
+      return;
+    }
+  }
   // epilogue: lane holds column l32 and rows 8*(r/4) + 4*g + r%4 of each tile
+  if constexpr (OUT == OUT_SWIGLU) {
+    // a wave's 32-column tiles 2 jp and 2 jp + 1 are the gate and up columns
+    // of the same 32 features
+    static_assert(WTN % 2 == 0, "SwiGLU pairs need two 32-column tiles per wave");
+    static_assert(KIND == KIND_BF16, "the fused epilogues serve bf16");
+    const int nf = args.n / 2;
+#pragma unroll
+    for (int i = 0; i < WTM; ++i)
+#pragma unroll
+      for (int jp = 0; jp < WTN / 2; ++jp) {
+        const int feat = (n0 + wn * (BN / WN) + jp * 64) / 2 + l32;
+        const bool col_ok = !TAIL || feat < nf;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (TAIL && !(col_ok && row < args.m)) continue;
+          const float gv = bf16_to_f32(f32_to_bf16((float)acc[i][2 * jp][r]));
+          const float uv = bf16_to_f32(f32_to_bf16((float)acc[i][2 * jp + 1][r]));
+          ((uint16_t *)args.y)[(size_t)row * nf + feat] = f32_to_bf16(silu_mul_1(gv, uv));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < WTM; ++i)
 #pragma unroll
@@ -369,7 +463,27 @@ __global__ __launch_bounds__(256) void transpose_any_kernel(const T *__restrict_
 }
 
 template <int KIND, int OUT, int SB>
+int launch_gemm_tiles(hipStream_t st, GemmArgs args);
+
+template <int KIND, int OUT, int SB>
 int launch_gemm_sb(hipStream_t st, GemmArgs args) {
+  if constexpr (OUT != OUT_SWIGLU) {
+    return launch_gemm_tiles<KIND, OUT, SB>(st, args);
+  } else {
+    // gate/up column pairs need 64 columns per wave: 256x256 tiles always
+    args.tiles_m = (args.m + 255) / 256;
+    args.tiles_n = (args.n + 255) / 256;
+    const dim3 grid(args.tiles_m * args.tiles_n);
+    if (args.m % 256 == 0 && args.n % 256 == 0)
+      hipLaunchKernelGGL((gemm_nt_kernel<KIND, 256, 256, OUT, false, SB>), grid, dim3(512), 0, st, args);
+    else
+      hipLaunchKernelGGL((gemm_nt_kernel<KIND, 256, 256, OUT, true, SB>), grid, dim3(512), 0, st, args);
+    return launch_status("gemm_nt_kernel");
+  }
+}
+
+template <int KIND, int OUT, int SB>
+int launch_gemm_tiles(hipStream_t st, GemmArgs args) {
   // 256x256 tiles only where they divide the output and still fill the chip
   if (args.m % 256 == 0 && args.n % 256 == 0 && (args.m / 256) * (args.n / 256) >= 192) {
     args.tiles_m = args.m / 256;
@@ -464,6 +578,23 @@ extern "C" int wafer_hip_gemm_mfma(wafer_hip_context *ctx, const void *lhs, cons
                : launch_gemm<KIND_BF16, OUT_NARROW>(ctx->stream, args);
   return f32 ? launch_gemm<KIND_F16, OUT_F32>(ctx->stream, args)
              : launch_gemm<KIND_F16, OUT_NARROW>(ctx->stream, args);
+}
+
+extern "C" int wafer_hip_gemm_mfma_swiglu(wafer_hip_context *ctx, const void *lhs, const void *rhs_gu,
+                                          void *dst, uint32_t m, uint32_t k, uint32_t features,
+                                          uint32_t in_format) {
+  WAFER_CHECK_CTX(ctx);
+  if (in_format != WAFER_FMT_BF16)
+    return fail(WAFER_HIP_E_UNSUPPORTED, "gemm_mfma_swiglu: input format must be BF16");
+  if (!lhs || !rhs_gu || !dst) return fail(WAFER_HIP_E_INVALID_FIELD, "gemm_mfma_swiglu: null tensor");
+  if (features == 0 || features % 32)
+    return fail(WAFER_HIP_E_UNSUPPORTED, "gemm_mfma_swiglu: features must be a positive multiple of 32");
+  if (features > 0x3fffffffu) return fail(WAFER_HIP_E_INVALID_FIELD, "gemm_mfma_swiglu: output too large");
+  WAFER_TRY(check_shape(m, k, 2 * features, 2, "gemm_mfma_swiglu"));
+  WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
+  GemmArgs args{(const uint8_t *)lhs, (const uint8_t *)rhs_gu, dst, nullptr, nullptr, (int)m,
+                (int)(2 * features), (int)(k * 2), 0, 0};
+  return launch_gemm<KIND_BF16, OUT_SWIGLU>(ctx->stream, args);
 }
 
 extern "C" int wafer_hip_gemm_i8(wafer_hip_context *ctx, const int8_t *a, const int8_t *b,

@@ -43,7 +43,6 @@ __device__ inline float block_max(float v, float *red) {
   return s;
 }
 
-__device__ inline float explp_acc(float x) { return exp2f(x * 0x1.715476p+0f); }
 
 // y = x * Rsqrt(Sum(x*x) * (1/N) + eps) * w.  VEC: 8 columns per thread and
 // access (cols % 8 == 0, tensors 16-byte aligned).
@@ -104,11 +103,6 @@ __global__ __launch_bounds__(RT) void softmax_kernel(const void *__restrict__ x,
     store_from_f32<F>(y, base + c, explp_acc(load_as_f32<F>(x, base + c) - m) * rc);
 }
 
-// y = g * Recip(1 + ExpLp(-g)) * u
-__device__ inline float silu_mul_1(float g, float u) {
-  const float sig = 1.0f / (1.0f + explp_acc(-g));
-  return g * sig * u;
-}
 template <uint32_t F, bool VEC>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const void *__restrict__ gate,
                                                        const void *__restrict__ up,

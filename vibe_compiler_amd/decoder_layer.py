@@ -11,8 +11,12 @@ backend, each one a C-ABI call of ``libwafer_hip.so`` on the caller's stream:
     a    = o -> token-major  [T, Hq D]                wafer_hip_head_permute
     x1   = x + a . Wo^T                               wafer_hip_gemm_mfma, wafer_hip_elementwise(Add)
     h2   = RMSNorm(x1) * w_post
-    y    = x1 + (silu(h2 . Wg^T) * (h2 . Wu^T)) . Wd^T
-                                                      wafer_hip_gemm_mfma, wafer_hip_silu_mul, Add
+    act  = silu(h2 . Wg^T) * (h2 . Wu^T)              wafer_hip_gemm_mfma_swiglu
+    y    = x1 + act . Wd^T                            wafer_hip_gemm_mfma, Add
+
+The fused SwiGLU GEMM gives the same bits as the unfused sequence (gate and
+up GEMMs with narrow outputs, then the silu_mul region): its epilogue rounds
+each product to bf16 first and then applies the region's own arithmetic.
 
 The math is the reference's CPU reference of the decoder block
 (test/Tools/Inputs/wafer_pytorch_xla_capture.py:1183-1260: rms_norm with
@@ -25,8 +29,10 @@ regions is bf16, every region computes in f32; results match an f32 torch
 evaluation of the same layer within the attention tolerance, not bit for bit.
 
 Weights are kept in the nn.Linear orientation [out, in] (rhs Transpose for
-the GEMM), so no re-layout pass runs per call.  All buffers are allocated
-once in the constructor; ``forward`` launches only.
+the GEMM), so no re-layout pass runs per call; the gate and up weights are
+packed once, in the constructor, into the [2*ffn, hidden] operand of the
+fused SwiGLU GEMM (64-row groups of 32 gate and 32 up rows).  All buffers are
+allocated once in the constructor; ``forward`` launches only.
 """
 from __future__ import annotations
 
@@ -35,7 +41,6 @@ import math
 from . import backend as B
 
 ADD = B.EW["Add"]  # TargetElementwiseOperation::Add
-
 
 class DecoderLayer:
     """One decoder layer on one GPU, bf16 weights resident in HBM."""
@@ -50,6 +55,8 @@ class DecoderLayer:
         self.eps, self.theta = eps, theta
         if q_heads * head_dim != hidden:
             raise ValueError("q_heads * head_dim must equal hidden")
+        if ffn % 32:
+            raise ValueError("ffn must be a multiple of 32 (gate/up packing)")
         dev = torch.device("cuda", hip.device)
         bf = torch.bfloat16
 
@@ -67,6 +74,8 @@ class DecoderLayer:
         self.wg = w("wgate", (ffn, hidden))
         self.wu = w("wup", (ffn, hidden))
         self.wd = w("wdown", (hidden, ffn))
+        self.wgu = torch.empty((2 * ffn, hidden), dtype=bf, device=dev)
+        hip.interleave_gate_up(self.wg, self.wu, self.wgu)
 
         T = tokens
         e = lambda *s: torch.empty(s, dtype=bf, device=dev)
@@ -79,8 +88,6 @@ class DecoderLayer:
         self.attn = e(T, hidden)
         self.proj = e(T, hidden)
         self.x1 = e(T, hidden)
-        self.gate = e(T, ffn)
-        self.up = e(T, ffn)
         self.act = e(T, ffn)
         self.down = e(T, hidden)
         # RoPE runs on the head-major tensors as [heads*T, 1, D] rows, so the
@@ -107,9 +114,7 @@ class DecoderLayer:
         hip.gemm_mfma(self.attn, self.wo, self.proj, T, Hd, Hd, out_fmt=B.BF16, rhs_t=True)
         hip.elementwise(ADD, B.BF16, x, self.x1, self.proj)
         hip.rmsnorm(self.x1, self.w_post, self.h, self.eps)
-        hip.gemm_mfma(self.h, self.wg, self.gate, T, Hd, F, out_fmt=B.BF16, rhs_t=True)
-        hip.gemm_mfma(self.h, self.wu, self.up, T, Hd, F, out_fmt=B.BF16, rhs_t=True)
-        hip.silu_mul(self.gate, self.up, self.act)
+        hip.gemm_mfma_swiglu(self.h, self.wgu, self.act, T, Hd, F)
         hip.gemm_mfma(self.act, self.wd, self.down, T, F, Hd, out_fmt=B.BF16, rhs_t=True)
         hip.elementwise(ADD, B.BF16, self.x1, y, self.down)
         return y
