@@ -261,6 +261,21 @@ int wafer_hip_gelu_tanh(wafer_hip_context *ctx, uint32_t format, const void *x,
 int wafer_hip_rope(wafer_hip_context *ctx, uint32_t format, const void *x,
                    void *y, uint64_t tokens, uint64_t heads,
                    uint64_t head_dim, const int32_t *positions, float theta);
+/* RoPE fused into the token-major -> head-major re-layout of a projection:
+ * dst [heads, tokens, head_dim] = RoPE of src rows (token t, head h at
+ * element t * token_stride + h * head_dim), positions [tokens].  Equal bit
+ * for bit to wafer_hip_head_permute (direction 0) followed by wafer_hip_rope
+ * on the head-major tensor with each row's token position.  The rope step is
+ * the rotate-half form of the reference's RoPE region (ComputeLowering.cpp
+ * element ops; test/Tools/Inputs/wafer_pytorch_xla_capture.py:1183-1260 for
+ * the decoder block); the re-layout is the strided movement between the QKV
+ * GEMM and the attention region.  head_dim a multiple of 16, token_stride
+ * of 8, tensors 16-byte aligned; dst must not overlap src. */
+int wafer_hip_head_permute_rope(wafer_hip_context *ctx, uint32_t format,
+                                const void *src, void *dst, uint64_t tokens,
+                                uint64_t heads, uint64_t head_dim,
+                                uint64_t token_stride,
+                                const int32_t *positions, float theta);
 /* y = x + bias (bias F32 [cols], broadcast over rows). */
 int wafer_hip_bias_add(wafer_hip_context *ctx, uint32_t format, const void *x,
                        const float *bias, void *y, uint64_t rows,

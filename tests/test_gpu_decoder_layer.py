@@ -37,6 +37,37 @@ def torch():
     return torch
 
 
+# ------------------------------------------------------ head permute + RoPE
+@pytest.mark.parametrize("tokens,heads,head_dim,stride,offset,fmt", [
+    (1024, 32, 128, 6144, 0, "bf16"),      # the layer's Q
+    (1024, 8, 128, 6144, 4096, "bf16"),    # the layer's K
+    (1024, 40, 128, 6144, 0, "bf16"),      # the layer's Q and K together (head groups of 8)
+    (77, 3, 64, 200, 8, "bf16"),           # ragged: odd tokens and heads, head groups of 1
+    (300, 6, 32, 192, 0, "f16"),
+    (64, 5, 16, 96, 16, "f32"),
+])
+def test_head_permute_rope_bit_exact(hip, torch, tokens, heads, head_dim, stride, offset, fmt):
+    """The fused kernel against head_permute followed by rope, bit for bit
+    (the same rotation expressions; only the cos/sin sharing differs)."""
+    from vibe_compiler_amd import backend as B
+
+    F, dt = {"bf16": (B.BF16, torch.bfloat16), "f16": (B.F16, torch.float16), "f32": (B.F32, torch.float32)}[fmt]
+    gen = torch.Generator(device="cuda").manual_seed(tokens * 31 + heads)
+    src = torch.randn(tokens * stride + offset, generator=gen, device="cuda").to(dt)
+    pos = (torch.randperm(4 * tokens, generator=gen, device="cuda")[:tokens]).to(torch.int32)
+    ref = torch.empty(heads, tokens, head_dim, dtype=dt, device="cuda")
+    hip.head_permute(src, ref, tokens, heads, head_dim, stride, 0, fmt=F, src_offset=offset)
+    hip.rope(ref.view(heads * tokens, 1, head_dim), ref.view(heads * tokens, 1, head_dim), pos.repeat(heads),
+             1e4, fmt=F)
+    out = torch.full((heads * tokens * head_dim + 32,), 7.0, dtype=dt, device="cuda")
+    hip.head_permute_rope(src, out, tokens, heads, head_dim, stride, pos, 1e4, fmt=F, src_offset=offset)
+    torch.cuda.synchronize()
+    got = out[: heads * tokens * head_dim].view(heads, tokens, head_dim)
+    iv = torch.int32 if fmt == "f32" else torch.int16
+    assert torch.equal(got.view(iv), ref.view(iv))
+    assert torch.all(out[heads * tokens * head_dim:] == 7.0)
+
+
 # ------------------------------------------------------------- head permute
 @pytest.mark.parametrize("fmt_name,T,H,D,extra", [("BF16", 256, 8, 128, 0), ("BF16", 64, 3, 64, 256),
                                                   ("F32", 32, 4, 128, 64), ("F16", 16, 2, 8, 8)])

@@ -43,7 +43,7 @@ EXPORTS = (
     "wafer_hip_convert", "wafer_hip_reduce", "wafer_hip_physical_bytes", "wafer_hip_pack",
     "wafer_hip_unpack", "wafer_hip_attention_prefill", "wafer_hip_attention_decode",
     "wafer_hip_rmsnorm", "wafer_hip_softmax", "wafer_hip_silu_mul", "wafer_hip_gelu_tanh",
-    "wafer_hip_rope", "wafer_hip_bias_add", "wafer_hip_head_permute", "wafer_hip_buffer_alloc",
+    "wafer_hip_rope", "wafer_hip_bias_add", "wafer_hip_head_permute", "wafer_hip_head_permute_rope", "wafer_hip_buffer_alloc",
     "wafer_hip_buffer_free", "wafer_hip_copy_to_device", "wafer_hip_copy_to_host", "wafer_hip_convert_route",
     "wafer_hip_strided_copy", "wafer_hip_memset", "wafer_hip_bit2fp", "wafer_hip_mask_move",
     "wafer_hip_compare_expected", "wafer_hip_compare_statistics", "wafer_hip_environment",
@@ -127,6 +127,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wafer_hip_silu_mul.argtypes = [vp, u32, vp, vp, vp, u64]
     L.wafer_hip_gelu_tanh.argtypes = [vp, u32, vp, vp, u64]
     L.wafer_hip_rope.argtypes = [vp, u32, vp, vp, u64, u64, u64, vp, f32]
+    L.wafer_hip_head_permute_rope.argtypes = [vp, u32, vp, vp, u64, u64, u64, u64, vp, f32]
     L.wafer_hip_bias_add.argtypes = [vp, u32, vp, vp, vp, u64, u64]
     L.wafer_hip_head_permute.argtypes = [vp, u32, vp, vp, u64, u64, u64, u64, u32]
     L.wafer_hip_buffer_alloc.argtypes = [vp, u64, ctypes.POINTER(vp)]
@@ -318,6 +319,21 @@ class Context:
     def rope(self, x, y, positions, theta, fmt=BF16):
         T, H, D = x.shape
         _check(self._L.wafer_hip_rope(self._bind(), fmt, _p(x), _p(y), T, H, D, _p(positions), float(theta)))
+
+    def head_permute_rope(self, src, dst, tokens, heads, head_dim, token_stride, positions, theta, fmt=BF16,
+                          src_offset=0):
+        """dst [heads, tokens, head_dim] = RoPE of the token-major rows of
+        `src` (element offset src_offset, row stride token_stride), with
+        positions [tokens] (int32, device); equals head_permute + rope."""
+        es = 4 if fmt == F32 else 2
+        if src.element_size() != es or dst.element_size() != es:
+            raise ValueError("head_permute_rope: tensor element size does not match the format")
+        if src_offset < 0 or src_offset + (tokens - 1) * token_stride + heads * head_dim > src.numel() \
+                or dst.numel() < heads * tokens * head_dim or positions.numel() < tokens:
+            raise ValueError("head_permute_rope: the addressed region exceeds a tensor")
+        sp = ctypes.c_void_p(_p(src).value + src_offset * es)
+        _check(self._L.wafer_hip_head_permute_rope(self._bind(), fmt, sp, _p(dst), tokens, heads, head_dim,
+                                                   token_stride, _p(positions), float(theta)))
 
     def head_permute(self, src, dst, tokens, heads, head_dim, token_stride, direction, fmt=BF16,
                      src_offset=0, dst_offset=0):

@@ -156,11 +156,16 @@ __global__ __launch_bounds__(256) void gelu_tanh_kernel(const void *__restrict__
 // One thread per rotation pair (d, d + head_dim/2) of a row (VEC: per 8
 // consecutive pairs, head_dim % 16 == 0 and 16-byte aligned tensors): both
 // outputs of a pair come from the same two inputs, so y may alias x.
-__device__ inline void rope_pair(float xl, float xh, float angle, float &yl, float &yh) {
-  const float c = cosf(angle), s = sinf(angle);
-  // y[d] = x[d]*cos + rot[d]*sin with rot = (-x[d+half], x[d-half])
+// y[d] = x[d]*cos + rot[d]*sin with rot = (-x[d+half], x[d-half])
+__device__ inline void rope_rot(float xl, float xh, float c, float s, float &yl, float &yh) {
   yl = xl * c + (-xh) * s;
   yh = xh * c + xl * s;
+}
+__device__ inline void rope_pair(float xl, float xh, float angle, float &yl, float &yh) {
+  rope_rot(xl, xh, cosf(angle), sinf(angle), yl, yh);
+}
+__device__ inline float rope_inv_freq(float theta, int64_t i, int64_t head_dim) {
+  return 1.0f / powf(theta, (float)(2 * i) / (float)head_dim);
 }
 template <uint32_t F, bool VEC>
 __global__ __launch_bounds__(256) void rope_kernel(const void *x, void *y,
@@ -183,8 +188,7 @@ __global__ __launch_bounds__(256) void rope_kernel(const void *x, void *y,
       load8<F>(x, hi, xh);
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        const float inv_freq = 1.0f / powf(theta, (float)(2 * (i0 + k)) / (float)head_dim);
-        rope_pair(xl[k], xh[k], pos * inv_freq, yl[k], yh[k]);
+        rope_pair(xl[k], xh[k], pos * rope_inv_freq(theta, i0 + k, head_dim), yl[k], yh[k]);
       }
       store8<F>(y, lo, yl);
       store8<F>(y, hi, yh);
@@ -196,11 +200,57 @@ __global__ __launch_bounds__(256) void rope_kernel(const void *x, void *y,
       const int64_t rowi = e / half;  // (token, head)
       const int64_t t = rowi / heads;
       const int64_t lo = rowi * head_dim + i, hi = lo + half;
-      const float inv_freq = 1.0f / powf(theta, (float)(2 * i) / (float)head_dim);
       float yl, yh;
-      rope_pair(load_as_f32<F>(x, lo), load_as_f32<F>(x, hi), (float)positions[t] * inv_freq, yl, yh);
+      rope_pair(load_as_f32<F>(x, lo), load_as_f32<F>(x, hi), (float)positions[t] * rope_inv_freq(theta, i, head_dim),
+                yl, yh);
       store_from_f32<F>(y, lo, yl);
       store_from_f32<F>(y, hi, yh);
+    }
+  }
+}
+
+// RoPE fused into the token-major -> head-major re-layout of a projection:
+// y[h, t, :] = RoPE(x[t * ts + h * head_dim + :]) with the rope region's own
+// expressions (rope_inv_freq, pos * inv_freq, cosf/sinf, rope_rot), so it
+// equals head_permute followed by rope bit for bit.  One thread serves 8
+// frequencies of one token for a group of HG heads and takes the 8 angles'
+// cos/sin once for the group (the rope region recomputes them per head).
+// head_dim % 16 == 0, ts % 8 == 0, 16-byte aligned tensors.
+template <uint32_t F, int HG>
+__global__ __launch_bounds__(256) void permute_rope_kernel(const void *x, void *y, int64_t tokens,
+                                                           int64_t heads, int64_t head_dim, int64_t ts,
+                                                           const int32_t *__restrict__ positions,
+                                                           float theta) {
+  const int64_t half = head_dim / 2, per_row = half / 8;
+  const int64_t total = tokens * per_row * ((heads + HG - 1) / HG);
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+    // e = (group, token, chunk): consecutive lanes read consecutive chunks of
+    // a token's heads and write consecutive chunks of head-major rows
+    const int64_t c = e % per_row, tg = e / per_row;
+    const int64_t t = tg % tokens, hg = tg / tokens;
+    const int64_t i0 = c * 8;
+    const float pos = (float)positions[t];
+    float cs[8], sn[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float angle = pos * rope_inv_freq(theta, i0 + k, head_dim);
+      cs[k] = cosf(angle);
+      sn[k] = sinf(angle);
+    }
+#pragma unroll
+    for (int hh = 0; hh < HG; ++hh) {
+      const int64_t h = hg * HG + hh;
+      if (h >= heads) break;
+      const int64_t src = t * ts + h * head_dim + i0;
+      const int64_t dst = (h * tokens + t) * head_dim + i0;
+      float xl[8], xh[8], yl[8], yh[8];
+      load8<F>(x, src, xl);
+      load8<F>(x, src + half, xh);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) rope_rot(xl[k], xh[k], cs[k], sn[k], yl[k], yh[k]);
+      store8<F>(y, dst, yl);
+      store8<F>(y, dst + half, yh);
     }
   }
 }
@@ -331,6 +381,54 @@ extern "C" int wafer_hip_rope(wafer_hip_context *ctx, uint32_t format, const voi
   DISPATCH_FB(format, vec, rope_kernel, dim3(grid_for(vec ? count / 16 : count / 2)), dim3(256), x, y,
               (int64_t)tokens, (int64_t)heads, (int64_t)head_dim, positions, theta);
   return launch_status("rope_kernel");
+}
+
+template <uint32_t F>
+void launch_permute_rope(hipStream_t st, int hg, dim3 grid, const void *src, void *dst, int64_t tokens,
+                         int64_t heads, int64_t head_dim, int64_t ts, const int32_t *positions, float theta) {
+  if (hg == 8)
+    hipLaunchKernelGGL((permute_rope_kernel<F, 8>), grid, dim3(256), 0, st, src, dst, tokens, heads, head_dim, ts,
+                       positions, theta);
+  else if (hg == 4)
+    hipLaunchKernelGGL((permute_rope_kernel<F, 4>), grid, dim3(256), 0, st, src, dst, tokens, heads, head_dim, ts,
+                       positions, theta);
+  else if (hg == 2)
+    hipLaunchKernelGGL((permute_rope_kernel<F, 2>), grid, dim3(256), 0, st, src, dst, tokens, heads, head_dim, ts,
+                       positions, theta);
+  else
+    hipLaunchKernelGGL((permute_rope_kernel<F, 1>), grid, dim3(256), 0, st, src, dst, tokens, heads, head_dim, ts,
+                       positions, theta);
+}
+
+extern "C" int wafer_hip_head_permute_rope(wafer_hip_context *ctx, uint32_t format, const void *src,
+                                           void *dst, uint64_t tokens, uint64_t heads,
+                                           uint64_t head_dim, uint64_t token_stride,
+                                           const int32_t *positions, float theta) {
+  WAFER_TRY(prologue(ctx, format, "head_permute_rope"));
+  if (tokens == 0 || heads == 0 || head_dim == 0) return WAFER_HIP_OK;
+  if (!src || !dst || !positions) return fail(WAFER_HIP_E_INVALID_FIELD, "head_permute_rope: null tensor");
+  if (head_dim % 16 || token_stride % 8)
+    return fail(WAFER_HIP_E_UNSUPPORTED, "head_permute_rope: head_dim must be a multiple of 16, token_stride of 8");
+  if (token_stride < heads * head_dim)
+    return fail(WAFER_HIP_E_INVALID_FIELD, "head_permute_rope: token_stride < heads * head_dim");
+  if (!aligned16(src) || !aligned16(dst))
+    return fail(WAFER_HIP_E_INVALID_FIELD, "head_permute_rope: tensors must be 16-byte aligned");
+  // the largest head group (8, 4, 2, 1) that keeps the grid at 32768
+  // threads or more: the cos/sin work shrinks with the group, the memory
+  // parallelism with the thread count
+  const uint64_t rows = tokens * (head_dim / 16);
+  int hg = 8;
+  while (hg > 1 && rows * ((heads + hg - 1) / hg) < 32768) hg /= 2;
+  const uint64_t total = rows * ((heads + hg - 1) / hg);
+  const dim3 grid(grid_for(total));
+  const int64_t a0 = (int64_t)tokens, a1 = (int64_t)heads, a2 = (int64_t)head_dim, a3 = (int64_t)token_stride;
+  if (format == WAFER_FMT_F32)
+    launch_permute_rope<WAFER_FMT_F32>(ctx->stream, hg, grid, src, dst, a0, a1, a2, a3, positions, theta);
+  else if (format == WAFER_FMT_BF16)
+    launch_permute_rope<WAFER_FMT_BF16>(ctx->stream, hg, grid, src, dst, a0, a1, a2, a3, positions, theta);
+  else
+    launch_permute_rope<WAFER_FMT_F16>(ctx->stream, hg, grid, src, dst, a0, a1, a2, a3, positions, theta);
+  return launch_status("permute_rope_kernel");
 }
 
 extern "C" int wafer_hip_bias_add(wafer_hip_context *ctx, uint32_t format, const void *x,

@@ -5,8 +5,8 @@ backend, each one a C-ABI call of ``libwafer_hip.so`` on the caller's stream:
 
     h    = RMSNorm(x) * w_in                          wafer_hip_rmsnorm
     qkv  = h . Wqkv^T        [T, (Hq + 2 Hkv) D]      wafer_hip_gemm_mfma (bf16 MFMA)
-    q,k,v -> head-major      [H, T, D]                wafer_hip_head_permute
-    q,k  = RoPE(q), RoPE(k)  rotate-half, theta       wafer_hip_rope
+    q,k  = RoPE(q), RoPE(k) -> head-major [H, T, D]  wafer_hip_head_permute_rope
+    v    -> head-major       [Hkv, T, D]              wafer_hip_head_permute
     o    = causal GQA attention(q, k, v)              wafer_hip_attention_prefill (FA)
     a    = o -> token-major  [T, Hq D]                wafer_hip_head_permute
     x1   = x + a . Wo^T                               wafer_hip_gemm_mfma, wafer_hip_elementwise(Add)
@@ -81,8 +81,10 @@ class DecoderLayer:
         e = lambda *s: torch.empty(s, dtype=bf, device=dev)
         self.h = e(T, hidden)
         self.qkv = e(T, qkv_n)
-        self.q = e(q_heads, T, head_dim)
-        self.k = e(kv_heads, T, head_dim)
+        # Q and K head-major in one buffer: one permute+RoPE call over their
+        # Hq + Hkv heads, which sit side by side in each QKV row
+        self.qk = e(q_heads + kv_heads, T, head_dim)
+        self.q, self.k = self.qk[:q_heads], self.qk[q_heads:]
         self.v = e(kv_heads, T, head_dim)
         self.o = e(q_heads, T, head_dim)
         self.attn = e(T, hidden)
@@ -90,11 +92,7 @@ class DecoderLayer:
         self.x1 = e(T, hidden)
         self.act = e(T, ffn)
         self.down = e(T, hidden)
-        # RoPE runs on the head-major tensors as [heads*T, 1, D] rows, so the
-        # position of row (h, t) is t
-        pos = torch.arange(T, dtype=torch.int32, device=dev)
-        self.pos_q = pos.repeat(q_heads)
-        self.pos_k = pos.repeat(kv_heads)
+        self.pos = torch.arange(T, dtype=torch.int32, device=dev)
 
     def forward(self, x, y):
         """x, y: bf16 [tokens, hidden] device tensors (y may not alias x)."""
@@ -103,11 +101,8 @@ class DecoderLayer:
         qkv_n = self.qkv.shape[1]
         hip.rmsnorm(x, self.w_in, self.h, self.eps)
         hip.gemm_mfma(self.h, self.wqkv, self.qkv, T, Hd, qkv_n, out_fmt=B.BF16, rhs_t=True)
-        hip.head_permute(self.qkv, self.q, T, Hq, D, qkv_n, 0)
-        hip.head_permute(self.qkv, self.k, T, Hkv, D, qkv_n, 0, src_offset=Hq * D)
+        hip.head_permute_rope(self.qkv, self.qk, T, Hq + Hkv, D, qkv_n, self.pos, self.theta)
         hip.head_permute(self.qkv, self.v, T, Hkv, D, qkv_n, 0, src_offset=(Hq + Hkv) * D)
-        hip.rope(self.q.view(Hq * T, 1, D), self.q.view(Hq * T, 1, D), self.pos_q, self.theta)
-        hip.rope(self.k.view(Hkv * T, 1, D), self.k.view(Hkv * T, 1, D), self.pos_k, self.theta)
         hip.attention_prefill(self.q.view(1, Hq, T, D), self.k.view(1, Hkv, T, D), self.v.view(1, Hkv, T, D),
                               self.o.view(1, Hq, T, D), 1.0 / math.sqrt(D), causal=True)
         hip.head_permute(self.o, self.attn, T, Hq, D, Hd, 1)
