@@ -178,6 +178,17 @@ int wafer_hip_convert(wafer_hip_context *ctx, uint32_t opcode,
  * validating a FormalConvertOperation's descriptors (host only). */
 int wafer_hip_convert_route(uint32_t opcode, uint32_t *source_format,
                             uint32_t *destination_format);
+/* The managed lane works in the non-NaN domain: it refuses a NaN input
+ * value and a NaN result (decodeNonNaN / encodeNonNaN,
+ * lib/Wafer/Simulator/Reference/ManagedReferenceTargetModel.cpp:137-185).
+ * wafer_hip_elementwise / _convert / _reduce compute IEEE results (a NaN
+ * propagates); a caller that needs the managed lane's refusal checks the
+ * logical inputs and the result with this entry, as the C++ seam does.
+ * *first = the index of the first NaN among `count` F16/BF16/F32 values, or
+ * `count` when there is none.  Synchronous (reads the index back); refused on
+ * a capturing stream. */
+int wafer_hip_first_nan(wafer_hip_context *ctx, uint32_t format,
+                        const void *values, uint64_t count, uint64_t *first);
 /* op TargetReduceOperation {Sum, Max, Min} and dim TargetReduceDimension
  * (TargetOperation.h:102-113); shape is the logical shape (rank <= 8) and dst
  * holds the shape with reduced dimensions set to 1. */

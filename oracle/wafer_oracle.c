@@ -947,7 +947,10 @@ int oracle_rope(int format, const void *x, void *y, int64_t tokens,
   return 0;
 }
 
-/* Bias add in F32 then narrow (a CT Add with an F32 broadcast operand). */
+/* Bias add in F32 then narrow (a CT Add with an F32 broadcast operand: the
+ * managed lane's `float` Add, ManagedReferenceTargetModel.cpp:245, then the
+ * output format's RNE store).  Pinned by numpy's IEEE float32 add and its
+ * float16 / a bit-level bf16 RNE narrowing (test_bias_add_closed_form). */
 int oracle_bias_add(int format, const void *x, const float *bias, void *y,
                     int64_t rows, int64_t cols) {
   if (!float_format(format)) return -1;

@@ -91,7 +91,8 @@ void gemm_case(HipTargetModelBackend &be, std::mt19937 &rng, LogicalFormat fin, 
   if (psum) ps = desc(LogicalFormat::F32, L, shp(M, N));
   auto a = random_logical(lhs, rng), b = random_logical(rhs, rng);
   std::vector<uint8_t> p = psum ? random_logical(*ps, rng) : std::vector<uint8_t>{};
-  TargetModelGemmRequest req{FormalGemmOperation{lhs, rhs, dst, M, K, N, B, TargetGemmOrientation::Normal,
+  TargetModelGemmRequest req{FormalGemmOperation{lhs, rhs, dst, M, K, N, B, *getCanonicalFormalGemmGeometry(batched ? 3 : 2),
+                                                 TargetGemmOrientation::Normal,
                                                  rt ? TargetGemmOrientation::Transpose : TargetGemmOrientation::Normal, ps},
                              TargetModelNumericOperands{{{lhs, to_physical(lhs, a, 0)}, {rhs, to_physical(rhs, b, 0)}},
                                                         {dst, std::vector<uint8_t>(*dst.getStorageBytes(), 0xA5)}}};
@@ -109,6 +110,7 @@ void gemm_case(HipTargetModelBackend &be, std::mt19937 &rng, LogicalFormat fin, 
   }
   const TargetModelOneDNNResult &res = **r;
   check(res.destination.key == dst && res.destination.storage == want, "  gemm bytes equal the formal lane, template bytes kept");
+  check(!res.flags.any(), "  gemm flags empty, as the managed lane returns them");
   check(res.evidence.matmulInvocations == 1 && res.evidence.reorderInvocations <= 1 &&
             res.evidence.formalFusedMultiplyAdds == 0 && !res.evidence.evidenceDigest.empty() &&
             !res.evidence.implementation.empty(),
@@ -174,7 +176,8 @@ int main() {
     PhysicalTensorDescriptor s = desc(LogicalFormat::F32, PhysicalTensorLayout::Cx, {21, 300});
     PhysicalTensorDescriptor d = desc(LogicalFormat::BF16, PhysicalTensorLayout::Cx, {21, 300});
     auto x = random_logical(s, rng, 1e3f);
-    TargetModelConvertRequest req{FormalConvertOperation{167, s, d},
+    TargetModelConvertRequest req{FormalConvertOperation{167, s, d, TargetConvertParameter::roundingMode(
+                                                                     TargetRoundingMode::NearestEven)},
                                   TargetModelNumericOperands{{{s, to_physical(s, x, 0)}},
                                                              {d, std::vector<uint8_t>(*d.getStorageBytes(), 0x77)}}};
     std::vector<uint8_t> wl(d.getElementCount() * 2);
@@ -182,7 +185,7 @@ int main() {
     auto r = be.execute(req, budget);
     check((bool)r && r->destination.storage == to_physical(d, wl, 0x77), "convert F32->BF16 (route 167) Cx");
     // route/format mismatch: BF16 descriptors with the F32->BF16 route
-    TargetModelConvertRequest bad{FormalConvertOperation{167, d, d},
+    TargetModelConvertRequest bad{FormalConvertOperation{167, d, d, std::nullopt},
                                   TargetModelNumericOperands{{{d, std::vector<uint8_t>(*d.getStorageBytes(), 0)}},
                                                              {d, std::vector<uint8_t>(*d.getStorageBytes(), 0)}}};
     auto rb = be.execute(bad, budget);
@@ -206,6 +209,124 @@ int main() {
           "reduce Sum Trailing0 f32 NCx (evaluations = input elements)");
   }
 
+  // ---- the managed lane's domain (ManagedReferenceTargetModel.cpp:137-458):
+  // each refusal fails with ManagedReferenceBackendFailure and the
+  // reference's message, and returns no output
+  {
+    auto refused = [&](const auto &r, const char *message, const char *name) {
+      const bool ok = !r && r.error().code == TargetModelKernelErrorCode::ManagedReferenceBackendFailure &&
+                      r.error().detail == std::string("managed-reference tensor: ") + message;
+      check(ok, name);
+      if (!ok && !r) std::printf("     got %s: %s\n", stringifyTargetModelKernelErrorCode(r.error().code),
+                                 r.error().detail.c_str());
+    };
+    auto set_f32 = [](std::vector<uint8_t> &v, size_t i, uint32_t bits) { std::memcpy(&v[4 * i], &bits, 4); };
+    PhysicalTensorDescriptor f = desc(LogicalFormat::F32, PhysicalTensorLayout::Cx, {6, 70});
+    PhysicalTensorDescriptor b = desc(LogicalFormat::BF16, PhysicalTensorLayout::Cx, {6, 70});
+    auto tmpl = [](const PhysicalTensorDescriptor &d) { return std::vector<uint8_t>(*d.getStorageBytes(), 0x3C); };
+    auto x = random_logical(f, rng);
+    // convert: a TowardZero parameter; a zero-point parameter
+    {
+      TargetModelConvertRequest r{FormalConvertOperation{167, f, b, TargetConvertParameter::roundingMode(
+                                                                        TargetRoundingMode::TowardZero)},
+                                  TargetModelNumericOperands{{{f, to_physical(f, x, 0)}}, {b, tmpl(b)}}};
+      refused(be.execute(r, budget), "convert is not nearest-even", "convert TowardZero is refused");
+      r.operation.parameter = TargetConvertParameter::zeroPoint(3);
+      refused(be.execute(r, budget), "convert is not nearest-even", "convert with a zero point is refused");
+    }
+    // convert: an integer route, and one layout to another
+    {
+      PhysicalTensorDescriptor i32 = desc(LogicalFormat::I32, PhysicalTensorLayout::Cx, {6, 70});
+      TargetModelConvertRequest r{FormalConvertOperation{149, i32, f, std::nullopt},
+                                  TargetModelNumericOperands{{{i32, std::vector<uint8_t>(*i32.getStorageBytes(), 0)}},
+                                                             {f, tmpl(f)}}};
+      refused(be.execute(r, budget), "convert is outside the F16/BF16/F32 same-shape domain",
+              "convert I32->F32 is outside the managed domain");
+      PhysicalTensorDescriptor bt = desc(LogicalFormat::BF16, PhysicalTensorLayout::Tensor, {6, 70});
+      TargetModelConvertRequest r2{FormalConvertOperation{167, f, bt, std::nullopt},
+                                   TargetModelNumericOperands{{{f, to_physical(f, x, 0)}}, {bt, tmpl(bt)}}};
+      refused(be.execute(r2, budget), "convert is outside the F16/BF16/F32 same-shape domain",
+              "convert Cx -> Tensor layout is outside the managed domain");
+    }
+    // convert: a NaN input
+    {
+      auto xn = x;
+      set_f32(xn, 131, 0x7fc00000u);
+      TargetModelConvertRequest r{FormalConvertOperation{167, f, b, std::nullopt},
+                                  TargetModelNumericOperands{{{f, to_physical(f, xn, 0)}}, {b, tmpl(b)}}};
+      refused(be.execute(r, budget), "input value is outside the non-NaN domain", "convert of a NaN is refused");
+    }
+    // elementwise: NaN result (Sqrt of a negative), NaN input (Add), an
+    // operation outside the managed set, an arity mismatch
+    {
+      TargetModelElementwiseRequest r{FormalElementwiseOperation{TargetElementwiseOperation::Sqrt, {f}, f},
+                                      TargetModelNumericOperands{{{f, to_physical(f, x, 0)}}, {f, tmpl(f)}}};
+      refused(be.execute(r, budget), "result value is outside the non-NaN domain", "Sqrt of a negative is refused");
+      auto xa = x, xb = x;  // xa = |x|
+      for (size_t i = 0; i < f.getElementCount(); ++i) {
+        float v;
+        std::memcpy(&v, &x[4 * i], 4);
+        v = v < 0 ? -v : v;
+        std::memcpy(&xa[4 * i], &v, 4);
+      }
+      set_f32(xb, 17, 0xffc00000u);
+      TargetModelElementwiseRequest r2{FormalElementwiseOperation{TargetElementwiseOperation::Add, {f, f}, f},
+                                       TargetModelNumericOperands{{{f, to_physical(f, xa, 0)}, {f, to_physical(f, xb, 0)}},
+                                                                  {f, tmpl(f)}}};
+      refused(be.execute(r2, budget), "input value is outside the non-NaN domain", "Add with a NaN input is refused");
+      TargetModelElementwiseRequest r3{FormalElementwiseOperation{TargetElementwiseOperation::Eq, {f, f}, f},
+                                       TargetModelNumericOperands{{{f, to_physical(f, xa, 0)}, {f, to_physical(f, xa, 0)}},
+                                                                  {f, tmpl(f)}}};
+      refused(be.execute(r3, budget), "elementwise operation is not in the managed domain", "Eq is refused");
+      TargetModelElementwiseRequest r4{FormalElementwiseOperation{TargetElementwiseOperation::Add, {f}, f},
+                                       TargetModelNumericOperands{{{f, to_physical(f, xa, 0)}}, {f, tmpl(f)}}};
+      refused(be.execute(r4, budget), "elementwise input arity does not match semantics", "unary Add is refused");
+      // and the positive counterpart: the same Sqrt on |x| succeeds with empty flags
+      TargetModelElementwiseRequest r5{FormalElementwiseOperation{TargetElementwiseOperation::Sqrt, {f}, f},
+                                       TargetModelNumericOperands{{{f, to_physical(f, xa, 0)}}, {f, tmpl(f)}}};
+      auto ok = be.execute(r5, budget);
+      check((bool)ok && !ok->flags.any(), "Sqrt of |x| succeeds with empty flags");
+    }
+    // reduce: a BF16 Sum, an accumulator that meets +inf and -inf, a NaN input to Max
+    {
+      PhysicalTensorDescriptor in = desc(LogicalFormat::BF16, PhysicalTensorLayout::NCx, {2, 3, 4, 40});
+      PhysicalTensorDescriptor out = desc(LogicalFormat::BF16, PhysicalTensorLayout::NCx, {2, 3, 4, 1});
+      TargetModelReduceRequest r{FormalReduceOperation{TargetReduceOperation::Sum, in, out, TargetReduceDimension::Trailing0},
+                                 TargetModelNumericOperands{{{in, std::vector<uint8_t>(*in.getStorageBytes(), 0)}},
+                                                            {out, tmpl(out)}}};
+      refused(be.execute(r, budget), "reduce requires F32 sum or F16/BF16/F32 max/min", "BF16 Sum is refused");
+      PhysicalTensorDescriptor fi = desc(LogicalFormat::F32, PhysicalTensorLayout::NCx, {2, 3, 4, 40});
+      PhysicalTensorDescriptor fo = desc(LogicalFormat::F32, PhysicalTensorLayout::NCx, {2, 3, 4, 1});
+      auto xi = random_logical(fi, rng);
+      set_f32(xi, 45, 0x7f800000u);
+      set_f32(xi, 77, 0xff800000u);  // same row (40..79) as index 45
+      TargetModelReduceRequest r2{FormalReduceOperation{TargetReduceOperation::Sum, fi, fo, TargetReduceDimension::Trailing0},
+                                  TargetModelNumericOperands{{{fi, to_physical(fi, xi, 0)}}, {fo, tmpl(fo)}}};
+      refused(be.execute(r2, budget), "reduce accumulator left the non-NaN domain", "Sum of +inf and -inf is refused");
+      auto xm = random_logical(fi, rng);
+      set_f32(xm, 300, 0x7fc00001u);
+      TargetModelReduceRequest r3{FormalReduceOperation{TargetReduceOperation::Max, fi, fo, TargetReduceDimension::Trailing0},
+                                  TargetModelNumericOperands{{{fi, to_physical(fi, xm, 0)}}, {fo, tmpl(fo)}}};
+      refused(be.execute(r3, budget), "input value is outside the non-NaN domain", "Max over a NaN is refused");
+    }
+    // GEMM: axes other than the canonical ones
+    {
+      PhysicalTensorDescriptor l = desc(LogicalFormat::F32, PhysicalTensorLayout::Cx, {8, 64});
+      PhysicalTensorDescriptor d = desc(LogicalFormat::F32, PhysicalTensorLayout::Cx, {8, 8});
+      PhysicalTensorDescriptor rr = desc(LogicalFormat::F32, PhysicalTensorLayout::Cx, {64, 8});
+      FormalGemmGeometry axes = *getCanonicalFormalGemmGeometry(2);
+      std::swap(axes.lhsMDimension, axes.lhsContractingDimension);
+      TargetModelGemmRequest g{FormalGemmOperation{l, rr, d, 8, 64, 8, 1, axes, TargetGemmOrientation::Normal,
+                                                   TargetGemmOrientation::Normal, std::nullopt},
+                               TargetModelNumericOperands{{{l, std::vector<uint8_t>(*l.getStorageBytes(), 0)},
+                                                           {rr, std::vector<uint8_t>(*rr.getStorageBytes(), 0)}},
+                                                          {d, tmpl(d)}}};
+      auto rg = be.tryExecute(g);
+      check(!rg && rg.error().code == TargetModelKernelErrorCode::InvalidCommandField,
+            "GEMM with non-canonical axes is refused");
+    }
+  }
+
   // ---- bad requests fail with no output
   {
     PhysicalTensorDescriptor d = desc(LogicalFormat::F32, PhysicalTensorLayout::Cx, {4, 64});
@@ -215,7 +336,8 @@ int main() {
     auto r = be.execute(req, budget);
     check(!r && r.error().code == TargetModelKernelErrorCode::InvalidCommandField, "short input storage fails");
     PhysicalTensorDescriptor i8 = desc(LogicalFormat::I8, PhysicalTensorLayout::Cx, {4, 128});
-    TargetModelGemmRequest g{FormalGemmOperation{i8, i8, i8, 4, 128, 4, 1, TargetGemmOrientation::Normal,
+    TargetModelGemmRequest g{FormalGemmOperation{i8, i8, i8, 4, 128, 4, 1, *getCanonicalFormalGemmGeometry(2),
+                                                 TargetGemmOrientation::Normal,
                                                  TargetGemmOrientation::Normal, std::nullopt},
                              TargetModelNumericOperands{{{i8, std::vector<uint8_t>(*i8.getStorageBytes(), 0)},
                                                          {i8, std::vector<uint8_t>(*i8.getStorageBytes(), 0)}},

@@ -8,11 +8,20 @@ test/Tools/Inputs/wafer_pytorch_xla_capture.py:1183-1260) on the same bf16
 weights and input.  The backend stores every intermediate in bf16 while the
 reference keeps float32 throughout, so the bound is a tolerance:
 
-  on the layer's update d = y - x (the residual stream itself would hide
-  errors): cosine >= 0.9995 and relative L2 <= 0.03; on y: relative L2 <= 0.01
-  (the attention policy's bound; y's own bf16 rounding is ~0.001 of it).
+  at BASELINE config 4, the attention policy (cosine >= 0.9999, relative
+  L2 <= 0.01) on the layer's update d = y - x (the residual stream itself
+  would hide errors) and on y;
+  on the small T=256, hidden-1024 layer, whose update has fewer terms per
+  output and so a larger relative share of bf16 storage rounding: cosine >=
+  0.9998 and relative L2 <= 0.02 on the update, relative L2 <= 0.01 on y.
 Measured: T=256 small layer cos 0.99993 / relL2 0.012 (update), 0.0026 (y);
 BASELINE config 4 cos 0.99998 / relL2 0.0062 (update), 0.0057 (y).
+
+The layer is also composed from the CPU oracle's regions (formal-order bf16
+GEMMs, RMSNorm, RoPE, online-softmax attention with 64-key blocks, SiLU-mul,
+managed Add), which round every intermediate to bf16 where the backend does,
+and the backend's output on sampled tokens is held to the attention gate
+against it (test_decoder_layer_vs_oracle_composition).
 """
 import math
 
@@ -165,7 +174,10 @@ def test_decoder_layer_vs_torch_f32(hip, torch, T, Hd, Hq, Hkv, F):
     cos_d, rel_d = stats(torch, y.float() - x.float(), ref - x.float())
     _, rel_y = stats(torch, y.float(), ref)
     print(f"update cos {cos_d:.6f} relL2 {rel_d:.5f}; output relL2 {rel_y:.6f}", flush=True)
-    assert cos_d >= 0.9995 and rel_d <= 0.03
+    if T == 1024:  # the attention policy
+        assert cos_d >= 0.9999 and rel_d <= 0.01
+    else:
+        assert cos_d >= 0.9998 and rel_d <= 0.02
     assert rel_y <= 0.01
     # determinism: a second forward gives the same bits
     y2 = torch.empty_like(x)
@@ -173,3 +185,63 @@ def test_decoder_layer_vs_torch_f32(hip, torch, T, Hd, Hq, Hkv, F):
     torch.cuda.synchronize()
     assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
 
+
+
+def test_decoder_layer_vs_oracle_composition(hip, torch, oracle):
+    """BASELINE config 4 against the CPU oracle's composition of the same
+    regions, on sampled tokens.  K and V are formed for every token (the
+    sampled tokens attend to all earlier ones); Q, attention, the output
+    projection, the residual Adds, RMSNorm and the SwiGLU FFN only for the
+    sampled tokens.  Every intermediate is bf16, as in the backend, so the
+    two differ only by accumulation order (MFMA vs k-order fma, tree vs
+    sequential row sums) and FA's lazy rescale.  Gate: the attention policy
+    (rtol 0.006, atol 0.008, cosine >= 0.9999, relative L2 <= 0.01) on y and
+    on the update y - x."""
+    import numpy as np
+
+    from tests.similarity import attention_gate, stats as sim_stats
+    from vibe_compiler_amd import decoder_layer as DL
+
+    T, Hd, Hq, Hkv, D, F = 1024, 4096, 32, 8, 128, 14336
+    eps, theta = 1e-5, 1e4
+    print("decoder layer vs oracle composition (config 4, sampled tokens)", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(20260805)
+    W = DL.random_weights(torch, gen, hidden=Hd, q_heads=Hq, kv_heads=Hkv, head_dim=D, ffn=F)
+    x = torch.randn((T, Hd), device="cuda", generator=gen).to(torch.bfloat16)
+    layer = DL.DecoderLayer(hip, W, T, hidden=Hd, q_heads=Hq, kv_heads=Hkv, head_dim=D, ffn=F)
+    y = torch.empty_like(x)
+    layer.forward(x, y)
+    torch.cuda.synchronize()
+    u16 = lambda t: t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+    xb, yb = u16(x), u16(y)
+    Wn = {k: u16(v) for k, v in W.items()}
+    BF = oracle.BF16
+    gemm = lambda a, w, n: oracle.gemm_formal(BF, BF, a, w, a.shape[0], a.shape[1], n,
+                                              rhs_t=True).reshape(a.shape[0], n)
+    h = oracle.rmsnorm(xb, Wn["input_norm"], eps)
+    wqkv = Wn["wqkv"]
+    kv = gemm(h, np.ascontiguousarray(wqkv[Hq * D:]), 2 * Hkv * D)
+    pos = np.arange(T, dtype=np.int32)
+    k = oracle.rope(np.ascontiguousarray(kv[:, :Hkv * D]).reshape(T, Hkv, D), pos, theta)
+    v = np.ascontiguousarray(kv[:, Hkv * D:]).reshape(T, Hkv, D)
+    idx = np.array([0, 1, 63, 64, 200, 511, 777, 1023])
+    q = oracle.rope(gemm(np.ascontiguousarray(h[idx]), np.ascontiguousarray(wqkv[:Hq * D]), Hq * D)
+                    .reshape(len(idx), Hq, D), idx.astype(np.int32), theta)
+    o = np.zeros((len(idx), Hq, D), np.uint16)
+    for i, t in enumerate(idx):
+        kt = np.ascontiguousarray(k[:t + 1].transpose(1, 0, 2))[None]
+        vt = np.ascontiguousarray(v[:t + 1].transpose(1, 0, 2))[None]
+        o[i] = oracle.attention_prefill(q[i][None, :, None, :], kt, vt, 1.0 / math.sqrt(D),
+                                        causal=False, block_k=64)[0, :, 0, :]
+    add = 8  # TargetElementwiseOperation::Add
+    x1 = oracle.elementwise(add, BF, np.ascontiguousarray(xb[idx]), gemm(o.reshape(len(idx), Hd), Wn["wo"], Hd))
+    h2 = oracle.rmsnorm(x1, Wn["post_norm"], eps)
+    act = oracle.silu_mul(gemm(h2, Wn["wgate"], F), gemm(h2, Wn["wup"], F))
+    yo = oracle.elementwise(add, BF, x1, gemm(act, Wn["wdown"], Hd))
+    got = oracle.bf16_to_f32(yb[idx]).reshape(len(idx), Hd).astype(np.float64)
+    exp = oracle.bf16_to_f32(yo).reshape(len(idx), Hd).astype(np.float64)
+    xf = oracle.bf16_to_f32(xb[idx]).reshape(len(idx), Hd).astype(np.float64)
+    cos_d, rel_d, _ = sim_stats(got - xf, exp - xf)
+    print(f"vs oracle: update cos {cos_d:.7f} relL2 {rel_d:.5f}", flush=True)
+    attention_gate(got, exp, what="decoder layer y vs oracle composition")
+    assert cos_d >= 0.9999 and rel_d <= 0.01

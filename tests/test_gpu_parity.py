@@ -262,6 +262,38 @@ def test_i8_gemm_baseline_size_rows(hip, B, oracle):
     assert np.array_equal(accg.astype(np.int64).sum(0), colsum)
 
 
+@pytest.mark.parametrize("rt", [0, 1])
+def test_i8_gemm_baseline_size_y_only(hip, B, oracle, rt):
+    """BASELINE config 3 exactly as the bench runs it: 4096^3 with no
+    accumulator output, which takes the 256x256 tiles with the LDS-staged
+    dequant epilogue (passing acc_out switches the staging off).  y must be
+    bit-identical to the acc_out run's y, and to the int64 closed form plus
+    the dequant chain bf16(f32(f32(acc) * scale)) on sampled rows."""
+    say("i8 gemm 4096^3 y-only", rt)
+    rng = np.random.default_rng(20260804 + rt)
+    M = N = K = 4096
+    a = rng.integers(-127, 128, size=(M, K), dtype=np.int64).astype(np.int8)
+    b = rng.integers(-127, 128, size=(K, N), dtype=np.int64).astype(np.int8)
+    bb = np.ascontiguousarray(b.T) if rt else b
+    scale = rng.uniform(0.001, 0.01, size=N).astype(np.float32)
+    ad, bd, sd = dev(a), dev(bb), dev(scale)
+    y_only = torch.full((M, N), 0x1234, dtype=torch.int16, device="cuda")
+    hip.gemm_i8(ad, bd, sd, y_only, M, K, N, rhs_t=bool(rt))
+    acc = torch.zeros((M, N), dtype=torch.int32, device="cuda")
+    y_acc = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    hip.gemm_i8(ad, bd, sd, y_acc, M, K, N, acc_out=acc, rhs_t=bool(rt))
+    yo, ya = host(y_only).view(np.uint16), host(y_acc).view(np.uint16)
+    assert np.array_equal(yo, ya)
+    rows = np.concatenate([[0, 1, 127, 128, 255, 256, 2047, 4095], rng.choice(M, 16, replace=False)])
+    exact = a[rows].astype(np.int64) @ b.astype(np.int64)
+    yr = oracle.f32_to_bf16((exact.astype(np.float32) * scale).astype(np.float32)).reshape(exact.shape)
+    assert np.array_equal(yo[rows], yr)
+    # every column of every 256-wide tile: the accumulator's column sums
+    # (checked exactly against (colsum A) @ B) feed the same y
+    colsum = a.astype(np.int64).sum(0) @ b.astype(np.int64)
+    assert np.array_equal(host(acc).astype(np.int64).sum(0), colsum)
+
+
 @pytest.mark.parametrize("m,k,n,rt", [(100, 192, 130, 0), (1, 64, 1, 1), (300, 128, 257, 0), (129, 256, 200, 1),
                                       (257, 64, 128, 0), (130, 320, 384, 1), (64, 128, 1000, 0)])
 def test_i8_gemm_ragged_bit_exact(hip, B, oracle, m, k, n, rt):
@@ -311,6 +343,52 @@ def test_mfma_gemm_vs_formal(hip, B, oracle, m, k, n, rt, fmt):
     gf = oracle.to_float(fmt, gn).reshape(m, n)
     rel = np.linalg.norm(gf - ref) / np.linalg.norm(ref)
     assert rel <= 2e-3 and np.abs(gf - ref).max() <= 2e-2 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("rt,fmt,out", [(1, 3, 3), (0, 3, 5), (1, 2, 2)])
+def test_mfma_gemm_256_tiles_vs_formal(hip, B, oracle, rt, fmt, out):
+    """m = n = 4096, k = 1024: 256 tiles of 256x256, which takes the 256x256
+    instantiation (used only from 192 such tiles on).  Sampled rows against
+    the formal lane run on the GPU (bit-exact k-order fma chains; itself
+    pinned against the CPU oracle on two rows here), held to the MFMA GEMM
+    tolerances: f32 out relL2 <= 1e-5, narrowed out relL2 <= 2e-3."""
+    say("mfma gemm 256x256 tiles", rt, fmt, out)
+    rng = np.random.default_rng(4096 + 10 * rt + fmt)
+    M, K, N = 4096, 1024, 4096
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    b = (rng.standard_normal((K, N)) / math.sqrt(K)).astype(np.float32)
+    if fmt == B.BF16:
+        ah, bh = oracle.f32_to_bf16(a).reshape(a.shape), oracle.f32_to_bf16(b).reshape(b.shape)
+    else:
+        ah, bh = a.astype(np.float16).view(np.uint16), b.astype(np.float16).view(np.uint16)
+    bt = np.ascontiguousarray(bh.T) if rt else bh
+    ad, bd = u16(ah), u16(bt)
+    if out == B.F32:
+        dst = torch.full((M, N), 7.5, dtype=torch.float32, device="cuda")
+    else:
+        dst = torch.full((M, N), 0x1234, dtype=torch.int16, device="cuda")
+    hip.gemm_mfma(ad, bd, dst, M, K, N, in_fmt=fmt, out_fmt=out, rhs_t=bool(rt))
+    got_all = host(dst)
+    rows = np.concatenate([[0, 1, 255, 256, 2047, 4095], rng.choice(M, 26, replace=False)])
+    sub = np.ascontiguousarray(ah[rows])
+    ref_d = torch.zeros((len(rows), N), dtype=torch.float32, device="cuda")
+    hip.gemm(u16(sub), bd, ref_d, len(rows), K, N, in_fmt=fmt, out_fmt=B.F32, rhs_t=bool(rt))
+    ref = host(ref_d)
+    cpu = oracle.gemm_formal(fmt, oracle.F32, np.ascontiguousarray(sub[:2]), bt, 2, K, N, rhs_t=bool(rt))
+    assert np.array_equal(cpu.reshape(2, N).view(np.uint32), ref[:2].view(np.uint32))
+    if out == B.F32:
+        got = got_all[rows]
+        tol_rel, tol_max = 1e-5, 1e-4
+    else:
+        got = oracle.to_float(fmt, got_all.view(np.uint16)[rows]).reshape(len(rows), N)
+        tol_rel, tol_max = 2e-3, 2e-2
+    rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert rel <= tol_rel and np.abs(got - ref).max() <= tol_max * np.abs(ref).max(), (rel,)
+    # every output written (no sentinel left)
+    if out == B.F32:
+        assert not np.any(got_all == 7.5)
+    else:
+        assert int(np.count_nonzero(got_all.view(np.uint16) == 0x1234)) < 64
 
 
 @pytest.mark.parametrize("m,k,n,rt,fmt", [(100, 96, 130, 0, 3), (1, 32, 1, 1, 2), (300, 256, 257, 1, 3),

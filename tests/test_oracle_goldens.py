@@ -509,3 +509,41 @@ def test_fused_regions_vs_float64(oracle):
     xd = xr.astype(np.float64)
     rot = np.concatenate([-xd[..., D // 2:], xd[..., :D // 2]], -1)
     assert np.allclose(y, xd * np.cos(ang) + rot * np.sin(ang), rtol=1e-4, atol=2e-4)
+
+
+def test_bias_add_closed_form(oracle):
+    """bias_add is one IEEE binary32 Add per element (the managed lane's
+    `float` Add, ManagedReferenceTargetModel.cpp:245) followed by the RNE
+    narrowing of the output format: numpy's float32 add, then numpy's own
+    float16 conversion (IEEE RNE) or a round-half-even bf16 narrowing written
+    here from the bit definition.  Edge values cover cancellation to +0,
+    signed zeros, infinities and a bf16 tie in both directions."""
+    rng = np.random.default_rng(951)
+    rows, cols = 7, 193
+    x = rng.standard_normal((rows, cols)).astype(np.float32) * 3
+    b = (rng.standard_normal(cols) * 0.02).astype(np.float32)
+    x[0, :4] = [1.0, -0.0, np.inf, 65504.0]
+    b[:4] = [-1.0, -0.0, 1.0, 16.0]
+    y = oracle.bias_add(x, b, fmt=oracle.F32)
+    ref = (x + b[None, :]).astype(np.float32)
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+    assert y[0, 0].view(np.uint32) == 0 and y[0, 1].view(np.uint32) == 0x80000000
+
+    def bf16_rne(f):
+        u = f.view(np.uint32).astype(np.uint64)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+    # bf16 storage: x is bf16, the sum is formed in f32 and narrowed RNE
+    xb = oracle.f32_to_bf16(x).reshape(x.shape)
+    xb[1, :2] = [0x3F80, 0x3F80]          # 1.0
+    b2 = b.copy()
+    b2[:2] = [f32(0x3B800000), f32(0x3BC00000)]   # 2^-8 (tie, stays even) and 1.5*2^-8 (rounds up)
+    yb = oracle.bias_add(xb, b2, fmt=oracle.BF16)
+    wide = (oracle.bf16_to_f32(xb).reshape(x.shape) + b2[None, :]).astype(np.float32)
+    assert np.array_equal(yb, bf16_rne(wide))
+    assert [int(v) for v in yb[1, :2]] == [0x3F80, 0x3F81]
+    # f16 storage: numpy's float32 -> float16 cast is IEEE RNE with overflow to inf
+    xh = x.astype(np.float16)
+    yh = oracle.bias_add(xh.view(np.uint16), b, fmt=oracle.F16)
+    wideh = (xh.astype(np.float32) + b[None, :]).astype(np.float32)
+    assert np.array_equal(yh, wideh.astype(np.float16).view(np.uint16))

@@ -47,6 +47,7 @@ EXPORTS = (
     "wafer_hip_buffer_free", "wafer_hip_copy_to_device", "wafer_hip_copy_to_host", "wafer_hip_convert_route",
     "wafer_hip_strided_copy", "wafer_hip_memset", "wafer_hip_bit2fp", "wafer_hip_mask_move",
     "wafer_hip_compare_expected", "wafer_hip_compare_statistics", "wafer_hip_environment",
+    "wafer_hip_first_nan",
 )
 
 # ProgramElementType codes (the comparator's dtypes) and verdicts
@@ -140,6 +141,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wafer_hip_memset.argtypes = [vp, vp, u32, u32, u64]
     L.wafer_hip_bit2fp.argtypes = [vp, vp, vp, u32, u64]
     L.wafer_hip_mask_move.argtypes = [vp, vp, vp, vp, u32, u64]
+    L.wafer_hip_first_nan.argtypes = [vp, u32, vp, u64, ctypes.POINTER(u64)]
     pt = ctypes.POINTER(ProgramTensorDesc)
     L.wafer_hip_compare_expected.argtypes = [vp, pt, pt, ctypes.POINTER(ComparisonPolicy), u32p, ctypes.c_char_p,
                                              ctypes.c_size_t]
@@ -174,6 +176,41 @@ def _fits(what, *pairs):
 
 
 _GEMM_ESIZE = {F16: 2, BF16: 2, F32: 4}
+_ESIZE = {I8: 1, U8: 1, BOOL: 1, I16: 2, U16: 2, F16: 2, BF16: 2, I32: 4, U32: 4, F32: 4, TF32: 4, I64: 8, U64: 8}
+_FMT_NAME = {I8: "I8", I16: "I16", F16: "F16", BF16: "BF16", I32: "I32", F32: "F32", TF32: "TF32", BOOL: "Bool",
+             U8: "U8", U16: "U16", U32: "U32", I64: "I64", U64: "U64"}
+# torch floating dtypes and the one format each may carry; integer dtypes of
+# the right width carry raw storage bits of any format
+_DTYPE_FMT = {"torch.float16": F16, "torch.bfloat16": BF16, "torch.float32": F32}
+
+
+def _arg(what, name, t, fmt, count):
+    """Raise ValueError before any launch unless tensor `t` can hold `count`
+    elements of format `fmt`: the element width must be the format's, a
+    floating dtype must be the format's own, and the tensor must be large
+    enough (the C ABI takes bare pointers and cannot check either)."""
+    if t is None:
+        raise ValueError(f"{what}: {name} is missing")
+    es = _ESIZE.get(fmt)
+    if es is None:
+        return  # an unknown format: the library rejects it before any launch
+    if t.element_size() != es:
+        raise ValueError(f"{what}: {name} has {t.element_size()}-byte elements, {_FMT_NAME[fmt]} needs {es}")
+    dfmt = _DTYPE_FMT.get(str(t.dtype))
+    if dfmt is not None and dfmt != fmt:
+        raise ValueError(f"{what}: {name} is {t.dtype}, the format is {_FMT_NAME[fmt]}")
+    if t.numel() < count:
+        raise ValueError(f"{what}: {name} holds {t.numel()} elements, the shape needs {count}")
+
+
+def _ew_arity(op):
+    """Operand count of a managed elementwise operation (TargetOperation.h:251-256);
+    0 for operations outside the managed domain (the library rejects them)."""
+    if op in (6, 7, 8, 9, 10):  # Max Min Add Sub Mul
+        return 2
+    if op in (0, 1, 2, 3, 4, 5) or 22 <= op <= 31 or op == 34:
+        return 1
+    return 0
 
 
 def _shape(shape):
@@ -237,7 +274,9 @@ class Context:
                                       int(lhs_t), int(rhs_t)))
 
     def gemm_mfma(self, lhs, rhs, dst, m, k, n, in_fmt=BF16, out_fmt=F32, rhs_t=False):
-        _fits("gemm_mfma", (lhs, m * k * 2), (rhs, k * n * 2), (dst, m * n * (4 if out_fmt == F32 else 2)))
+        _arg("gemm_mfma", "lhs", lhs, in_fmt, m * k)
+        _arg("gemm_mfma", "rhs", rhs, in_fmt, k * n)
+        _arg("gemm_mfma", "dst", dst, out_fmt, m * n)
         _check(self._L.wafer_hip_gemm_mfma(self._bind(), _p(lhs), _p(rhs), _p(dst), m, k, n, in_fmt,
                                            out_fmt, int(rhs_t)))
 
@@ -245,7 +284,9 @@ class Context:
         """dst [m, features] = silu_mul(gate, up) of the gate/up products, with
         rhs_gu [2*features, k] in 64-row groups (32 gate rows, then the 32 up
         rows of the same features); see interleave_gate_up."""
-        _fits("gemm_mfma_swiglu", (lhs, m * k * 2), (rhs_gu, 2 * features * k * 2), (dst, m * features * 2))
+        _arg("gemm_mfma_swiglu", "lhs", lhs, in_fmt, m * k)
+        _arg("gemm_mfma_swiglu", "rhs_gu", rhs_gu, in_fmt, 2 * features * k)
+        _arg("gemm_mfma_swiglu", "dst", dst, in_fmt, m * features)
         _check(self._L.wafer_hip_gemm_mfma_swiglu(self._bind(), _p(lhs), _p(rhs_gu), _p(dst), m, k, features,
                                                   in_fmt))
 
@@ -261,29 +302,71 @@ class Context:
                               (features // 32, 1, 1), dst_offset=part * blk)
 
     def gemm_i8(self, a, b, scale, y, m, k, n, acc_out=None, rhs_t=False):
-        _fits("gemm_i8", (a, m * k), (b, k * n), (scale, n * 4), (y, m * n * 2), (acc_out, m * n * 4))
+        _arg("gemm_i8", "a", a, I8, m * k)
+        _arg("gemm_i8", "b", b, I8, k * n)
+        _arg("gemm_i8", "scale", scale, F32, n)
+        _arg("gemm_i8", "y", y, BF16, m * n)
+        if acc_out is not None:
+            _arg("gemm_i8", "acc_out", acc_out, I32, m * n)
         _check(self._L.wafer_hip_gemm_i8(self._bind(), _p(a), _p(b), _p(scale), _p(acc_out), _p(y),
                                          m, k, n, int(rhs_t)))
 
     def elementwise(self, op, fmt, in0, dst, in1=None):
         op = EW[op] if isinstance(op, str) else op
+        n = in0.numel()
+        _arg("elementwise", "in0", in0, fmt, n)
+        _arg("elementwise", "dst", dst, fmt, n)
+        if _ew_arity(op) == 2:
+            _arg("elementwise", "in1", in1, fmt, n)
         _check(self._L.wafer_hip_elementwise(self._bind(), op, fmt, _p(in0), _p(in1), _p(dst),
                                              in0.numel()))
 
     def convert(self, opcode, src, dst, rounding=0):
+        sf, df = ctypes.c_uint32(), ctypes.c_uint32()
+        if load().wafer_hip_convert_route(opcode, ctypes.byref(sf), ctypes.byref(df)) == 0:
+            _arg("convert", "src", src, sf.value, src.numel())
+            _arg("convert", "dst", dst, df.value, src.numel())
         _check(self._L.wafer_hip_convert(self._bind(), opcode, rounding, _p(src), _p(dst), src.numel()))
 
     def reduce(self, op, dim, fmt, shape, src, dst):
         arr, rank = _shape(shape)
+        n = 1
+        for e in shape:
+            n *= int(e)
+        _arg("reduce", "src", src, fmt, n)
+        red = [False] * rank
+        if dim <= 3 and dim < rank:
+            red[rank - 1 - dim] = True
+        elif dim in (4, 5) and rank >= 3:
+            for d in range(rank - 3, rank - (1 if dim == 4 else 0)):
+                red[d] = True
+        out = 1
+        for d, e in enumerate(shape):
+            out *= 1 if red[d] else int(e)
+        _arg("reduce", "dst", dst, fmt, out)
         _check(self._L.wafer_hip_reduce(self._bind(), op, dim, fmt, arr, rank, _p(src), _p(dst)))
 
     def pack(self, fmt, layout, shape, logical, storage):
         arr, rank = _shape(shape)
+        n = 1
+        for e in shape:
+            n *= int(e)
+        _arg("pack", "logical", logical, fmt, n)
+        need = physical_bytes(fmt, layout, shape)
+        if storage.numel() * storage.element_size() < need:
+            raise ValueError(f"pack: storage holds fewer than the {need} bytes of the physical image")
         _check(self._L.wafer_hip_pack(self._bind(), fmt, layout, arr, rank, _p(logical), _p(storage),
                                       storage.numel() * storage.element_size()))
 
     def unpack(self, fmt, layout, shape, storage, logical):
         arr, rank = _shape(shape)
+        n = 1
+        for e in shape:
+            n *= int(e)
+        _arg("unpack", "logical", logical, fmt, n)
+        need = physical_bytes(fmt, layout, shape)
+        if storage.numel() * storage.element_size() < need:
+            raise ValueError(f"unpack: storage holds fewer than the {need} bytes of the physical image")
         _check(self._L.wafer_hip_unpack(self._bind(), fmt, layout, arr, rank, _p(storage),
                                         storage.numel() * storage.element_size(), _p(logical)))
 
@@ -291,33 +374,57 @@ class Context:
     def attention_prefill(self, q, k, v, o, scale, causal=True, fmt=BF16):
         B, Hq, Sq, D = q.shape
         _, Hkv, Skv, _ = k.shape
+        if k.dim() != 4 or tuple(v.shape) != tuple(k.shape) or k.shape[0] != B or k.shape[3] != D:
+            raise ValueError("attention_prefill: k and v must be [batch, kv_heads, kv_len, head_dim] like q")
+        for name, t, n in (("q", q, B * Hq * Sq * D), ("k", k, B * Hkv * Skv * D), ("v", v, B * Hkv * Skv * D),
+                           ("o", o, B * Hq * Sq * D)):
+            _arg("attention_prefill", name, t, fmt, n)
         _check(self._L.wafer_hip_attention_prefill(self._bind(), fmt, _p(q), _p(k), _p(v), _p(o), B, Hq,
                                                    Hkv, Sq, Skv, D, float(scale), int(causal)))
 
     def attention_decode(self, q, k_cache, v_cache, o, scale, chunks=16, kv_len=None, fmt=BF16):
-        B, Hq, _, D = q.shape
+        B, Hq, one, D = q.shape
         _, Hkv, cap, _ = k_cache.shape
         kv_len = cap if kv_len is None else kv_len
+        if one != 1 or tuple(v_cache.shape) != tuple(k_cache.shape) or k_cache.shape[0] != B or \
+                k_cache.shape[3] != D or not 0 <= kv_len <= cap:
+            raise ValueError("attention_decode: q [batch, q_heads, 1, head_dim], caches [batch, kv_heads, cap, "
+                             "head_dim] with kv_len <= cap")
+        for name, t, n in (("q", q, B * Hq * D), ("k_cache", k_cache, B * Hkv * cap * D),
+                           ("v_cache", v_cache, B * Hkv * cap * D), ("o", o, B * Hq * D)):
+            _arg("attention_decode", name, t, fmt, n)
         _check(self._L.wafer_hip_attention_decode(self._bind(), fmt, _p(q), _p(k_cache), _p(v_cache),
                                                   _p(o), B, Hq, Hkv, kv_len, cap, D, float(scale), chunks))
 
     def rmsnorm(self, x, w, y, eps, fmt=BF16):
         cols = x.shape[-1]
+        _arg("rmsnorm", "x", x, fmt, x.numel())
+        _arg("rmsnorm", "w", w, fmt, cols)
+        _arg("rmsnorm", "y", y, fmt, x.numel())
         _check(self._L.wafer_hip_rmsnorm(self._bind(), fmt, _p(x), _p(w), _p(y), x.numel() // cols, cols,
                                          float(eps)))
 
     def softmax(self, x, y, fmt=BF16):
         cols = x.shape[-1]
+        _arg("softmax", "x", x, fmt, x.numel())
+        _arg("softmax", "y", y, fmt, x.numel())
         _check(self._L.wafer_hip_softmax(self._bind(), fmt, _p(x), _p(y), x.numel() // cols, cols))
 
     def silu_mul(self, gate, up, y, fmt=BF16):
+        for name, t in (("gate", gate), ("up", up), ("y", y)):
+            _arg("silu_mul", name, t, fmt, gate.numel())
         _check(self._L.wafer_hip_silu_mul(self._bind(), fmt, _p(gate), _p(up), _p(y), gate.numel()))
 
     def gelu_tanh(self, x, y, fmt=BF16):
+        _arg("gelu_tanh", "x", x, fmt, x.numel())
+        _arg("gelu_tanh", "y", y, fmt, x.numel())
         _check(self._L.wafer_hip_gelu_tanh(self._bind(), fmt, _p(x), _p(y), x.numel()))
 
     def rope(self, x, y, positions, theta, fmt=BF16):
         T, H, D = x.shape
+        _arg("rope", "x", x, fmt, T * H * D)
+        _arg("rope", "y", y, fmt, T * H * D)
+        _arg("rope", "positions", positions, I32, T)
         _check(self._L.wafer_hip_rope(self._bind(), fmt, _p(x), _p(y), T, H, D, _p(positions), float(theta)))
 
     def head_permute_rope(self, src, dst, tokens, heads, head_dim, token_stride, positions, theta, fmt=BF16,
@@ -325,9 +432,10 @@ class Context:
         """dst [heads, tokens, head_dim] = RoPE of the token-major rows of
         `src` (element offset src_offset, row stride token_stride), with
         positions [tokens] (int32, device); equals head_permute + rope."""
-        es = 4 if fmt == F32 else 2
-        if src.element_size() != es or dst.element_size() != es:
-            raise ValueError("head_permute_rope: tensor element size does not match the format")
+        _arg("head_permute_rope", "src", src, fmt, 0)
+        _arg("head_permute_rope", "dst", dst, fmt, 0)
+        _arg("head_permute_rope", "positions", positions, I32, tokens)
+        es = _ESIZE[fmt]
         if src_offset < 0 or src_offset + (tokens - 1) * token_stride + heads * head_dim > src.numel() \
                 or dst.numel() < heads * tokens * head_dim or positions.numel() < tokens:
             raise ValueError("head_permute_rope: the addressed region exceeds a tensor")
@@ -347,8 +455,8 @@ class Context:
         tok_off, hm_off = (src_offset, dst_offset) if direction == 0 else (dst_offset, src_offset)
         if min(tok_off, hm_off) < 0 or tok_off + tok_extent > tok.numel() or hm_off + head_extent > hm.numel():
             raise ValueError("head_permute: the addressed region exceeds a tensor")
-        if src.element_size() != es or dst.element_size() != es:
-            raise ValueError("head_permute: tensor element size does not match the format")
+        _arg("head_permute", "src", src, fmt, 0)
+        _arg("head_permute", "dst", dst, fmt, 0)
         sp = ctypes.c_void_p(_p(src).value + src_offset * es)
         dp = ctypes.c_void_p(_p(dst).value + dst_offset * es)
         _check(self._L.wafer_hip_head_permute(self._bind(), fmt, sp, dp, tokens, heads, head_dim,
@@ -380,11 +488,16 @@ class Context:
         _check(self._L.wafer_hip_memset(self._bind(), _p(dst), fmt, value, count))
 
     def bit2fp(self, bits, dst, fmt, count):
+        if fmt in (F16, BF16, F32):
+            _arg("bit2fp", "dst", dst, fmt, count)
         if (count + 7) // 8 > bits.numel() * bits.element_size() or count > dst.numel():
             raise ValueError("bit2fp: count exceeds a tensor")
         _check(self._L.wafer_hip_bit2fp(self._bind(), _p(bits), _p(dst), fmt, count))
 
     def mask_move(self, src, mask, dst, fmt):
+        if fmt in (F16, BF16, F32):
+            for name, t in (("src", src), ("mask", mask), ("dst", dst)):
+                _arg("mask_move", name, t, fmt, 0)
         if not (src.numel() == mask.numel() == dst.numel()):
             raise ValueError("mask_move: element counts differ")
         _check(self._L.wafer_hip_mask_move(self._bind(), _p(src), _p(mask), _p(dst), fmt, dst.numel()))
@@ -431,4 +544,16 @@ class Context:
 
     def bias_add(self, x, bias, y, fmt=F32):
         cols = x.shape[-1]
+        _arg("bias_add", "x", x, fmt, x.numel())
+        _arg("bias_add", "bias", bias, F32, cols)
+        _arg("bias_add", "y", y, fmt, x.numel())
         _check(self._L.wafer_hip_bias_add(self._bind(), fmt, _p(x), _p(bias), _p(y), x.numel() // cols, cols))
+
+    def first_nan(self, fmt, values, count=None):
+        """Index of the first NaN among the logical F16/BF16/F32 values (count
+        when there is none); synchronous."""
+        count = values.numel() if count is None else count
+        _arg("first_nan", "values", values, fmt, count)
+        out = ctypes.c_uint64()
+        _check(self._L.wafer_hip_first_nan(self._bind(), fmt, _p(values), count, ctypes.byref(out)))
+        return int(out.value)

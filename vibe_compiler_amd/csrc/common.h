@@ -35,6 +35,18 @@ int check_hip(hipError_t err, const char *what);
 int ensure_workspace(wafer_hip_context *ctx, void **slot, size_t *slot_bytes,
                      size_t need);
 int launch_status(const char *kernel);
+// Fails with WAFER_HIP_E_UNSUPPORTED when the context's stream is capturing:
+// for entries that synchronise the stream, read results back to the host or
+// (re)allocate memory, none of which a graph capture can record.
+int refuse_capture(wafer_hip_context *ctx, const char *what);
+// The context's 256-byte device word area (allocated on first use), after
+// refusing a capturing stream.  Layout: bytes [0,4) the convert / MaskMove
+// status word, [64,72) a 64-bit first-index word.
+int status_words(wafer_hip_context *ctx, const char *what, uint8_t **words);
+// Sets n 32-bit words at p to `value` with a one-wave kernel on the context's
+// stream (a memset node recorded into a graph has given wrong results on
+// later replays, so device words are never cleared with hipMemsetAsync).
+int fill_words(wafer_hip_context *ctx, void *p, uint32_t n, uint32_t value);
 
 #define WAFER_CHECK_CTX(ctx)                                                   \
   do {                                                                         \

@@ -663,6 +663,7 @@ double rel_l2_of(const Totals &t) {
 int run_stats(wafer_hip_context *ctx, uint32_t fmt, const void *act, const void *exp, uint64_t n, double atol,
               double rtol, int mode, Totals &t) {
   const bool quantiles = mode == FULL;
+  WAFER_TRY(refuse_capture(ctx, "compare"));  // the statistics are read back to the host
   WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
   const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
   const uint64_t want = (n + (uint64_t)NT * 8 - 1) / ((uint64_t)NT * 8);
@@ -810,10 +811,11 @@ int raw_gate(wafer_hip_context *ctx, const wafer_hip_program_tensor *a, const wa
              Verdict &v) {
   if (a->bytes == 0) return v.set(WAFER_CMP_ACCEPTED, "");
   WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
-  if (!ctx->status) WAFER_TRY(check_hip(hipMalloc((void **)&ctx->status, 256), "hipMalloc(status)"));
-  unsigned long long *first = (unsigned long long *)((uint8_t *)ctx->status + 64);
+  uint8_t *words = nullptr;
+  WAFER_TRY(status_words(ctx, "compare (raw bytes)", &words));
+  unsigned long long *first = (unsigned long long *)(words + 64);
   const unsigned long long none = ~0ull;
-  WAFER_TRY(check_hip(hipMemcpyAsync(first, &none, sizeof none, hipMemcpyHostToDevice, ctx->stream), "hipMemcpyAsync"));
+  WAFER_TRY(fill_words(ctx, first, 2, 0xffffffffu));
   const unsigned grid = (unsigned)std::min<uint64_t>((a->bytes + NT - 1) / NT, 8192);
   hipLaunchKernelGGL(raw_diff_kernel, dim3(grid), dim3(NT), 0, ctx->stream, (const uint8_t *)a->data,
                      (const uint8_t *)e->data, a->bytes, first);

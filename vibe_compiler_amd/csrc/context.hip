@@ -26,12 +26,42 @@ int launch_status(const char *kernel) {
   return check_hip(hipGetLastError(), kernel);
 }
 
+int refuse_capture(wafer_hip_context *ctx, const char *what) {
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  WAFER_TRY(check_hip(hipStreamIsCapturing(ctx->stream, &capture), "hipStreamIsCapturing"));
+  if (capture != hipStreamCaptureStatusNone)
+    return fail(WAFER_HIP_E_UNSUPPORTED,
+                std::string(what) + ": synchronises the stream or allocates, which a stream capture cannot record");
+  return WAFER_HIP_OK;
+}
+
+namespace {
+__global__ void fill_words_kernel(uint32_t *p, uint32_t n, uint32_t value) {
+  for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) p[i] = value;
+}
+}  // namespace
+
+int fill_words(wafer_hip_context *ctx, void *p, uint32_t n, uint32_t value) {
+  hipLaunchKernelGGL(fill_words_kernel, dim3(1), dim3(64), 0, ctx->stream, (uint32_t *)p, n, value);
+  return launch_status("fill_words_kernel");
+}
+
+int status_words(wafer_hip_context *ctx, const char *what, uint8_t **words) {
+  WAFER_TRY(refuse_capture(ctx, what));
+  if (!ctx->status) WAFER_TRY(check_hip(hipMalloc((void **)&ctx->status, 256), "hipMalloc(status)"));
+  *words = (uint8_t *)ctx->status;
+  return WAFER_HIP_OK;
+}
+
 // Grows *slot to at least `need` bytes.  The old contents are discarded; the
 // growth is stream-ordered by synchronising the context's stream first, so
-// in-flight kernels never see the buffer freed under them.
+// in-flight kernels never see the buffer freed under them.  Growing is
+// refused on a capturing stream (a captured graph would keep the old
+// address); a slot that is already large enough is used as it is.
 int ensure_workspace(wafer_hip_context *ctx, void **slot, size_t *slot_bytes,
                      size_t need) {
   if (*slot_bytes >= need) return WAFER_HIP_OK;
+  WAFER_TRY(refuse_capture(ctx, "growing the context workspace"));
   WAFER_TRY(check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize"));
   if (*slot) {
     WAFER_TRY(check_hip(hipFree(*slot), "hipFree(workspace)"));

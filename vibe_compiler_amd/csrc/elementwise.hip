@@ -247,9 +247,71 @@ __global__ __launch_bounds__(256) void reduce_kernel(ReduceGeom g, int op,
 }
 
 }  // namespace
+// Index of the first NaN among n logical values (atomic minimum over the
+// grid; *first stays all-ones when there is none).  16-bit formats load 8
+// values per 16-byte access when the base is aligned.
+template <uint32_t F>
+__global__ __launch_bounds__(256) void first_nan_kernel(const void *__restrict__ v, uint64_t n, bool vec,
+                                                        unsigned long long *first) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  const uint64_t t0 = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  unsigned long long mine = ~0ull;
+  if (vec) {
+    for (uint64_t g = t0; g * 8 < n && mine == ~0ull; g += stride) {
+      float x[8];
+      if (g * 8 + 8 <= n) {
+        load8<F>(v, (int64_t)(g * 8), x);
+      } else {
+        for (int e = 0; e < 8; ++e) x[e] = g * 8 + e < n ? load_as_f32<F>(v, (int64_t)(g * 8 + e)) : 0.0f;
+      }
+      for (int e = 0; e < 8; ++e)
+        if (x[e] != x[e]) { mine = g * 8 + e; break; }
+    }
+  } else {
+    for (uint64_t i = t0; i < n; i += stride) {
+      const float x = load_as_f32<F>(v, (int64_t)i);
+      if (x != x) { mine = i; break; }
+    }
+  }
+  if (mine != ~0ull) atomicMin(first, mine);
+}
+
 }  // namespace wafer
 
 using namespace wafer;
+
+extern "C" int wafer_hip_first_nan(wafer_hip_context *ctx, uint32_t format, const void *values, uint64_t count,
+                                   uint64_t *first) {
+  WAFER_CHECK_CTX(ctx);
+  if (!first) return fail(WAFER_HIP_E_INVALID_FIELD, "first_nan: null output pointer");
+  *first = count;
+  if (!is_float_format(format)) return fail(WAFER_HIP_E_UNSUPPORTED, "first_nan: format must be F16, BF16 or F32");
+  if (count == 0) return WAFER_HIP_OK;
+  if (!values) return fail(WAFER_HIP_E_INVALID_FIELD, "first_nan: null tensor");
+  WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
+  uint8_t *words = nullptr;
+  WAFER_TRY(status_words(ctx, "first_nan", &words));
+  unsigned long long *slot = (unsigned long long *)(words + 64);
+  WAFER_TRY(fill_words(ctx, slot, 2, 0xffffffffu));
+  const bool vec = aligned16(values);
+  const uint64_t work = vec ? (count + 7) / 8 : count;
+  const unsigned blocks = (unsigned)std::min<uint64_t>((work + 255) / 256, 8192);
+  if (format == WAFER_FMT_F32)
+    hipLaunchKernelGGL(first_nan_kernel<WAFER_FMT_F32>, dim3(blocks), dim3(256), 0, ctx->stream, values, count, vec,
+                       slot);
+  else if (format == WAFER_FMT_BF16)
+    hipLaunchKernelGGL(first_nan_kernel<WAFER_FMT_BF16>, dim3(blocks), dim3(256), 0, ctx->stream, values, count,
+                       vec, slot);
+  else
+    hipLaunchKernelGGL(first_nan_kernel<WAFER_FMT_F16>, dim3(blocks), dim3(256), 0, ctx->stream, values, count, vec,
+                       slot);
+  WAFER_TRY(launch_status("first_nan_kernel"));
+  unsigned long long host = ~0ull;
+  WAFER_TRY(check_hip(hipMemcpyAsync(&host, slot, sizeof host, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpyAsync"));
+  WAFER_TRY(check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize"));
+  *first = host == ~0ull ? count : (uint64_t)host;
+  return WAFER_HIP_OK;
+}
 
 extern "C" int wafer_hip_elementwise(wafer_hip_context *ctx, uint32_t op, uint32_t format,
                                      const void *in0, const void *in1, void *dst, uint64_t count) {
@@ -303,10 +365,11 @@ extern "C" int wafer_hip_convert(wafer_hip_context *ctx, uint32_t opcode, uint32
   WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
   const bool checks = !is_float_format(route->dst);
   int *status = nullptr;
-  if (checks) {
-    if (!ctx->status) WAFER_TRY(check_hip(hipMalloc((void **)&ctx->status, 256), "hipMalloc(status)"));
-    status = ctx->status;
-    WAFER_TRY(check_hip(hipMemsetAsync(status, 0, sizeof(int), ctx->stream), "hipMemsetAsync"));
+  if (checks) {  // integer routes report range errors through a status word
+    uint8_t *words = nullptr;
+    WAFER_TRY(status_words(ctx, "convert to an integer format", &words));
+    status = (int *)words;
+    WAFER_TRY(fill_words(ctx, status, 1, 0));
   }
   const unsigned blocks = (unsigned)std::min<uint64_t>((count + 255) / 256, 65536);
   hipLaunchKernelGGL(convert_kernel, dim3(blocks), dim3(256), 0, ctx->stream, route->src, route->dst,

@@ -434,8 +434,9 @@ extern "C" int wafer_hip_mask_move(wafer_hip_context *ctx, const void *src, cons
   if (!is_float_format(format)) return fail(WAFER_HIP_E_UNSUPPORTED, "MaskMove requires F16, BF16 or F32");
   if (!src || !mask || !dst) return fail(WAFER_HIP_E_INVALID_FIELD, "mask_move: null tensor");
   WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
-  if (!ctx->status) WAFER_TRY(check_hip(hipMalloc((void **)&ctx->status, 256), "hipMalloc(status)"));
-  WAFER_TRY(check_hip(hipMemsetAsync(ctx->status, 0, sizeof(int), ctx->stream), "hipMemsetAsync"));
+  uint8_t *words = nullptr;
+  WAFER_TRY(status_words(ctx, "mask_move", &words));  // the mask check reads back a status word
+  WAFER_TRY(fill_words(ctx, words, 1, 0));
   const uint32_t one = one_bits(format);
   const unsigned g = grid_of(element_count);
   // pass 1: every mask value canonical zero or one, else the command fails

@@ -563,8 +563,10 @@ Expected<TargetModelGemmRequest> materializeHipQualificationCase(const HipTarget
   if (!b) return b.error();
   auto bytes = dst->getStorageBytes();
   if (!bytes) return bytes.error();
+  auto axes = getCanonicalFormalGemmGeometry(lhs->getShape().size());
+  if (!axes) return axes.error();
   return TargetModelGemmRequest{
-      FormalGemmOperation{*lhs, *rhs, *dst, spec.m, spec.k, spec.n, spec.batch, TargetGemmOrientation::Normal,
+      FormalGemmOperation{*lhs, *rhs, *dst, spec.m, spec.k, spec.n, spec.batch, *axes, TargetGemmOrientation::Normal,
                           spec.rhsOrientation, std::nullopt},
       TargetModelNumericOperands{{{*lhs, std::move(*a)}, {*rhs, std::move(*b)}},
                                  {*dst, std::vector<uint8_t>(*bytes, 0xA5)}}};

@@ -7,8 +7,12 @@
 //   TargetModelNumericTensor / Operands / *Request / *Result / *Evidence
 //     include/Wafer/Simulator/Kernel/TargetModelKernel.h:108-200
 //   TargetModelKernelErrorCode                      TargetModelKernel.h:21-32
-//   FormalGemmOperation, FormalElementwiseOperation, FormalConvertOperation,
+//   FormalGemmOperation (with FormalGemmGeometry axes), FormalElementwiseOperation,
+//   FormalConvertOperation (with its optional TargetConvertParameter),
 //   FormalReduceOperation      include/Wafer/Simulator/Reference/FormalOperations.h:21-113
+//   TargetConvertParameter, TargetRoundingMode
+//                              include/Wafer/Target/TargetOperation.h:31-56, 175-181
+//   FormalNumericExceptionFlags include/Wafer/Simulator/Reference/FormalNumeric.h:21-42
 //   PhysicalTensorDescriptor   include/Wafer/Target/PhysicalTensor/PhysicalTensorDescriptor.h:20-55
 //   FormalNumericWorkBudget    include/Wafer/Simulator/Reference/FormalTensorNumeric.h:22-47
 // llvm::Expected<T> becomes Expected<T> below (a value or a typed error with
@@ -48,6 +52,53 @@ enum class TargetElementwiseOperation : uint8_t {
 enum class TargetReduceOperation : uint8_t { Sum, Max, Min, Avg };
 enum class TargetReduceDimension : uint8_t {
   Trailing0 = 0, Trailing1 = 1, Trailing2 = 2, Trailing3 = 3, Trailing2And1 = 4, Trailing2And1And0 = 5,
+};
+// TargetOperation.h:175-181
+enum class TargetRoundingMode : uint8_t { NearestEven, TowardZero, TowardPositive, TowardNegative, Stochastic };
+
+// A convert command's parameter: a rounding mode or a zero point (TargetOperation.h:31-56).
+class TargetConvertParameter {
+public:
+  enum class Kind : uint8_t { RoundingMode, ZeroPoint };
+  TargetConvertParameter() = delete;
+  static constexpr TargetConvertParameter roundingMode(TargetRoundingMode mode) {
+    return TargetConvertParameter(Kind::RoundingMode, (uint32_t)mode);
+  }
+  static constexpr TargetConvertParameter zeroPoint(uint32_t value) {
+    return TargetConvertParameter(Kind::ZeroPoint, value);
+  }
+  Kind getKind() const { return kind; }
+  std::optional<TargetRoundingMode> getRoundingMode() const {
+    if (kind != Kind::RoundingMode) return std::nullopt;
+    return (TargetRoundingMode)payload;
+  }
+  std::optional<uint32_t> getZeroPoint() const {
+    if (kind != Kind::ZeroPoint) return std::nullopt;
+    return payload;
+  }
+  friend constexpr bool operator==(TargetConvertParameter a, TargetConvertParameter b) {
+    return a.kind == b.kind && a.payload == b.payload;
+  }
+
+private:
+  constexpr TargetConvertParameter(Kind k, uint32_t p) : kind(k), payload(p) {}
+  Kind kind;
+  uint32_t payload;
+};
+
+// Model-only IEEE exception observations of one operation (FormalNumeric.h:21-42).
+// The managed and oneDNN-seam lanes return them empty, and so does this backend.
+struct FormalNumericExceptionFlags {
+  bool invalid = false;
+  bool divByZero = false;
+  bool overflow = false;
+  bool underflow = false;
+  bool inexact = false;
+  constexpr bool any() const { return invalid || divByZero || overflow || underflow || inexact; }
+  friend constexpr bool operator==(FormalNumericExceptionFlags a, FormalNumericExceptionFlags b) {
+    return a.invalid == b.invalid && a.divByZero == b.divByZero && a.overflow == b.overflow &&
+           a.underflow == b.underflow && a.inexact == b.inexact;
+  }
 };
 
 // ---- errors --------------------------------------------------------------
@@ -138,9 +189,35 @@ struct TargetModelNumericOperands {
 };
 
 // ---- operations and requests ------------------------------------------------
+// The GEMM's dimension mapping (FormalOperations.h:47-74).  The formal
+// operation factory admits only the canonical one: leading batch axes, then
+// M and K of lhs, K and N of rhs, M and N of the destination.
+struct FormalGemmGeometry {
+  std::vector<uint64_t> lhsBatchDimensions;
+  uint64_t lhsMDimension = 0;
+  uint64_t lhsContractingDimension = 0;
+  std::vector<uint64_t> rhsBatchDimensions;
+  uint64_t rhsContractingDimension = 0;
+  uint64_t rhsNDimension = 0;
+  std::vector<uint64_t> destinationBatchDimensions;
+  uint64_t destinationMDimension = 0;
+  uint64_t destinationNDimension = 0;
+  friend bool operator==(const FormalGemmGeometry &a, const FormalGemmGeometry &b) {
+    return a.lhsBatchDimensions == b.lhsBatchDimensions && a.lhsMDimension == b.lhsMDimension &&
+           a.lhsContractingDimension == b.lhsContractingDimension && a.rhsBatchDimensions == b.rhsBatchDimensions &&
+           a.rhsContractingDimension == b.rhsContractingDimension && a.rhsNDimension == b.rhsNDimension &&
+           a.destinationBatchDimensions == b.destinationBatchDimensions &&
+           a.destinationMDimension == b.destinationMDimension && a.destinationNDimension == b.destinationNDimension;
+  }
+};
+// The canonical mapping for tensors of `rank` (>= 2) dimensions
+// (getCanonicalFormalGemmGeometry, lib/Wafer/Simulator/Reference/Formal/FormalOperations.cpp:70-88).
+Expected<FormalGemmGeometry> getCanonicalFormalGemmGeometry(uint64_t rank);
+
 struct FormalGemmOperation {
   PhysicalTensorDescriptor lhs, rhs, destination;
   uint16_t m, k, n, batchCount;
+  FormalGemmGeometry axes;
   TargetGemmOrientation lhsOrientation = TargetGemmOrientation::Normal;
   TargetGemmOrientation rhsOrientation = TargetGemmOrientation::Normal;
   std::optional<PhysicalTensorDescriptor> psum;
@@ -153,6 +230,7 @@ struct FormalElementwiseOperation {
 struct FormalConvertOperation {
   uint16_t opcode;  // a route of the Data_Format route table (TargetFormat.cpp:164-196)
   PhysicalTensorDescriptor source, destination;
+  std::optional<TargetConvertParameter> parameter;
 };
 struct FormalReduceOperation {
   TargetReduceOperation operation;
@@ -178,6 +256,7 @@ struct TargetModelOneDNNDispatchEvidence {
 };
 struct TargetModelOneDNNResult {
   TargetModelNumericTensor destination;
+  FormalNumericExceptionFlags flags;
   TargetModelOneDNNDispatchEvidence evidence;
 };
 struct TargetModelManagedReferenceEvidence {
@@ -187,6 +266,7 @@ struct TargetModelManagedReferenceEvidence {
 };
 struct TargetModelManagedReferenceResult {
   TargetModelNumericTensor destination;
+  FormalNumericExceptionFlags flags;
   TargetModelManagedReferenceEvidence evidence;
 };
 
@@ -220,6 +300,12 @@ public:
   // GEMM on the formal-order kernel: bit-identical to the formal lane, so a
   // request is always handled (never the empty optional) unless it is
   // outside the formal operation's own domain, which is reported as an error.
+  // The three managed-reference commands keep the managed lane's domain
+  // (ManagedReferenceTargetModel.cpp:137-458): F16/BF16/F32 values, no NaN
+  // input or result, NearestEven converts between those formats with one
+  // shape and layout, F32 sums and F16/BF16/F32 extrema; a request outside it
+  // fails with ManagedReferenceBackendFailure and the reference's message.
+  // Flags are returned empty, as the managed lane returns them.
   Expected<std::optional<TargetModelOneDNNResult>> tryExecute(const TargetModelGemmRequest &request) const override;
   Expected<TargetModelManagedReferenceResult> execute(const TargetModelConvertRequest &request,
                                                       FormalNumericWorkBudget scalarBudget) const override;
