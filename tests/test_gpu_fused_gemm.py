@@ -78,5 +78,6 @@ def test_fused_entries_reject_unsupported(hip, torch):
     t = torch.zeros(64 * 64, dtype=torch.bfloat16, device="cuda")
     with pytest.raises(B.WaferHipError):
         hip.gemm_mfma_swiglu(t, t, t, 8, 64, 16)  # features not a multiple of 32
+    r = t.view(torch.int16)  # raw 16-bit storage, so the library (not the wrapper) sees F16
     with pytest.raises(B.WaferHipError):
-        hip.gemm_mfma_swiglu(t, t, t, 8, 64, 32, in_fmt=B.F16)  # bf16 only
+        hip.gemm_mfma_swiglu(r, r, r, 8, 64, 32, in_fmt=B.F16)  # bf16 only

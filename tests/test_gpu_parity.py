@@ -736,11 +736,12 @@ def test_invalid_arguments_fail_without_launch(hip, B):
     with pytest.raises(ValueError):  # operands smaller than the shape: caught before the C call
         hip.gemm_i8(t, t, t, t, 100, 64, 128)
     big = torch.zeros(4096, dtype=torch.int16, device="cuda")
+    i8, f32 = torch.zeros(4096, dtype=torch.int8, device="cuda"), torch.zeros(64, dtype=torch.float32, device="cuda")
     with pytest.raises(B.WaferHipError) as e:
-        hip.gemm_i8(big, big, big, big, 1, 100, 1)
+        hip.gemm_i8(i8, i8, f32, big, 1, 100, 1)
     assert e.value.status == -3  # k not a multiple of one 64-byte stage
     with pytest.raises(B.WaferHipError) as e:
-        hip.gemm_mfma(big, big, big, 1, 40, 1)
+        hip.gemm_mfma(big, big, big, 1, 40, 1, out_fmt=B.BF16)
     assert e.value.status == -3
 
 

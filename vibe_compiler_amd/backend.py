@@ -188,12 +188,17 @@ def _arg(what, name, t, fmt, count):
     """Raise ValueError before any launch unless tensor `t` can hold `count`
     elements of format `fmt`: the element width must be the format's, a
     floating dtype must be the format's own, and the tensor must be large
-    enough (the C ABI takes bare pointers and cannot check either)."""
+    enough (the C ABI takes bare pointers and cannot check either).  A uint8
+    tensor is raw storage: only its byte size is checked."""
     if t is None:
         raise ValueError(f"{what}: {name} is missing")
     es = _ESIZE.get(fmt)
     if es is None:
         return  # an unknown format: the library rejects it before any launch
+    if str(t.dtype) == "torch.uint8":  # a byte tensor carries raw storage of any format
+        if t.numel() < count * es:
+            raise ValueError(f"{what}: {name} holds {t.numel()} bytes, the shape needs {count * es}")
+        return
     if t.element_size() != es:
         raise ValueError(f"{what}: {name} has {t.element_size()}-byte elements, {_FMT_NAME[fmt]} needs {es}")
     dfmt = _DTYPE_FMT.get(str(t.dtype))
