@@ -247,6 +247,26 @@ int wafer_hip_attention_decode(wafer_hip_context *ctx, uint32_t format,
                                uint32_t head_dim, float scale,
                                uint32_t chunks);
 
+/* FD decode without allocation: the same arguments, validation, kernels and
+ * results as wafer_hip_attention_decode (bit for bit), for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  This entry has no counterpart in
+ * the reference.  The chunk-grid path keeps its chunk states in the library's
+ * static device scratch instead of the context workspace: at most 8192
+ * states (batch * q_heads * chunks), 4.125 MiB held on each GPU the library
+ * runs on until the process ends; a request beyond that fails with
+ * WAFER_HIP_E_UNSUPPORTED before any launch.  It calls no hipMalloc / hipFree.
+ * All calls on one GPU share that scratch (it keeps the last call's
+ * contents; every state is written before it is read), so calls that overlap
+ * on one GPU -- on different streams or from different threads -- race. */
+int wafer_hip_attention_decode_noalloc(wafer_hip_context *ctx, uint32_t format,
+                                       const void *q, const void *k_cache,
+                                       const void *v_cache, void *o,
+                                       uint32_t batch, uint32_t q_heads,
+                                       uint32_t kv_heads, uint32_t kv_len,
+                                       uint32_t kv_capacity, uint32_t head_dim,
+                                       float scale, uint32_t chunks);
+
 /* ---- region entries: fused TileRegions ----------------------------------------
  * Compositions of the managed elementwise / reduce commands with the op
  * mapping of getInstrElementwiseKindAttr

@@ -47,7 +47,7 @@ EXPORTS = (
     "wafer_hip_buffer_free", "wafer_hip_copy_to_device", "wafer_hip_copy_to_host", "wafer_hip_convert_route",
     "wafer_hip_strided_copy", "wafer_hip_memset", "wafer_hip_bit2fp", "wafer_hip_mask_move",
     "wafer_hip_compare_expected", "wafer_hip_compare_statistics", "wafer_hip_environment",
-    "wafer_hip_first_nan",
+    "wafer_hip_first_nan", "wafer_hip_attention_decode_noalloc",
 )
 
 # ProgramElementType codes (the comparator's dtypes) and verdicts
@@ -123,6 +123,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wafer_hip_unpack.argtypes = [vp, u32, u32, vp, u32, vp, i64, vp]
     L.wafer_hip_attention_prefill.argtypes = [vp, u32, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32, u32]
     L.wafer_hip_attention_decode.argtypes = [vp, u32, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32, u32]
+    L.wafer_hip_attention_decode_noalloc.argtypes = [vp, u32, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32, u32]
     L.wafer_hip_rmsnorm.argtypes = [vp, u32, vp, vp, vp, u64, u64, f32]
     L.wafer_hip_softmax.argtypes = [vp, u32, vp, vp, u64, u64]
     L.wafer_hip_silu_mul.argtypes = [vp, u32, vp, vp, vp, u64]
@@ -400,6 +401,22 @@ class Context:
             _arg("attention_decode", name, t, fmt, n)
         _check(self._L.wafer_hip_attention_decode(self._bind(), fmt, _p(q), _p(k_cache), _p(v_cache),
                                                   _p(o), B, Hq, Hkv, kv_len, cap, D, float(scale), chunks))
+
+    def attention_decode_noalloc(self, q, k_cache, v_cache, o, scale, chunks=16, kv_len=None, fmt=BF16):
+        """attention_decode with the library's static scratch for chunk
+        states instead of the context workspace (no device allocation)."""
+        B, Hq, one, D = q.shape
+        _, Hkv, cap, _ = k_cache.shape
+        kv_len = cap if kv_len is None else kv_len
+        if one != 1 or tuple(v_cache.shape) != tuple(k_cache.shape) or k_cache.shape[0] != B or \
+                k_cache.shape[3] != D or not 0 <= kv_len <= cap:
+            raise ValueError("attention_decode_noalloc: q [batch, q_heads, 1, head_dim], caches [batch, kv_heads, "
+                             "cap, head_dim] with kv_len <= cap")
+        for name, t, n in (("q", q, B * Hq * D), ("k_cache", k_cache, B * Hkv * cap * D),
+                           ("v_cache", v_cache, B * Hkv * cap * D), ("o", o, B * Hq * D)):
+            _arg("attention_decode_noalloc", name, t, fmt, n)
+        _check(self._L.wafer_hip_attention_decode_noalloc(self._bind(), fmt, _p(q), _p(k_cache), _p(v_cache), _p(o),
+                                                          B, Hq, Hkv, kv_len, cap, D, float(scale), chunks))
 
     def rmsnorm(self, x, w, y, eps, fmt=BF16):
         cols = x.shape[-1]

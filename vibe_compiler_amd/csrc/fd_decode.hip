@@ -33,6 +33,8 @@
 // ExpLp becomes one exp2 of an fma; see fa_prefill.hip for the rounding note.
 #include "common.h"
 
+#include <mutex>
+
 namespace wafer {
 namespace {
 
@@ -308,17 +310,36 @@ __global__ __launch_bounds__(128) void fd_fold_bf16_d128(const ChunkState *__res
   O[(size_t)bh * D + d] = f32_to_bf16(a * coef);
 }
 
-}  // namespace
-}  // namespace wafer
+// ---- the no-allocation variant's scratch -------------------------------------
+// File-scope device array for the chunk states of the chunk-grid path, for
+// callers that cannot allocate.  Each GPU holds its own copy at its own
+// address, looked up once per device with hipGetSymbolAddress (the array's
+// name is only a host-side stand-in and is never passed to a kernel).
+constexpr size_t SCRATCH_STATES = 8192;  // 8192 x 528 B = 4.125 MiB per GPU
+static __device__ __align__(256) ChunkState scratch[SCRATCH_STATES];
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mutex;
+ChunkState *g_scratch[MAX_DEVICES] = {};
 
-using namespace wafer;
+int scratch_for(int device, ChunkState **out) {
+  if (device < 0 || device >= MAX_DEVICES)
+    return fail(WAFER_HIP_E_UNSUPPORTED, "attention_decode_noalloc: device index above 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch[device]) {
+    void *ptr = nullptr;  // the device is current (set by the caller)
+    WAFER_TRY(check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"));
+    g_scratch[device] = (ChunkState *)ptr;
+  }
+  *out = g_scratch[device];
+  return WAFER_HIP_OK;
+}
 
-extern "C" int wafer_hip_attention_decode(wafer_hip_context *ctx, uint32_t format,
-                                          const void *q, const void *k_cache,
-                                          const void *v_cache, void *o, uint32_t batch,
-                                          uint32_t q_heads, uint32_t kv_heads,
-                                          uint32_t kv_len, uint32_t kv_capacity,
-                                          uint32_t head_dim, float scale, uint32_t chunks) {
+// Shared by both entries: validation, then the group path (no workspace) or
+// the chunk grid plus fold, whose states go to `part` when given, else to
+// the context's workspace (grown on demand).
+int decode(wafer_hip_context *ctx, uint32_t format, const void *q, const void *k_cache, const void *v_cache, void *o,
+           uint32_t batch, uint32_t q_heads, uint32_t kv_heads, uint32_t kv_len, uint32_t kv_capacity,
+           uint32_t head_dim, float scale, uint32_t chunks, bool noalloc) {
   WAFER_CHECK_CTX(ctx);
   if (format != WAFER_FMT_BF16)
     return fail(WAFER_HIP_E_UNSUPPORTED, "attention_decode: only BF16 storage is served");
@@ -341,12 +362,18 @@ extern "C" int wafer_hip_attention_decode(wafer_hip_context *ctx, uint32_t forma
   // (lib/Wafer/IR/LinalgExt/AttentionOps.cpp:439-450); one chunk is the FA
   // state and is served as well.
   const int chunk_len = (int)((kv_len + chunks - 1) / chunks);
+  const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+  const bool group = G <= 4 && chunks <= (uint32_t)WG_WAVES && (uint64_t)batch * kv_heads * 4 >= (uint64_t)cus * 3;
+  const size_t states = (size_t)batch * q_heads * chunks;
+  if (noalloc && !group && states > SCRATCH_STATES)
+    return fail(WAFER_HIP_E_UNSUPPORTED, "attention_decode_noalloc: batch * q_heads * chunks = " +
+                                             std::to_string(states) + " chunk states exceed the scratch maximum of " +
+                                             std::to_string(SCRATCH_STATES));
   WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
   const float c = scale * 0x1.715476p+0f;
-  const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
 
   // (G = 8 needs more than the 128 VGPRs a 16-wave workgroup allows)
-  if (G <= 4 && chunks <= (uint32_t)WG_WAVES && (uint64_t)batch * kv_heads * 4 >= (uint64_t)cus * 3) {
+  if (group) {
     const int sub = WG_WAVES / (int)chunks;
     dim3 grid(kv_heads, batch);
 #define FD_GROUP(GV)                                                                              \
@@ -363,9 +390,13 @@ extern "C" int wafer_hip_attention_decode(wafer_hip_context *ctx, uint32_t forma
     return launch_status("fd_group_bf16_d128");
   }
 
-  const size_t state_bytes = (size_t)batch * q_heads * chunks * sizeof(ChunkState);
-  WAFER_TRY(ensure_workspace(ctx, &ctx->workspace, &ctx->workspace_bytes, state_bytes));
-  auto *part = (ChunkState *)ctx->workspace;
+  ChunkState *part = nullptr;
+  if (noalloc) {
+    WAFER_TRY(scratch_for(ctx->device, &part));
+  } else {
+    WAFER_TRY(ensure_workspace(ctx, &ctx->workspace, &ctx->workspace_bytes, states * sizeof(ChunkState)));
+    part = (ChunkState *)ctx->workspace;
+  }
   dim3 grid(chunks, kv_heads, batch);
 #define FD_CHUNK(GV)                                                                              \
   hipLaunchKernelGGL(fd_chunk_bf16_d128<GV>, grid, dim3(256), 0, ctx->stream, (const uint16_t *)q, \
@@ -382,4 +413,29 @@ extern "C" int wafer_hip_attention_decode(wafer_hip_context *ctx, uint32_t forma
   hipLaunchKernelGGL(fd_fold_bf16_d128, dim3(batch * q_heads), dim3(D), 0, ctx->stream, part,
                      (uint16_t *)o, (int)chunks);
   return launch_status("fd_fold_bf16_d128");
+}
+
+}  // namespace
+}  // namespace wafer
+
+using namespace wafer;
+
+extern "C" int wafer_hip_attention_decode(wafer_hip_context *ctx, uint32_t format,
+                                          const void *q, const void *k_cache,
+                                          const void *v_cache, void *o, uint32_t batch,
+                                          uint32_t q_heads, uint32_t kv_heads,
+                                          uint32_t kv_len, uint32_t kv_capacity,
+                                          uint32_t head_dim, float scale, uint32_t chunks) {
+  return decode(ctx, format, q, k_cache, v_cache, o, batch, q_heads, kv_heads, kv_len, kv_capacity, head_dim, scale,
+                chunks, false);
+}
+
+extern "C" int wafer_hip_attention_decode_noalloc(wafer_hip_context *ctx, uint32_t format,
+                                                  const void *q, const void *k_cache,
+                                                  const void *v_cache, void *o, uint32_t batch,
+                                                  uint32_t q_heads, uint32_t kv_heads,
+                                                  uint32_t kv_len, uint32_t kv_capacity,
+                                                  uint32_t head_dim, float scale, uint32_t chunks) {
+  return decode(ctx, format, q, k_cache, v_cache, o, batch, q_heads, kv_heads, kv_len, kv_capacity, head_dim, scale,
+                chunks, true);
 }
