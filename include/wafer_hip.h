@@ -222,14 +222,58 @@ int wafer_hip_unpack(wafer_hip_context *ctx, uint32_t format, uint32_t layout,
  * q [batch, q_heads, q_len, head_dim], k/v [batch, kv_heads, kv_len, head_dim],
  * o like q; q_heads % kv_heads == 0 (GQA: q head h reads kv head
  * h / (q_heads/kv_heads)).  Causal: query i sees key j iff j <= i (and
- * j < kv_len).  format BF16; head_dim 128; any q_len, kv_len >= 1 (kv_len up
- * to 8388607). */
+ * j < kv_len).  format BF16 or F16 (the compiler's F16/BF16 attention
+ * formation, include/Wafer/IR/LinalgExt/AttentionOps.td:42-46); head_dim 128
+ * or 1..64; any q_len, kv_len >= 1 (kv_len up to 8388607).  BF16 with
+ * head_dim 128 runs the dedicated kernel, every other case the kernels of
+ * wafer_hip_attention_prefill_masked with the causal flag alone. */
 int wafer_hip_attention_prefill(wafer_hip_context *ctx, uint32_t format,
                                 const void *q, const void *k, const void *v,
                                 void *o, uint32_t batch, uint32_t q_heads,
                                 uint32_t kv_heads, uint32_t q_len,
                                 uint32_t kv_len, uint32_t head_dim,
                                 float scale, uint32_t causal);
+
+/* FA prefill with the attention op's optional mask operand, its graph-defined
+ * score region and its position bias (include/Wafer/IR/LinalgExt/AttentionOps.td:42-64;
+ * applyScoreRegion lib/Wafer/Transforms/Linalg/OnlineAttentionDecomposition.cpp:279-426,
+ * causal diagonal and valid-prefix ranges :185-210, zero_fully_masked
+ * finalize lib/Wafer/Transforms/Linalg/OnlineAttentionMaterialization.cpp:229-242).
+ * Per score: t = (q.k) * scale; ROUND_SCALED narrows t to the storage type;
+ * with a bias, t = t + bias[b, h, i, j] and ROUND_BIASED narrows that sum;
+ * t becomes -inf where key j is invisible to query i: j >= kv_len, CAUSAL
+ * and j > i + causal_diagonal (0: top-left aligned as SDPA's is_causal;
+ * kv_len - q_len: lower-right aligned), WINDOW and
+ * j < i + causal_diagonal - window + 1, or a boolean mask that is zero.
+ * A query row with no visible key yields exactly 0.
+ * K/V heads are kv_capacity tokens apart (a cache of which the first kv_len
+ * tokens are valid: the valid-KV-prefix case).  bias / keep element
+ * (b, h, i, j) sits at [b*strides[0] + h*strides[1] + i*strides[2] + j]
+ * (stride 0 broadcasts a dimension; j < kv_len is read).
+ * format BF16 or F16; head_dim 64 or 128 (MFMA kernel) or 1..63 (one thread
+ * per query row).  A NULL mask means no flags and no operands. */
+#define WAFER_HIP_ATT_CAUSAL 1u
+#define WAFER_HIP_ATT_WINDOW 2u
+#define WAFER_HIP_ATT_ROUND_SCALED 4u
+#define WAFER_HIP_ATT_ROUND_BIASED 8u
+typedef struct wafer_hip_attention_mask {
+  uint32_t flags;          /* WAFER_HIP_ATT_* */
+  uint32_t kv_capacity;    /* K/V tokens per (batch, kv head); 0 = kv_len */
+  int64_t causal_diagonal; /* CAUSAL / WINDOW anchor */
+  int64_t window;          /* WINDOW: >= 1 keys ending at the diagonal */
+  const float *bias;       /* additive F32 mask or NULL */
+  int64_t bias_strides[3]; /* batch, head, query strides in elements */
+  const uint8_t *keep;     /* boolean mask (nonzero = visible) or NULL */
+  int64_t keep_strides[3];
+} wafer_hip_attention_mask;
+int wafer_hip_attention_prefill_masked(wafer_hip_context *ctx,
+                                       uint32_t format, const void *q,
+                                       const void *k, const void *v, void *o,
+                                       uint32_t batch, uint32_t q_heads,
+                                       uint32_t kv_heads, uint32_t q_len,
+                                       uint32_t kv_len, uint32_t head_dim,
+                                       float scale,
+                                       const wafer_hip_attention_mask *mask);
 
 /* FD decode: one query token per sequence.  Each of `chunks` KV chunks gets
  * its own online state, then the states are folded left to right

@@ -72,6 +72,11 @@ def _declare(L: ctypes.CDLL) -> None:
     L.oracle_reduce.argtypes = [i32, i32, i32, vp, i32, vp, vp]
     L.oracle_attention_prefill.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, i32, i32, i32]
     L.oracle_attention_decode.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, i32, i32, i32]
+    L.oracle_attention_prefill_ex.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, f32,
+                                              ctypes.c_uint32, i64, i64, vp, i64, i64, i64, vp, i64, i64, i64,
+                                              i32, i32]
+    L.oracle_attention_score.argtypes = [i32, ctypes.c_uint32, f32, f32, ctypes.POINTER(ctypes.c_float)]
+    L.oracle_attention_score.restype = ctypes.c_float
     L.oracle_rmsnorm.argtypes = [i32, vp, vp, vp, i64, i64, f32]
     L.oracle_softmax.argtypes = [i32, vp, vp, i64, i64]
     L.oracle_silu_mul.argtypes = [i32, vp, vp, vp, i64]
@@ -225,6 +230,59 @@ def attention_prefill(q, k, v, scale, causal=True, block_k=64, fmt=BF16, nthread
                                           float(scale), int(causal), block_k, nthreads or threads()),
            "attention_prefill")
     return o
+
+
+ATT_CAUSAL, ATT_WINDOW, ATT_ROUND_SCALED, ATT_ROUND_BIASED = 1, 2, 4, 8
+
+
+def _mask_operand(m, dtype, B, Hq, Sq, kv_len):
+    """A [b, h, q, kv] mask broadcast over size-1 leading dims -> (array, strides)."""
+    if m is None:
+        return None, (0, 0, 0)
+    m = np.ascontiguousarray(m, dtype=dtype)
+    if m.ndim != 4 or m.shape[0] not in (1, B) or m.shape[1] not in (1, Hq) or m.shape[2] not in (1, Sq) \
+            or m.shape[3] < kv_len:
+        raise ValueError(f"mask shape {m.shape} does not broadcast to [{B}, {Hq}, {Sq}, >={kv_len}]")
+    st = [m.strides[i] // m.itemsize if m.shape[i] > 1 else 0 for i in range(3)]
+    return m, tuple(st)
+
+
+def attention_prefill_ex(q, k, v, scale, *, kv_len=None, causal=False, diagonal=0, window=0, bias=None,
+                         keep=None, round_scaled=False, round_biased=False, block_k=64, fmt=BF16, nthreads=None):
+    """FA prefill with masks: k/v [B, Hkv, capacity, D] of which kv_len tokens are valid; causal: key j
+    visible to query i iff j <= i + diagonal; window > 0: and j > i + diagonal - window; bias: additive
+    f32 [b|1, h|1, q|1, >=kv_len]; keep: boolean mask of the same form (nonzero = visible)."""
+    B, Hq, Sq, D = q.shape
+    _, Hkv, cap, _ = k.shape
+    kv_len = cap if kv_len is None else kv_len
+    q, k, v = (np.ascontiguousarray(t, dtype=np.uint16) for t in (q, k, v))
+    bias, bst = _mask_operand(bias, np.float32, B, Hq, Sq, kv_len)
+    keep, kst = _mask_operand(keep, np.uint8, B, Hq, Sq, kv_len)
+    flags = (ATT_CAUSAL if causal else 0) | (ATT_WINDOW if window > 0 else 0) | \
+        (ATT_ROUND_SCALED if round_scaled else 0) | (ATT_ROUND_BIASED if round_biased else 0)
+    o = np.zeros((B, Hq, Sq, D), dtype=np.uint16)
+    _check(lib().oracle_attention_prefill_ex(fmt, _p(q), _p(k), _p(v), _p(o), B, Hq, Hkv, Sq, kv_len, cap, D,
+                                             float(scale), flags, int(diagonal), int(window),
+                                             _p(bias) if bias is not None else None, *bst,
+                                             _p(keep) if keep is not None else None, *kst,
+                                             block_k, nthreads or threads()),
+           "attention_prefill_ex")
+    return o
+
+
+def attention_score(raw, scale, bias=None, round_scaled=False, round_biased=False, fmt=F16):
+    """The score region element by element (oracle_attention_score), as float32."""
+    raw = np.asarray(raw, dtype=np.float32).ravel()
+    flags = (ATT_ROUND_SCALED if round_scaled else 0) | (ATT_ROUND_BIASED if round_biased else 0)
+    out = np.empty_like(raw)
+    b = None if bias is None else np.asarray(bias, dtype=np.float32).ravel()
+    cell = ctypes.c_float()
+    for i in range(raw.size):
+        if b is not None:
+            cell.value = float(b[i])
+        out[i] = lib().oracle_attention_score(fmt, flags, float(raw[i]), float(scale),
+                                              ctypes.byref(cell) if b is not None else None)
+    return out
 
 
 def attention_decode(q, k, v, scale, chunks=16, kv_len=None, block_k=64, fmt=BF16, nthreads=None):

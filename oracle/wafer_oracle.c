@@ -668,10 +668,53 @@ static inline float maximumf(float a, float b) {
   return a > b ? a : (b > a ? b : (signbit(a) ? b : a));
 }
 
+/* Score masking of one query row: the score region and the position bias of
+ * applyScoreRegion (lib/Wafer/Transforms/Linalg/OnlineAttentionDecomposition.cpp:279-426).
+ * Key j is visible iff lo <= j <= hi and keep[j] != 0 (when a boolean mask is
+ * given); an invisible key's score gets + (-inf), as the 0/-inf position
+ * bias template of :316-330 does (its `visible` = min(diagonal + q + 1,
+ * valid) is hi + 1 here, valid = kv_len). */
+typedef struct {
+  int format;
+  uint32_t flags;
+  const float *bias;    /* this row of the additive F32 mask, or NULL */
+  const uint8_t *keep;  /* this row of the boolean mask, or NULL */
+  int64_t lo, hi;       /* visible key positions */
+} att_row;
+
+#define ATT_CAUSAL 1u
+#define ATT_WINDOW 2u
+#define ATT_ROUND_SCALED 4u
+#define ATT_ROUND_BIASED 8u
+
+static inline float round_storage(int format, float x) {
+  if (format == F_BF16) return oracle_bf16_to_f32(oracle_f32_to_bf16(x));
+  uint16_t h;
+  if (oracle_f32_to_f16(x, &h) != 0) return x; /* NaN stays NaN */
+  return oracle_f16_to_f32(h);
+}
+
+/* The score region of one element: s = raw * scale; ROUND_SCALED narrows it
+ * to the storage type (the exported graph's convert after the scale
+ * multiply, test/Board/Support/wafer_target_model_source_runner.py:85-99);
+ * an additive mask value is then added, and ROUND_BIASED narrows that sum
+ * (the storage-typed mask add of the same program). */
+float oracle_attention_score(int format, uint32_t flags, float raw,
+                             float scale, const float *bias) {
+  float s = raw * scale;
+  if (flags & ATT_ROUND_SCALED) s = round_storage(format, s);
+  if (bias) {
+    s = s + *bias;
+    if (flags & ATT_ROUND_BIASED) s = round_storage(format, s);
+  }
+  return s;
+}
+
 /* decomposeOne for one KV block [j0, j1) and one query row
  * (lib/Wafer/Transforms/Linalg/OnlineAttentionDecomposition.cpp:568-597):
  *   S = sum_d f32(q)*f32(k) (createQK :242-277, a GEMM: fma chain from +0),
- *   S = S*scale (+ 0/-inf causal bias, applyScoreRegion :279-426),
+ *   S = score region (scale, optional rounding and additive mask) + 0/-inf
+ *       position bias (applyScoreRegion :279-426; att_row above),
  *   m' = max(m, rowmax S); e = (m' == -inf ? 0 : m') (AttentionMath.cpp:21-48),
  *   alpha = ExpLp(m - e); P = ExpLp(S - e)   (Exp -> ExpLp, ComputeLowering.cpp:2585),
  *   l = l*alpha, then l += P left to right (createReduction with init),
@@ -681,15 +724,17 @@ static inline float maximumf(float a, float b) {
 static void att_block(att_state *st, int format, const uint16_t *qrow,
                       const uint16_t *kbase, const uint16_t *vbase,
                       int64_t kv_stride, int j0, int j1, int head_dim,
-                      float scale, int causal_limit, float *s, float *pv) {
+                      float scale, const att_row *row, float *s, float *pv) {
   float rowmax = -INFINITY;
   for (int j = j0; j < j1; ++j) {
     const uint16_t *krow = kbase + (int64_t)j * kv_stride;
     float dot = 0.0f;
     for (int d = 0; d < head_dim; ++d)
       dot = fmaf(load_float(format, qrow, d), load_float(format, krow, d), dot);
-    float sc = dot * scale;
-    if (causal_limit >= 0 && j > causal_limit) sc = sc + (-INFINITY);
+    float sc = oracle_attention_score(format, row->flags, dot, scale,
+                                      row->bias ? row->bias + j : NULL);
+    if (j < row->lo || j > row->hi || (row->keep && !row->keep[j]))
+      sc = sc + (-INFINITY);
     s[j - j0] = sc;
     rowmax = maximumf(rowmax, sc);
   }
@@ -744,7 +789,13 @@ typedef struct {
   uint16_t *o;
   int batch, q_heads, kv_heads, q_len, kv_len, kv_capacity, head_dim;
   float scale;
-  int causal, block_k, chunks;
+  int block_k, chunks;
+  uint32_t flags;
+  int64_t diagonal, window;
+  const float *bias;
+  int64_t bias_sb, bias_sh, bias_sq;
+  const uint8_t *keep;
+  int64_t keep_sb, keep_sh, keep_sq;
 } att_job;
 
 static void prefill_range(void *p, int64_t begin, int64_t end) {
@@ -760,22 +811,57 @@ static void prefill_range(void *p, int64_t begin, int64_t end) {
     int b = (int)(row / ((int64_t)j->q_len * j->q_heads));
     int kvh = h / group;
     const uint16_t *qrow = j->q + (((int64_t)b * j->q_heads + h) * j->q_len + i) * D;
-    const uint16_t *kb = j->k + ((int64_t)b * j->kv_heads + kvh) * j->kv_len * D;
-    const uint16_t *vb = j->v + ((int64_t)b * j->kv_heads + kvh) * j->kv_len * D;
+    const uint16_t *kb = j->k + ((int64_t)b * j->kv_heads + kvh) * j->kv_capacity * D;
+    const uint16_t *vb = j->v + ((int64_t)b * j->kv_heads + kvh) * j->kv_capacity * D;
+    att_row mk = {j->format, j->flags, NULL, NULL, 0, (int64_t)j->kv_len - 1};
+    if (j->bias) mk.bias = j->bias + b * j->bias_sb + h * j->bias_sh + i * j->bias_sq;
+    if (j->keep) mk.keep = j->keep + b * j->keep_sb + h * j->keep_sh + i * j->keep_sq;
+    if ((j->flags & ATT_CAUSAL) && i + j->diagonal < mk.hi) mk.hi = i + j->diagonal;
+    if ((j->flags & ATT_WINDOW) && i + j->diagonal - j->window + 1 > mk.lo)
+      mk.lo = i + j->diagonal - j->window + 1;
     att_state st = {-INFINITY, 0.0f, acc};
     for (int d = 0; d < D; ++d) acc[d] = 0.0f;
-    int limit = j->causal ? i : -1;
-    int kv_end = j->kv_len;
-    /* A causal query row never sees keys beyond its own index; blocks that
-     * are fully masked contribute exactly nothing (alpha = 1, P = 0). */
-    if (j->causal && i + 1 < kv_end) kv_end = i + 1;
-    for (int j0 = 0; j0 < kv_end; j0 += j->block_k) {
-      int j1 = j0 + j->block_k < kv_end ? j0 + j->block_k : kv_end;
-      att_block(&st, j->format, qrow, kb, vb, D, j0, j1, D, j->scale, limit, s, pv);
+    /* Key blocks wholly outside [lo, hi] contribute exactly nothing (no
+     * visible score: alpha = 1 and P = 0, or m stays -inf with l = acc = 0),
+     * so only the blocks that meet the visible range are walked. */
+    if (mk.lo <= mk.hi) {
+      int64_t first = mk.lo / j->block_k * j->block_k;
+      for (int64_t j0 = first; j0 <= mk.hi; j0 += j->block_k) {
+        int64_t j1 = j0 + j->block_k <= mk.hi + 1 ? j0 + j->block_k : mk.hi + 1;
+        att_block(&st, j->format, qrow, kb, vb, D, (int)j0, (int)j1, D, j->scale, &mk, s, pv);
+      }
     }
     att_finalize(&st, j->format, j->o + (((int64_t)b * j->q_heads + h) * j->q_len + i) * D, D);
   }
   free(s); free(pv); free(acc);
+}
+
+/* FA prefill with the optional mask operand, score-region rounding and
+ * position bias (flags ATT_*, diagonal, window), K/V heads kv_capacity
+ * tokens apart of which the first kv_len are valid
+ * (OnlineAttentionDecomposition.cpp:185-210: causal diagonal range and valid
+ * prefix).  bias / keep element (b, h, i, j) sits at b*sb + h*sh + i*sq + j. */
+int oracle_attention_prefill_ex(int format, const uint16_t *q,
+                                const uint16_t *k, const uint16_t *v,
+                                uint16_t *o, int batch, int q_heads,
+                                int kv_heads, int q_len, int kv_len,
+                                int kv_capacity, int head_dim, float scale,
+                                uint32_t flags, int64_t diagonal,
+                                int64_t window, const float *bias,
+                                int64_t bias_sb, int64_t bias_sh,
+                                int64_t bias_sq, const uint8_t *keep,
+                                int64_t keep_sb, int64_t keep_sh,
+                                int64_t keep_sq, int block_k, int threads) {
+  if ((format != F_BF16 && format != F_F16) || kv_heads <= 0 ||
+      q_heads % kv_heads != 0 || block_k <= 0 || kv_len > kv_capacity ||
+      ((flags & ATT_WINDOW) && window < 1))
+    return -1;
+  att_job j = {format, q, k, v, o, batch, q_heads, kv_heads, q_len, kv_len,
+               kv_capacity, head_dim, scale, block_k, 1, flags, diagonal,
+               window, bias, bias_sb, bias_sh, bias_sq, keep, keep_sb,
+               keep_sh, keep_sq};
+  parallel_for((int64_t)batch * q_heads * q_len, threads, prefill_range, &j);
+  return 0;
 }
 
 int oracle_attention_prefill(int format, const uint16_t *q, const uint16_t *k,
@@ -783,13 +869,11 @@ int oracle_attention_prefill(int format, const uint16_t *q, const uint16_t *k,
                              int q_heads, int kv_heads, int q_len, int kv_len,
                              int head_dim, float scale, int causal,
                              int block_k, int threads) {
-  if ((format != F_BF16 && format != F_F16) || kv_heads <= 0 ||
-      q_heads % kv_heads != 0 || block_k <= 0)
-    return -1;
-  att_job j = {format, q, k, v, o, batch, q_heads, kv_heads, q_len, kv_len,
-               kv_len, head_dim, scale, causal, block_k, 1};
-  parallel_for((int64_t)batch * q_heads * q_len, threads, prefill_range, &j);
-  return 0;
+  return oracle_attention_prefill_ex(format, q, k, v, o, batch, q_heads,
+                                     kv_heads, q_len, kv_len, kv_len, head_dim,
+                                     scale, causal ? ATT_CAUSAL : 0u, 0, 0,
+                                     NULL, 0, 0, 0, NULL, 0, 0, 0, block_k,
+                                     threads);
 }
 
 /* FD: per-chunk online state over the chunk's keys, then the left fold in
@@ -804,6 +888,7 @@ static void decode_range(void *p, int64_t begin, int64_t end) {
   float *acc2 = (float *)malloc(sizeof(float) * (size_t)D);
   int group = j->q_heads / j->kv_heads;
   int chunk_len = (j->kv_len + j->chunks - 1) / j->chunks;
+  const att_row mk = {j->format, 0u, NULL, NULL, 0, (int64_t)j->kv_len - 1};
   for (int64_t row = begin; row < end; ++row) {
     int h = (int)(row % j->q_heads);
     int b = (int)(row / j->q_heads);
@@ -820,7 +905,7 @@ static void decode_range(void *p, int64_t begin, int64_t end) {
       for (int d = 0; d < D; ++d) acc2[d] = 0.0f;
       for (int j0 = c0; j0 < c1; j0 += j->block_k) {
         int j1 = j0 + j->block_k < c1 ? j0 + j->block_k : c1;
-        att_block(&part, j->format, qrow, kb, vb, D, j0, j1, D, j->scale, -1, s, pv);
+        att_block(&part, j->format, qrow, kb, vb, D, j0, j1, D, j->scale, &mk, s, pv);
       }
       if (c == 0) {
         total.m = part.m;
@@ -846,7 +931,8 @@ int oracle_attention_decode(int format, const uint16_t *q,
       kv_len > kv_capacity)
     return -1;
   att_job j = {format, q, k_cache, v_cache, o, batch, q_heads, kv_heads, 1,
-               kv_len, kv_capacity, head_dim, scale, 0, block_k, chunks};
+               kv_len, kv_capacity, head_dim, scale, block_k, chunks, 0u, 0,
+               0, NULL, 0, 0, 0, NULL, 0, 0, 0};
   parallel_for((int64_t)batch * q_heads, threads, decode_range, &j);
   return 0;
 }

@@ -86,6 +86,22 @@ int oracle_attention_prefill(int format, const uint16_t *q, const uint16_t *k,
                              int q_heads, int kv_heads, int q_len, int kv_len,
                              int head_dim, float scale, int causal,
                              int block_k, int threads);
+/* flags: 1 causal (key j <= i + diagonal), 2 window (key j > i + diagonal -
+ * window), 4 round the scaled score to the storage type, 8 round the score
+ * plus additive mask to the storage type. */
+int oracle_attention_prefill_ex(int format, const uint16_t *q,
+                                const uint16_t *k, const uint16_t *v,
+                                uint16_t *o, int batch, int q_heads,
+                                int kv_heads, int q_len, int kv_len,
+                                int kv_capacity, int head_dim, float scale,
+                                uint32_t flags, int64_t diagonal,
+                                int64_t window, const float *bias,
+                                int64_t bias_sb, int64_t bias_sh,
+                                int64_t bias_sq, const uint8_t *keep,
+                                int64_t keep_sb, int64_t keep_sh,
+                                int64_t keep_sq, int block_k, int threads);
+float oracle_attention_score(int format, uint32_t flags, float raw,
+                             float scale, const float *bias);
 int oracle_attention_decode(int format, const uint16_t *q,
                             const uint16_t *k_cache, const uint16_t *v_cache,
                             uint16_t *o, int batch, int q_heads, int kv_heads,

@@ -1,0 +1,296 @@
+"""GPU parity for the reference's own attention cases
+(test/Board/PyTorch/wafer_pytorch_board_cases.py:937-1130, 1478-1516): FP16
+and BF16 storage, head_dim 64 / 128 and the head_dim-16 probability-rounding
+case, additive F32, boolean padding, fully-masked and sliding-window masks,
+a valid-KV prefix, a lower-right causal decode, GQA, and the score-region
+rounding flags, through wafer_hip_attention_prefill_masked and
+wafer_hip_attention_prefill, against the CPU oracle's masked FA
+(oracle_attention_prefill_ex) on identical inputs.
+
+Tolerance: the reference's attention policy (cosine >= 0.9999, relative L2
+<= 0.01) plus elementwise rtol 0.006 / atol 0.008; fully-masked rows exactly
++0; bit-exact where two calls run the same kernel walk over the same keys.
+"""
+import ctypes
+import math
+import sys
+import zlib
+
+import numpy as np
+import pytest
+
+from tests.similarity import attention_gate
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+F16, BF16 = 2, 3
+
+
+def say(*a):
+    print("[gpu-case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def hip():
+    from vibe_compiler_amd import backend
+
+    ctx = backend.Context(0)
+    yield ctx
+    ctx.close()
+
+
+@pytest.fixture(scope="module")
+def B():
+    from vibe_compiler_amd import backend
+
+    return backend
+
+
+def u16(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint16).view(np.int16)).cuda()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def back(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy().view(np.uint16)
+
+
+def store(oracle, fmt, x):
+    x = np.asarray(x, np.float32)
+    if fmt == BF16:
+        return oracle.f32_to_bf16(x).reshape(x.shape)
+    return x.astype(np.float16).view(np.uint16)
+
+
+def inputs(oracle, rng, fmt, Hq, Hkv, Sq, Skv, D, Bn=1):
+    q = store(oracle, fmt, rng.standard_normal((Bn, Hq, Sq, D)) * 0.125)
+    k = store(oracle, fmt, rng.standard_normal((Bn, Hkv, Skv, D)) * 0.125)
+    v = store(oracle, fmt, rng.standard_normal((Bn, Hkv, Skv, D)))
+    return q, k, v
+
+
+def band(Sq, Skv, diag, window=None):
+    i = np.arange(Sq)[:, None]
+    j = np.arange(Skv)[None, :]
+    vis = j <= i + diag
+    if window is not None:
+        vis &= j > i + diag - window
+    return vis
+
+
+def run_masked(hip, fmt, q, k, v, scale, **kw):
+    Bn, Hq, Sq, D = q.shape
+    o = torch.full((Bn, Hq, Sq, D), 0x7E00, dtype=torch.int16, device="cuda")
+    dkw = dict(kw)
+    for name in ("bias", "keep"):
+        if dkw.get(name) is not None:
+            dkw[name] = dev(dkw[name])
+    hip.attention_prefill_masked(u16(q), u16(k), u16(v), o, scale, fmt=fmt, **dkw)
+    return back(o)
+
+
+def tof(oracle, fmt, a):
+    return oracle.to_float(fmt, a).reshape(a.shape)
+
+
+# (name, Hq, Hkv, Sq, Skv, valid, D, mode): the board cases at their own shapes
+CASES = [
+    ("attention-noncausal", 1, 1, 1024, 33, None, 64, "none"),
+    ("attention-noncausal-additive", 1, 1, 1024, 33, None, 64, "additive"),
+    ("attention-padding", 1, 1, 1024, 33, None, 64, "padding"),
+    ("attention-valid-kv-prefix", 1, 1, 1025, 1031, 1024, 64, "causal"),
+    ("attention-sliding-window", 1, 1, 1025, 1031, None, 64, "sliding"),
+    ("attention-sliding-window-flags", 1, 1, 1025, 1031, None, 64, "window"),
+    ("attention-causal-decode-two-tokens", 1, 1, 2, 1026, None, 64, "lower-right"),
+    ("attention-probability-rounding-1024", 2, 2, 1024, 33, None, 16, "none"),
+    ("attention-probability-rounding-1025", 2, 2, 1025, 33, None, 16, "none"),
+    ("attention-probability-rounding-1031", 2, 2, 1031, 33, None, 16, "none"),
+    ("attention-prefill", 1, 1, 1024, 1024, None, 64, "causal"),
+    ("attention-prefill-tail-1025", 1, 1, 1025, 1025, None, 64, "causal"),
+    ("attention-prefill-tail-1031", 1, 1, 1031, 1031, None, 64, "causal"),
+    ("attention-gqa", 32, 8, 1024, 1024, None, 128, "causal"),
+    ("attention-gqa-tail-1025", 32, 8, 1025, 1025, None, 128, "causal"),
+]
+
+
+def case_kwargs(rng, Sq, L, mode):
+    kw = dict(kv_len=L)
+    if mode == "additive":
+        kw["bias"] = (rng.standard_normal((1, 1, Sq, L)) * 0.125).astype(np.float32)
+    elif mode == "padding":
+        keep = np.zeros((1, 1, 1, L), np.uint8)
+        keep[..., :L - 7] = 1
+        kw["keep"] = keep
+    elif mode == "causal":
+        kw.update(causal=True, diagonal=0)
+    elif mode == "lower-right":
+        kw.update(causal=True, diagonal=L - Sq)
+    elif mode == "sliding":
+        kw["keep"] = band(Sq, L, L - Sq, 64)[None, None].astype(np.uint8)
+    elif mode == "window":
+        kw.update(causal=True, diagonal=L - Sq, window=64)
+    return kw
+
+
+@pytest.mark.parametrize("fmt", [F16, BF16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_reference_attention_case(hip, oracle, case, fmt):
+    name, Hq, Hkv, Sq, Skv, valid, D, mode = case
+    say(name, "fmt", fmt)
+    rng = np.random.default_rng(zlib.crc32(name.encode()) + fmt)
+    q, k, v = inputs(oracle, rng, fmt, Hq, Hkv, Sq, Skv, D)
+    L = Skv if valid is None else valid
+    kw = case_kwargs(rng, Sq, L, mode)
+    scale = 1.0 / math.sqrt(D)
+    ref = oracle.attention_prefill_ex(q, k, v, scale, fmt=fmt, **kw)
+    got = run_masked(hip, fmt, q, k, v, scale, **kw)
+    attention_gate(tof(oracle, fmt, got), tof(oracle, fmt, ref), what=f"{name} masked")
+    if mode in ("causal", "none") and valid is None:
+        # the plain entry: BF16 head_dim 128 takes its own kernel, the rest
+        # the masked kernels with the causal flag alone
+        o = torch.full(q.shape, 0x7E00, dtype=torch.int16, device="cuda")
+        hip.attention_prefill(u16(q), u16(k), u16(v), o, scale, causal=mode == "causal", fmt=fmt)
+        attention_gate(tof(oracle, fmt, back(o)), tof(oracle, fmt, ref), what=f"{name} plain")
+
+
+@pytest.mark.parametrize("fmt", [F16, BF16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("D", [128, 64, 16])
+def test_fully_masked_is_exact_zero(hip, oracle, fmt, D):
+    """attention-fully-masked (q 1024, kv 33): every output exactly +0; and a
+    causal diagonal that hides the first rows' keys zeroes exactly those."""
+    say("fully masked", fmt, D)
+    rng = np.random.default_rng(21 + D)
+    q, k, v = inputs(oracle, rng, fmt, 1, 1, 1024, 33, D)
+    got = run_masked(hip, fmt, q, k, v, 0.125, keep=np.zeros((1, 1, 1, 33), np.uint8))
+    assert not got.any()
+    got = run_masked(hip, fmt, q, k, v, 0.125, causal=True, diagonal=-5)
+    assert not got[:, :, :5].any() and got[:, :, 5:].any(axis=-1).all()
+    ref = oracle.attention_prefill_ex(q, k, v, 0.125, causal=True, diagonal=-5, fmt=fmt)
+    attention_gate(tof(oracle, fmt, got), tof(oracle, fmt, ref), what="diagonal -5")
+    got = run_masked(hip, fmt, q, k, v, 0.125, causal=True, diagonal=-(1 << 40))
+    assert not got.any()
+
+
+@pytest.mark.parametrize("D", [128, 64, 32])
+def test_general_operands_and_rounding(hip, oracle, D):
+    """Per-(batch, head, query) additive mask, a per-batch boolean padding mask
+    broadcast over heads and queries, GQA, batch 2, and both score-rounding
+    flags on scores near 512 (an f16 ulp of 0.5: the rounding is visible)."""
+    say("general operands", D)
+    fmt = F16
+    rng = np.random.default_rng(31 + D)
+    Bn, Hq, Hkv, Sq, Skv = 2, 4, 2, 150, 140
+    qi = rng.integers(-1, 2, (Bn, Hq, Sq, D))
+    ki = rng.integers(-1, 2, (Bn, Hkv, Skv, D))
+    qi[..., :8], ki[..., :8] = 8, 8
+    q, k = store(oracle, fmt, qi), store(oracle, fmt, ki)
+    v = store(oracle, fmt, rng.standard_normal((Bn, Hkv, Skv, D)))
+    bias = (rng.standard_normal((Bn, Hq, Sq, Skv)) * 0.3).astype(np.float32)
+    keep = np.ones((Bn, 1, 1, Skv), np.uint8)
+    keep[0, ..., 100:] = 0
+    keep[1, ..., :3] = 0
+    for flags in (dict(), dict(round_scaled=True), dict(round_scaled=True, round_biased=True)):
+        ref = oracle.attention_prefill_ex(q, k, v, 1.0, bias=bias, keep=keep, fmt=fmt, **flags)
+        got = run_masked(hip, fmt, q, k, v, 1.0, bias=bias, keep=keep, **flags)
+        attention_gate(tof(oracle, fmt, got), tof(oracle, fmt, ref), what=f"D{D} {flags}")
+    # causal lower-right with a window and the bias, BF16
+    qb, kb, vb = inputs(oracle, rng, BF16, Hq, Hkv, Sq, Skv, D, Bn=Bn)
+    kw = dict(causal=True, diagonal=Skv - Sq, window=37, bias=bias)
+    ref = oracle.attention_prefill_ex(qb, kb, vb, 0.2, fmt=BF16, **kw)
+    got = run_masked(hip, BF16, qb, kb, vb, 0.2, **kw)
+    attention_gate(tof(oracle, BF16, got), tof(oracle, BF16, ref), what=f"D{D} window")
+
+
+@pytest.mark.parametrize("fmt", [F16, BF16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("D", [128, 64, 16])
+def test_valid_prefix_never_reads_the_tail(hip, oracle, fmt, D):
+    """K/V heads kv_capacity tokens apart with NaN past kv_len: the output is
+    bit-identical to the same call on the contiguous valid prefix."""
+    say("valid prefix", fmt, D)
+    rng = np.random.default_rng(41 + D)
+    Hq, Hkv, Sq, cap, L = 4, 2, 200, 300, 229
+    q, k, v = inputs(oracle, rng, fmt, Hq, Hkv, Sq, cap, D)
+    nan = 0x7E00 if fmt == F16 else 0x7FC0
+    k[:, :, L:] = nan
+    v[:, :, L:] = nan
+    kw = dict(causal=True, diagonal=L - Sq)
+    got = run_masked(hip, fmt, q, k, v, 0.09, kv_len=L, **kw)
+    sliced = run_masked(hip, fmt, q, np.ascontiguousarray(k[:, :, :L]), np.ascontiguousarray(v[:, :, :L]), 0.09, **kw)
+    assert np.array_equal(got, sliced)
+    ref = oracle.attention_prefill_ex(q, k, v, 0.09, kv_len=L, fmt=fmt, **kw)
+    attention_gate(tof(oracle, fmt, got), tof(oracle, fmt, ref), what="valid prefix")
+
+
+@pytest.mark.parametrize("fmt", [F16, BF16], ids=["f16", "bf16"])
+def test_config1_shape_f16_and_masked_bf16(hip, oracle, fmt):
+    """The headline shape [1, 16, 2048, 128] causal through the masked entry
+    (and, for F16, the plain entry, which routes there), against the oracle."""
+    say("config-1 shape masked", fmt)
+    rng = np.random.default_rng(51)
+    q, k, v = inputs(oracle, rng, fmt, 16, 16, 2048, 2048, 128)
+    scale = 1.0 / math.sqrt(128)
+    ref = oracle.attention_prefill_ex(q, k, v, scale, causal=True, fmt=fmt)
+    got = run_masked(hip, fmt, q, k, v, scale, causal=True)
+    attention_gate(tof(oracle, fmt, got), tof(oracle, fmt, ref), what="config-1 masked")
+    if fmt == F16:
+        o = torch.full(q.shape, 0x7E00, dtype=torch.int16, device="cuda")
+        hip.attention_prefill(u16(q), u16(k), u16(v), o, scale, causal=True, fmt=fmt)
+        assert np.array_equal(back(o), got)
+
+
+def test_diagonal_past_the_keys_is_noncausal(hip, oracle):
+    """A causal diagonal at or beyond kv_len hides nothing: bit-identical to
+    the non-causal call (same kernel, same key walk)."""
+    rng = np.random.default_rng(61)
+    for D in (128, 64, 16):
+        q, k, v = inputs(oracle, rng, BF16, 2, 1, 130, 77, D)
+        a = run_masked(hip, BF16, q, k, v, 0.1)
+        b = run_masked(hip, BF16, q, k, v, 0.1, causal=True, diagonal=77)
+        c = run_masked(hip, BF16, q, k, v, 0.1, causal=True, diagonal=1 << 40)
+        assert np.array_equal(a, b) and np.array_equal(a, c), D
+
+
+def test_masked_entry_rejects_bad_arguments(hip, B):
+    t = torch.zeros(64 * 64, dtype=torch.int16, device="cuda").view(1, 1, 64, 64)
+    L = hip._L
+
+    def call(m, D=64, fmt=B.F16):
+        src = torch.zeros(64 * D, dtype=torch.int16, device="cuda")
+        dst = torch.zeros(64 * D, dtype=torch.int16, device="cuda")
+        p = src.data_ptr()
+        return L.wafer_hip_attention_prefill_masked(hip._bind(), fmt, p, p, p, dst.data_ptr(), 1, 1, 1, 64, 64, D,
+                                                    0.1, ctypes.byref(m))
+
+    ok = B.AttentionMask()
+    assert call(ok) == 0
+    hip.synchronize()
+    bad = B.AttentionMask()
+    bad.flags = 16
+    assert call(bad) == -1
+    bad = B.AttentionMask()
+    bad.kv_capacity = 10  # < kv_len
+    assert call(bad) == -1
+    bad = B.AttentionMask()
+    bad.flags = B.ATT_WINDOW
+    bad.window = 0
+    assert call(bad) == -1
+    bad = B.AttentionMask()
+    bad.bias_strides[1] = -1
+    assert call(bad) == -1
+    assert call(B.AttentionMask(), D=96) == -3
+    assert call(B.AttentionMask(), fmt=B.F32) == -3
+    with pytest.raises(ValueError):  # a mask that does not broadcast: caught before the C call
+        hip.attention_prefill_masked(t, t, t, t, 0.1, fmt=B.F16, bias=torch.zeros(2, 1, 1, 64, device="cuda"))
+    with pytest.raises(ValueError):
+        hip.attention_prefill_masked(t, t, t, t, 0.1, fmt=B.F16, keep=torch.zeros(1, 1, 1, 63, device="cuda",
+                                                                                    dtype=torch.uint8))
+    with pytest.raises(ValueError):
+        hip.attention_prefill_masked(t, t, t, t, 0.1, fmt=B.F16, bias=torch.zeros(1, 1, 1, 64, device="cuda",
+                                                                                  dtype=torch.float16))

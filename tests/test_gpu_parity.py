@@ -727,10 +727,11 @@ def test_regions_vs_oracle(hip, B, oracle):
 
 
 def test_invalid_arguments_fail_without_launch(hip, B):
-    t = torch.zeros(16, dtype=torch.int16, device="cuda")
+    t96 = torch.zeros(96, dtype=torch.int16, device="cuda")
     with pytest.raises(B.WaferHipError) as e:
-        hip.attention_prefill(t.view(1, 1, 1, 16), t.view(1, 1, 1, 16), t.view(1, 1, 1, 16), t.view(1, 1, 1, 16), 0.1)
-    assert e.value.status == -3  # head_dim 16 is not served
+        hip.attention_prefill(*(t96.view(1, 1, 1, 96),) * 4, 0.1)
+    assert e.value.status == -3  # head_dim 96 is not served (128, or 1..64)
+    t = torch.zeros(16, dtype=torch.int16, device="cuda")
     with pytest.raises(B.WaferHipError):
         hip.gemm(t, t, t, 0, 1, 1)
     with pytest.raises(ValueError):  # operands smaller than the shape: caught before the C call

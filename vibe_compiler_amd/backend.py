@@ -47,8 +47,18 @@ EXPORTS = (
     "wafer_hip_buffer_free", "wafer_hip_copy_to_device", "wafer_hip_copy_to_host", "wafer_hip_convert_route",
     "wafer_hip_strided_copy", "wafer_hip_memset", "wafer_hip_bit2fp", "wafer_hip_mask_move",
     "wafer_hip_compare_expected", "wafer_hip_compare_statistics", "wafer_hip_environment",
-    "wafer_hip_first_nan", "wafer_hip_attention_decode_noalloc",
+    "wafer_hip_first_nan", "wafer_hip_attention_decode_noalloc", "wafer_hip_attention_prefill_masked",
 )
+
+# wafer_hip_attention_mask flags
+ATT_CAUSAL, ATT_WINDOW, ATT_ROUND_SCALED, ATT_ROUND_BIASED = 1, 2, 4, 8
+
+
+class AttentionMask(ctypes.Structure):
+    """wafer_hip_attention_mask (include/wafer_hip.h)."""
+    _fields_ = [("flags", ctypes.c_uint32), ("kv_capacity", ctypes.c_uint32), ("causal_diagonal", ctypes.c_int64),
+                ("window", ctypes.c_int64), ("bias", ctypes.c_void_p), ("bias_strides", ctypes.c_int64 * 3),
+                ("keep", ctypes.c_void_p), ("keep_strides", ctypes.c_int64 * 3)]
 
 # ProgramElementType codes (the comparator's dtypes) and verdicts
 # (ProgramTensorComparisonErrorCode + 1; 0 = accepted).
@@ -123,6 +133,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wafer_hip_unpack.argtypes = [vp, u32, u32, vp, u32, vp, i64, vp]
     L.wafer_hip_attention_prefill.argtypes = [vp, u32, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32, u32]
     L.wafer_hip_attention_decode.argtypes = [vp, u32, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32, u32]
+    L.wafer_hip_attention_prefill_masked.argtypes = [vp, u32, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32,
+                                                     ctypes.POINTER(AttentionMask)]
     L.wafer_hip_attention_decode_noalloc.argtypes = [vp, u32, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32, u32]
     L.wafer_hip_rmsnorm.argtypes = [vp, u32, vp, vp, vp, u64, u64, f32]
     L.wafer_hip_softmax.argtypes = [vp, u32, vp, vp, u64, u64]
@@ -387,6 +399,50 @@ class Context:
             _arg("attention_prefill", name, t, fmt, n)
         _check(self._L.wafer_hip_attention_prefill(self._bind(), fmt, _p(q), _p(k), _p(v), _p(o), B, Hq,
                                                    Hkv, Sq, Skv, D, float(scale), int(causal)))
+
+    def attention_prefill_masked(self, q, k, v, o, scale, *, kv_len=None, causal=False, diagonal=0, window=0,
+                                 bias=None, keep=None, round_scaled=False, round_biased=False, fmt=BF16):
+        """FA prefill with masks (wafer_hip_attention_prefill_masked).  k / v
+        [batch, kv_heads, capacity, head_dim] of which kv_len tokens are valid;
+        causal: key j visible to query i iff j <= i + diagonal; window > 0:
+        and j > i + diagonal - window; bias: additive float32 mask and keep:
+        boolean / uint8 mask, each 4-D [b|1, h|1, q|1, >=kv_len] (size-1
+        dimensions broadcast)."""
+        W = "attention_prefill_masked"
+        if q.dim() != 4 or k.dim() != 4:
+            raise ValueError(f"{W}: q and k must be 4-D")
+        B, Hq, Sq, D = q.shape
+        _, Hkv, cap, _ = k.shape
+        kv_len = cap if kv_len is None else kv_len
+        if tuple(v.shape) != tuple(k.shape) or k.shape[0] != B or k.shape[3] != D or not 0 < kv_len <= cap:
+            raise ValueError(f"{W}: k and v must be [batch, kv_heads, capacity, head_dim] like q, 0 < kv_len <= capacity")
+        for name, t, n in (("q", q, B * Hq * Sq * D), ("k", k, B * Hkv * cap * D), ("v", v, B * Hkv * cap * D),
+                           ("o", o, B * Hq * Sq * D)):
+            _arg(W, name, t, fmt, n)
+        m = AttentionMask()
+        m.flags = (ATT_CAUSAL if causal else 0) | (ATT_WINDOW if window else 0) | \
+            (ATT_ROUND_SCALED if round_scaled else 0) | (ATT_ROUND_BIASED if round_biased else 0)
+        m.kv_capacity = cap
+        m.causal_diagonal = int(diagonal)
+        m.window = int(window)
+
+        def operand(t, name, dtypes):
+            if t is None:
+                return None, (0, 0, 0)
+            if str(t.dtype) not in dtypes:
+                raise ValueError(f"{W}: {name} must be one of {dtypes}, got {t.dtype}")
+            if t.dim() != 4 or t.shape[0] not in (1, B) or t.shape[1] not in (1, Hq) or t.shape[2] not in (1, Sq) \
+                    or t.shape[3] < kv_len or t.stride(3) != 1:
+                raise ValueError(f"{W}: {name} {tuple(t.shape)} does not broadcast to [{B}, {Hq}, {Sq}, >={kv_len}] "
+                                 "with unit key stride")
+            return _p(t), tuple(t.stride(i) if t.shape[i] > 1 else 0 for i in range(3))
+
+        m.bias, bst = operand(bias, "bias", ("torch.float32",))
+        m.keep, kst = operand(keep, "keep", ("torch.bool", "torch.uint8"))
+        m.bias_strides[:] = bst
+        m.keep_strides[:] = kst
+        _check(self._L.wafer_hip_attention_prefill_masked(self._bind(), fmt, _p(q), _p(k), _p(v), _p(o), B, Hq, Hkv,
+                                                          Sq, kv_len, D, float(scale), ctypes.byref(m)))
 
     def attention_decode(self, q, k_cache, v_cache, o, scale, chunks=16, kv_len=None, fmt=BF16):
         B, Hq, one, D = q.shape

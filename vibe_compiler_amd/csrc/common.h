@@ -47,6 +47,12 @@ int status_words(wafer_hip_context *ctx, const char *what, uint8_t **words);
 // stream (a memset node recorded into a graph has given wrong results on
 // later replays, so device words are never cleared with hipMemsetAsync).
 int fill_words(wafer_hip_context *ctx, void *p, uint32_t n, uint32_t value);
+// FA prefill through the masked-attention kernels (fa_masked.hip): the
+// body of wafer_hip_attention_prefill_masked, also taken by
+// wafer_hip_attention_prefill for the cases its own kernel does not serve.
+int attention_prefill_masked(wafer_hip_context *ctx, uint32_t format, const void *q, const void *k, const void *v,
+                             void *o, uint32_t batch, uint32_t q_heads, uint32_t kv_heads, uint32_t q_len,
+                             uint32_t kv_len, uint32_t head_dim, float scale, const wafer_hip_attention_mask *mask);
 
 #define WAFER_CHECK_CTX(ctx)                                                   \
   do {                                                                         \

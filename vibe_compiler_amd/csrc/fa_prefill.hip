@@ -435,10 +435,12 @@ extern "C" int wafer_hip_attention_prefill(wafer_hip_context *ctx, uint32_t form
                                            uint32_t kv_len, uint32_t head_dim,
                                            float scale, uint32_t causal) {
   WAFER_CHECK_CTX(ctx);
-  if (format != WAFER_FMT_BF16)
-    return fail(WAFER_HIP_E_UNSUPPORTED, "attention_prefill: only BF16 storage is served");
-  if (head_dim != D)
-    return fail(WAFER_HIP_E_UNSUPPORTED, "attention_prefill: head_dim must be 128");
+  if (format != WAFER_FMT_BF16 || head_dim != D) {
+    wafer_hip_attention_mask mask{};
+    mask.flags = causal ? WAFER_HIP_ATT_CAUSAL : 0u;
+    return attention_prefill_masked(ctx, format, q, k, v, o, batch, q_heads, kv_heads, q_len, kv_len, head_dim,
+                                    scale, &mask);
+  }
   if (!q || !k || !v || !o) return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill: null tensor");
   if (batch == 0 || q_heads == 0 || kv_heads == 0 || q_len == 0 || kv_len == 0)
     return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill: empty dimension");
