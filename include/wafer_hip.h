@@ -281,7 +281,7 @@ int wafer_hip_attention_prefill_masked(wafer_hip_context *ctx,
  * merge OnlineAttentionMaterialization.cpp:264-373) and finalised as FA.
  * q [batch, q_heads, 1, head_dim]; k/v caches [batch, kv_heads, kv_capacity,
  * head_dim] of which the first kv_len tokens are valid; o like q.
- * format BF16; head_dim 128; q_heads/kv_heads in {1, 2, 4, 8}.
+ * format BF16 or F16; head_dim 128; q_heads/kv_heads in {1, 2, 4, 8}.
  * The context owns the partial-state workspace. */
 int wafer_hip_attention_decode(wafer_hip_context *ctx, uint32_t format,
                                const void *q, const void *k_cache,

@@ -294,3 +294,32 @@ def test_masked_entry_rejects_bad_arguments(hip, B):
     with pytest.raises(ValueError):
         hip.attention_prefill_masked(t, t, t, t, 0.1, fmt=B.F16, bias=torch.zeros(1, 1, 1, 64, device="cuda",
                                                                                   dtype=torch.float16))
+
+
+# ------------------------------------------------------------------ FD decode, F16 storage
+@pytest.mark.parametrize("fmt", [F16, BF16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("Bn,Hq,Hkv,L,cap,chunks", [
+    (1, 32, 32, 1024, 1024, 16),     # attention-decode-kv-cache: Llama-2-7b, 1023 past + 1
+    (1, 32, 32, 4095, 4096, 16),     # attention-decode-kv-cache-long-4096 (valid prefix of the cache)
+    (2, 8, 2, 1000, 1024, 16), (3, 8, 1, 100, 128, 5), (1, 16, 4, 777, 800, 1),
+    (64, 8, 4, 2048, 2048, 16), (48, 16, 8, 600, 600, 4), (64, 4, 2, 513, 513, 16), (64, 4, 4, 300, 300, 3),
+])
+def test_fd_decode_storage_formats(hip, oracle, fmt, Bn, Hq, Hkv, L, cap, chunks):
+    """FD on both storage formats: the chunk grid (small batch*kv_heads) and
+    the one-workgroup-per-(batch, kv head) path (large), GQA 1..8, ragged
+    chunks, a valid prefix of a larger cache; against the oracle's FD."""
+    say("fd decode", fmt, Bn, Hq, Hkv, L, cap, chunks)
+    rng = np.random.default_rng(L + chunks + fmt)
+    D = 128
+    q = store(oracle, fmt, rng.standard_normal((Bn, Hq, 1, D)) * 0.125)
+    k = store(oracle, fmt, rng.standard_normal((Bn, Hkv, cap, D)) * 0.125)
+    v = store(oracle, fmt, rng.standard_normal((Bn, Hkv, cap, D)))
+    scale = 1.0 / math.sqrt(D)
+    ref = oracle.attention_decode(q, k, v, scale, chunks=chunks, kv_len=L, block_k=64, fmt=fmt)
+    o = torch.full((Bn, Hq, 1, D), 0x7E00, dtype=torch.int16, device="cuda")
+    hip.attention_decode(u16(q), u16(k), u16(v), o, scale, chunks=chunks, kv_len=L, fmt=fmt)
+    got = back(o)
+    attention_gate(tof(oracle, fmt, got), tof(oracle, fmt, ref), what="FD")
+    o2 = torch.full((Bn, Hq, 1, D), 0x7E00, dtype=torch.int16, device="cuda")
+    hip.attention_decode_noalloc(u16(q), u16(k), u16(v), o2, scale, chunks=chunks, kv_len=L, fmt=fmt)
+    assert np.array_equal(back(o2), got)

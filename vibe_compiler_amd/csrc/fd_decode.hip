@@ -8,13 +8,13 @@
 // (lib/Wafer/Transforms/Linalg/OnlineAttentionMaterialization.cpp:264-373):
 //   m = max(mL, mR), sL = ExpLp(mL - m), sR = ExpLp(mR - m),
 //   l = lL*sL + lR*sR, acc = accL*sL + accR*sR,
-// then finalised as FA: out = bf16(acc * (1/l)).  GQA: q head h reads kv
+// then finalised as FA: out = narrow(acc * (1/l)) to the BF16 or F16 storage.  GQA: q head h reads kv
 // head h / (q_heads / kv_heads).
 //
 // The kernel is HBM-bound (every KV byte is read once, 4 B of traffic per
 // 4 FLOP), so the design goal is coalesced 128-bit streaming with enough
 // bytes in flight, and a GQA group's query heads served from one read:
-//  * Q.K^T on v_mfma_f32_16x16x32_bf16 with A = 16 keys x 32 d (each lane
+//  * Q.K^T on v_mfma_f32_16x16x32_{bf16,f16} with A = 16 keys x 32 d (each lane
 //    loads 16 B; 4 lanes cover 64 contiguous bytes of a key row) and
 //    B = Q^T padded to 16 head columns; scores land one head per lane column;
 //  * P.V on the VALU with fully coalesced 128-bit V loads (16 lanes read one
@@ -34,12 +34,42 @@
 #include "common.h"
 
 #include <mutex>
+#include <type_traits>
 
 namespace wafer {
 namespace {
 
 constexpr int D = 128;
 constexpr int BLK = 32;  // keys per wave step
+
+// storage type T (__bf16 or _Float16): 8-element operand vectors, the
+// 16x16x32 MFMA, RNE narrowing and the widening of 8 packed values
+template <typename T>
+using v8 = std::conditional_t<std::is_same_v<T, __bf16>, bf16x8, f16x8>;
+template <typename T>
+__device__ inline f32x4 mfma16(v8<T> a, v8<T> b, f32x4 c) {
+  if constexpr (std::is_same_v<T, __bf16>)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+template <typename T>
+__device__ inline uint16_t narrow(float x) {
+  return __builtin_bit_cast(uint16_t, (T)x);
+}
+// element e of 8 packed storage values, widened (exact); for F16 the
+// conversion folds into v_fma_mix_f32 at its use.  (The F16 half is taken
+// by shift and mask: an extract from a bit-cast <2 x half> of one vector
+// element was folded onto element 0 of the vector for every e.)
+template <typename T>
+__device__ inline float elem8(u32x4 w, int e) {
+  const uint32_t x = w[e >> 1];
+  if constexpr (std::is_same_v<T, __bf16>) {
+    return (e & 1) ? u2f(x & 0xffff0000u) : u2f(x << 16);
+  } else {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)((e & 1) ? (x >> 16) : (x & 0xffffu)));
+  }
+}
 
 struct ChunkState {  // per (batch, q_head, chunk), f32
   float acc[D];
@@ -58,13 +88,13 @@ __device__ inline void wave_lds_order() {
 // Online state of one wave over keys [k0, k1), for the G query heads of a
 // GQA group.  On return, lanes with grp == 0 hold acc[h][hl*8 + e]; every
 // lane holds m2 / l of head (lane & 15) (meaningful for heads < G).
-template <int G>
+template <typename T, int G>
 struct WaveSweep {
   float m2, lsum;
   float acc[G][8];
 
   __device__ void run(const uint16_t *__restrict__ Kp, const uint16_t *__restrict__ Vp,
-                      const bf16x8 (&qreg)[4], int k0, int k1, int nblk, float c,
+                      const v8<T> (&qreg)[4], int k0, int k1, int nblk, float c,
                       float (*sP)[G]) {
     const int lane = threadIdx.x & 63, hl = lane & 15, grp = lane >> 4;
     m2 = -__builtin_inff();
@@ -76,7 +106,7 @@ struct WaveSweep {
     for (int blk = 0; blk < nblk; ++blk) {
       const int kbase = k0 + blk * BLK;
       // K: 2 groups of 16 keys; lane loads key kbase + gi*16 + hl, 4 x 16 B
-      bf16x8 kreg[2][4];
+      v8<T> kreg[2][4];
 #pragma unroll
       for (int gi = 0; gi < 2; ++gi) {
         const int key = kbase + gi * 16 + hl;
@@ -84,9 +114,9 @@ struct WaveSweep {
         const uint16_t *kr = Kp + (size_t)(ok ? key : 0) * D + grp * 8;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          kreg[gi][s] = *(const bf16x8 *)(kr + s * 32);
+          kreg[gi][s] = *(const v8<T> *)(kr + s * 32);
           if (!ok)
-            for (int e = 0; e < 8; ++e) kreg[gi][s][e] = (__bf16)0.0f;
+            for (int e = 0; e < 8; ++e) kreg[gi][s][e] = (T)0.0f;
         }
       }
       // V: lane loads keys kbase + grp + 4 i, d = hl*8 + [0,8)
@@ -105,7 +135,7 @@ struct WaveSweep {
         sacc[gi] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-          sacc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kreg[gi][s], qreg[s], sacc[gi], 0, 0, 0);
+          sacc[gi] = mfma16<T>(kreg[gi][s], qreg[s], sacc[gi]);
       }
       float mx = -__builtin_inff();
 #pragma unroll
@@ -129,7 +159,7 @@ struct WaveSweep {
         for (int r = 0; r < 4; ++r) {
           const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[gi][r], c, -e2));
           rs += p;
-          if (hl < G) sP[gi * 16 + 4 * grp + r][hl] = (float)(__bf16)p;
+          if (hl < G) sP[gi * 16 + 4 * grp + r][hl] = (float)(T)p;
         }
       rs += __shfl_xor(rs, 16);
       rs += __shfl_xor(rs, 32);
@@ -149,16 +179,10 @@ struct WaveSweep {
         float p[G];
 #pragma unroll
         for (int h = 0; h < G; ++h) p[h] = sP[grp + 4 * i][h];
-        float vf[8];
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          vf[2 * w] = u2f(vreg[i][w] << 16);
-          vf[2 * w + 1] = u2f(vreg[i][w] & 0xffff0000u);
-        }
 #pragma unroll
         for (int h = 0; h < G; ++h)
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[h][e] = __builtin_fmaf(p[h], vf[e], acc[h][e]);
+          for (int e = 0; e < 8; ++e) acc[h][e] = __builtin_fmaf(p[h], elem8<T>(vreg[i], e), acc[h][e]);
       }
       wave_lds_order();  // the next block's writes to sP follow these reads
     }
@@ -185,19 +209,20 @@ __device__ inline void merge(float &m, float &l, float &a, float mr, float lr, f
   m = mm;
 }
 
-__device__ inline void load_q(const uint16_t *__restrict__ Q, int row_base, int G, bf16x8 (&qreg)[4]) {
+template <typename T>
+__device__ inline void load_q(const uint16_t *__restrict__ Q, int row_base, int G, v8<T> (&qreg)[4]) {
   const int lane = threadIdx.x & 63, hl = lane & 15, grp = lane >> 4;
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     if (hl < G)
-      qreg[s] = *(const bf16x8 *)(Q + ((size_t)(row_base + hl)) * D + s * 32 + grp * 8);
+      qreg[s] = *(const v8<T> *)(Q + ((size_t)(row_base + hl)) * D + s * 32 + grp * 8);
     else
-      for (int e = 0; e < 8; ++e) qreg[s][e] = (__bf16)0.0f;
+      for (int e = 0; e < 8; ++e) qreg[s][e] = (T)0.0f;
   }
 }
 
-template <int G>
-__device__ inline void publish_state(const WaveSweep<G> &st, int wave, float (*sAcc)[G][D],
+template <typename T, int G>
+__device__ inline void publish_state(const WaveSweep<T, G> &st, int wave, float (*sAcc)[G][D],
                                      float (*sM)[G], float (*sL)[G]) {
   const int lane = threadIdx.x & 63, hl = lane & 15, grp = lane >> 4;
   if (grp == 0) {
@@ -215,8 +240,8 @@ __device__ inline void publish_state(const WaveSweep<G> &st, int wave, float (*s
 // ---- one workgroup (16 waves) per (batch, kv_head) ----------------------------
 constexpr int WG_WAVES = 16;
 
-template <int G>
-__global__ __launch_bounds__(1024) void fd_group_bf16_d128(
+template <typename T, int G>
+__global__ __launch_bounds__(1024) void fd_group_d128(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ Kc,
     const uint16_t *__restrict__ Vc, uint16_t *__restrict__ O, int q_heads, int kv_heads,
     int kv_len, int cap, int chunks, int chunk_len, int sub, float c) {
@@ -238,11 +263,11 @@ __global__ __launch_bounds__(1024) void fd_group_bf16_d128(
   int k1 = min(k0 + per, cend);
   if (chunk >= chunks || k1 < k0) k0 = k1 = 0;
 
-  bf16x8 qreg[4];
-  load_q(Q, row_base, G, qreg);
-  WaveSweep<G> st;
+  v8<T> qreg[4];
+  load_q<T>(Q, row_base, G, qreg);
+  WaveSweep<T, G> st;
   st.run(Kp, Vp, qreg, k0, k1, (k1 - k0 + BLK - 1) / BLK, c, sP[wave]);
-  publish_state<G>(st, wave, sAcc, sM, sL);
+  publish_state<T, G>(st, wave, sAcc, sM, sL);
   __syncthreads();
   // left fold over the wave states in key order (= chunk order), finalize
   const int used = min(WG_WAVES, chunks * sub);
@@ -251,13 +276,13 @@ __global__ __launch_bounds__(1024) void fd_group_bf16_d128(
     float m = sM[0][h], l = sL[0][h], a = sAcc[0][h][d];
     for (int w = 1; w < used; ++w) merge(m, l, a, sM[w][h], sL[w][h], sAcc[w][h][d]);
     const float coef = (l == 0.0f) ? 0.0f : 1.0f / l;
-    O[(size_t)(row_base + h) * D + d] = f32_to_bf16(a * coef);
+    O[(size_t)(row_base + h) * D + d] = narrow<T>(a * coef);
   }
 }
 
 // ---- chunk grid + separate fold (small batches) --------------------------------
-template <int G>
-__global__ __launch_bounds__(256) void fd_chunk_bf16_d128(
+template <typename T, int G>
+__global__ __launch_bounds__(256) void fd_chunk_d128(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ Kc,
     const uint16_t *__restrict__ Vc, ChunkState *__restrict__ part, int q_heads, int kv_heads,
     int kv_len, int cap, int chunk_len, int chunks, float c) {
@@ -279,11 +304,11 @@ __global__ __launch_bounds__(256) void fd_chunk_bf16_d128(
   int k1 = min(k0 + per, c1);
   if (k1 < k0) k0 = k1 = 0;
 
-  bf16x8 qreg[4];
-  load_q(Q, row_base, G, qreg);
-  WaveSweep<G> st;
+  v8<T> qreg[4];
+  load_q<T>(Q, row_base, G, qreg);
+  WaveSweep<T, G> st;
   st.run(Kp, Vp, qreg, k0, k1, (k1 - k0 + BLK - 1) / BLK, c, sP[wave]);
-  publish_state<G>(st, wave, sAcc, sM, sL);
+  publish_state<T, G>(st, wave, sAcc, sM, sL);
   __syncthreads();
   for (int idx = threadIdx.x; idx < G * D; idx += 256) {
     const int h = idx / D, d = idx % D;
@@ -300,14 +325,15 @@ __global__ __launch_bounds__(256) void fd_chunk_bf16_d128(
 }
 
 // Left fold over the chunk states of one (batch, q_head), then finalize.
-__global__ __launch_bounds__(128) void fd_fold_bf16_d128(const ChunkState *__restrict__ part,
-                                                         uint16_t *__restrict__ O, int chunks) {
+template <typename T>
+__global__ __launch_bounds__(128) void fd_fold_d128(const ChunkState *__restrict__ part, uint16_t *__restrict__ O,
+                                                    int chunks) {
   const int bh = blockIdx.x, d = threadIdx.x;
   const ChunkState *ps = part + (size_t)bh * chunks;
   float m = ps[0].m2, l = ps[0].l, a = ps[0].acc[d];
   for (int cc = 1; cc < chunks; ++cc) merge(m, l, a, ps[cc].m2, ps[cc].l, ps[cc].acc[d]);
   const float coef = (l == 0.0f) ? 0.0f : 1.0f / l;
-  O[(size_t)bh * D + d] = f32_to_bf16(a * coef);
+  O[(size_t)bh * D + d] = narrow<T>(a * coef);
 }
 
 // ---- the no-allocation variant's scratch -------------------------------------
@@ -341,8 +367,8 @@ int decode(wafer_hip_context *ctx, uint32_t format, const void *q, const void *k
            uint32_t batch, uint32_t q_heads, uint32_t kv_heads, uint32_t kv_len, uint32_t kv_capacity,
            uint32_t head_dim, float scale, uint32_t chunks, bool noalloc) {
   WAFER_CHECK_CTX(ctx);
-  if (format != WAFER_FMT_BF16)
-    return fail(WAFER_HIP_E_UNSUPPORTED, "attention_decode: only BF16 storage is served");
+  if (format != WAFER_FMT_BF16 && format != WAFER_FMT_F16)
+    return fail(WAFER_HIP_E_UNSUPPORTED, "attention_decode: storage must be BF16 or F16");
   if (head_dim != D) return fail(WAFER_HIP_E_UNSUPPORTED, "attention_decode: head_dim must be 128");
   if (!q || !k_cache || !v_cache || !o)
     return fail(WAFER_HIP_E_INVALID_FIELD, "attention_decode: null tensor");
@@ -363,7 +389,10 @@ int decode(wafer_hip_context *ctx, uint32_t format, const void *q, const void *k
   // state and is served as well.
   const int chunk_len = (int)((kv_len + chunks - 1) / chunks);
   const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-  const bool group = G <= 4 && chunks <= (uint32_t)WG_WAVES && (uint64_t)batch * kv_heads * 4 >= (uint64_t)cus * 3;
+  // (the F16 group kernel for G = 4 would spill at the 128 VGPRs of a
+  // 16-wave workgroup: F16 groups of 4 take the chunk grid)
+  const uint32_t gmax = format == WAFER_FMT_BF16 ? 4u : 2u;
+  const bool group = G <= gmax && chunks <= (uint32_t)WG_WAVES && (uint64_t)batch * kv_heads * 4 >= (uint64_t)cus * 3;
   const size_t states = (size_t)batch * q_heads * chunks;
   if (noalloc && !group && states > SCRATCH_STATES)
     return fail(WAFER_HIP_E_UNSUPPORTED, "attention_decode_noalloc: batch * q_heads * chunks = " +
@@ -376,18 +405,25 @@ int decode(wafer_hip_context *ctx, uint32_t format, const void *q, const void *k
   if (group) {
     const int sub = WG_WAVES / (int)chunks;
     dim3 grid(kv_heads, batch);
-#define FD_GROUP(GV)                                                                              \
-  hipLaunchKernelGGL(fd_group_bf16_d128<GV>, grid, dim3(1024), 0, ctx->stream, (const uint16_t *)q, \
+#define FD_GROUP(TT, GV)                                                                          \
+  hipLaunchKernelGGL((fd_group_d128<TT, GV>), grid, dim3(1024), 0, ctx->stream, (const uint16_t *)q, \
                      (const uint16_t *)k_cache, (const uint16_t *)v_cache, (uint16_t *)o,        \
                      (int)q_heads, (int)kv_heads, (int)kv_len, (int)kv_capacity, (int)chunks,    \
                      chunk_len, sub, c)
-    switch (G) {
-    case 1: FD_GROUP(1); break;
-    case 2: FD_GROUP(2); break;
-    default: FD_GROUP(4); break;
+    if (format == WAFER_FMT_BF16) {
+      switch (G) {
+      case 1: FD_GROUP(__bf16, 1); break;
+      case 2: FD_GROUP(__bf16, 2); break;
+      default: FD_GROUP(__bf16, 4); break;
+      }
+    } else {
+      switch (G) {
+      case 1: FD_GROUP(_Float16, 1); break;
+      default: FD_GROUP(_Float16, 2); break;
+      }
     }
 #undef FD_GROUP
-    return launch_status("fd_group_bf16_d128");
+    return launch_status("fd_group_d128");
   }
 
   ChunkState *part = nullptr;
@@ -398,21 +434,34 @@ int decode(wafer_hip_context *ctx, uint32_t format, const void *q, const void *k
     part = (ChunkState *)ctx->workspace;
   }
   dim3 grid(chunks, kv_heads, batch);
-#define FD_CHUNK(GV)                                                                              \
-  hipLaunchKernelGGL(fd_chunk_bf16_d128<GV>, grid, dim3(256), 0, ctx->stream, (const uint16_t *)q, \
+#define FD_CHUNK(TT, GV)                                                                          \
+  hipLaunchKernelGGL((fd_chunk_d128<TT, GV>), grid, dim3(256), 0, ctx->stream, (const uint16_t *)q, \
                      (const uint16_t *)k_cache, (const uint16_t *)v_cache, part, (int)q_heads,    \
                      (int)kv_heads, (int)kv_len, (int)kv_capacity, chunk_len, (int)chunks, c)
-  switch (G) {
-  case 1: FD_CHUNK(1); break;
-  case 2: FD_CHUNK(2); break;
-  case 4: FD_CHUNK(4); break;
-  default: FD_CHUNK(8); break;
+  if (format == WAFER_FMT_BF16) {
+    switch (G) {
+    case 1: FD_CHUNK(__bf16, 1); break;
+    case 2: FD_CHUNK(__bf16, 2); break;
+    case 4: FD_CHUNK(__bf16, 4); break;
+    default: FD_CHUNK(__bf16, 8); break;
+    }
+  } else {
+    switch (G) {
+    case 1: FD_CHUNK(_Float16, 1); break;
+    case 2: FD_CHUNK(_Float16, 2); break;
+    case 4: FD_CHUNK(_Float16, 4); break;
+    default: FD_CHUNK(_Float16, 8); break;
+    }
   }
 #undef FD_CHUNK
-  WAFER_TRY(launch_status("fd_chunk_bf16_d128"));
-  hipLaunchKernelGGL(fd_fold_bf16_d128, dim3(batch * q_heads), dim3(D), 0, ctx->stream, part,
-                     (uint16_t *)o, (int)chunks);
-  return launch_status("fd_fold_bf16_d128");
+  WAFER_TRY(launch_status("fd_chunk_d128"));
+  if (format == WAFER_FMT_BF16)
+    hipLaunchKernelGGL(fd_fold_d128<__bf16>, dim3(batch * q_heads), dim3(D), 0, ctx->stream, part, (uint16_t *)o,
+                       (int)chunks);
+  else
+    hipLaunchKernelGGL(fd_fold_d128<_Float16>, dim3(batch * q_heads), dim3(D), 0, ctx->stream, part, (uint16_t *)o,
+                       (int)chunks);
+  return launch_status("fd_fold_d128");
 }
 
 }  // namespace
