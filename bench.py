@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the gfx950 numeric backend on BASELINE.json's headline metric.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fa,fd,i8,mlp,llama,mv,cmp]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fa,fd,i8,mlp,llama,mv,cmp,regions]
                   (also: copy = counter calibration, vendor = ROCm library kernels for context)
 
 One step = one launch of the hot path over one batch of synthetic, seeded
@@ -10,7 +10,9 @@ config (bf16 Q,K,V [1,16,2048,128], causal) in TFLOP/s of
 algorithmic (causal, visible-pair) work; FD decode (config 2), the int8 GEMM
 (config 3), the fp32 MLP block (config 0) and the decoder layer (config 4)
 are reported in `secondary`,
-each with its own roofline fraction and CPU baseline.  Timing: W untimed
+each with its own roofline fraction and CPU baseline; so are the movement
+commands, the comparator, and the elementwise command with the fused regions
+at HBM scale (`regions`).  Timing: W untimed
 launches, then exactly K launches captured into one HIP graph, replayed
 untimed for SETTLE_S seconds so the GPU clocks settle, and replayed once
 between two HIP events on the stream the kernels run on (the backend binds
@@ -387,6 +389,60 @@ def bench_vendor(torch, hip, steps, warmup):
     return {"workload": "ROCm library kernels on config 1 and 4096^3 GEMM shapes (context only)", **out}
 
 
+REGION_ROWS, REGION_COLS = 65536, 4096  # 256M elements: 512 MiB per bf16 tensor, twice the 256 MB last-level cache
+
+
+def bench_regions(torch, hip, steps, warmup):
+    """The managed elementwise command and the fused regions at HBM scale:
+    every tensor is 256M elements (512 MiB in bf16, 1 GiB in f32), twice the
+    256 MB last-level cache, so each launch streams from HBM.  Algorithmic
+    bytes = one read of every input element plus one write of every output
+    element (RMSNorm's weight, RoPE's positions and the bias row are a few
+    KiB).  Each entry carries its HBM roofline fraction and, when
+    profiles/traffic.json has it, the rocprofv3-measured bytes per launch."""
+    gen = torch.Generator(device="cuda").manual_seed(SEED)
+    R, C = REGION_ROWS, REGION_COLS
+    n = R * C
+    out = []
+
+    def leg(name, kernel, workload, fn, nbytes):
+        ms = timed(torch, fn, steps, warmup)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append({"name": name, "kernel": kernel, "workload": workload, "ms": ms, "value": gbs, "unit": "GB/s",
+                    "algorithmic_bytes": nbytes,
+                    "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK["hbm"], "unit": "GB/s",
+                                 "frac": gbs / PEAK["hbm"], "traffic": traffic_for(name)}})
+
+    B = 2  # bytes per bf16 element
+    x = rnd_bf16(torch, gen, (R, C))
+    y = torch.empty_like(x)
+    z = rnd_bf16(torch, gen, (R, C))
+    from vibe_compiler_amd.backend import BF16, F32
+    leg("ew_add", "ew_kernel (Add)", f"managed elementwise Add, bf16, {n} elements",
+        lambda: hip.elementwise("Add", BF16, x, y, z), 3 * n * B)
+    leg("silu_mul", "silu_mul", f"silu(gate) * up, bf16, {n} elements", lambda: hip.silu_mul(x, z, y), 3 * n * B)
+    leg("gelu_tanh", "gelu_tanh", f"tanh-GELU, bf16, {n} elements", lambda: hip.gelu_tanh(x, y), 2 * n * B)
+    w = rnd_bf16(torch, gen, (C,))
+    leg("rmsnorm", "rmsnorm", f"RMSNorm rows of {C}, bf16, {R} rows", lambda: hip.rmsnorm(x, w, y, 1e-5),
+        2 * n * B + C * B)
+    leg("softmax", "softmax", f"row softmax over {C} columns, bf16, {R} rows", lambda: hip.softmax(x, y),
+        2 * n * B)
+    xr, yr = x.view(R, 32, C // 32), y.view(R, 32, C // 32)
+    pos = torch.arange(R, dtype=torch.int32, device="cuda")
+    leg("rope", "rope", f"RoPE (rotate-half, theta 1e4), bf16 [{R}, 32, {C // 32}]",
+        lambda: hip.rope(xr, yr, pos, 1e4), 2 * n * B + R * 4)
+    del x, y, z, xr, yr
+    torch.cuda.empty_cache()
+    xf = torch.randn((R, C), device="cuda", generator=gen)
+    yf = torch.empty_like(xf)
+    bias = torch.randn((C,), device="cuda", generator=gen)
+    leg("bias_add", "bias_add", f"row bias add, f32 [{R}, {C}]", lambda: hip.bias_add(xf, bias, yf, fmt=F32),
+        2 * n * 4 + C * 4)
+    del xf, yf
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_copy(torch, steps, warmup):
     """A plain device copy of known size: the calibration kernel for the
     rocprofv3 FETCH_SIZE / WRITE_SIZE counters (reads and writes COPY_BYTES)."""
@@ -402,7 +458,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="fa,fd,i8,mlp,llama,mv,cmp", help="comma list of fa, fd, i8, mlp, llama, mv, cmp, copy, vendor")
+    ap.add_argument("--only", default="fa,fd,i8,mlp,llama,mv,cmp,regions",
+                    help="comma list of fa, fd, i8, mlp, llama, mv, cmp, regions, copy, vendor")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -435,6 +492,8 @@ def main() -> int:
         secondary.append(dict(name="movement", **bench_mv(torch, hip, args.steps, args.warmup)))
     if "cmp" in only:
         secondary.append(dict(name="comparator", **bench_cmp(torch, hip, args.steps, args.warmup)))
+    if "regions" in only:
+        secondary.append({"name": "regions", "legs": bench_regions(torch, hip, args.steps, args.warmup)})
     if "copy" in only:
         secondary.append(dict(name="copy", **bench_copy(torch, args.steps, args.warmup)))
     if "vendor" in only:

@@ -726,6 +726,52 @@ def test_regions_vs_oracle(hip, B, oracle):
     assert np.array_equal(host(yb), oracle.bias_add(x, bias))
 
 
+@pytest.mark.parametrize("rows,cols,fmt", [(7, 8, 3), (33, 2048, 3), (5, 2056, 3), (9, 6000, 2), (3, 8192, 5),
+                                           (4, 9000, 3), (2, 24, 5)])
+def test_softmax_shapes(hip, B, oracle, rows, cols, fmt):
+    """Register-resident softmax at 1, 2 and 4 chunks per thread (cols a
+    multiple of 8 up to 8192, with a partial last chunk), the scalar kernel
+    beyond (cols 2056 and 9000), all three float formats."""
+    say("softmax", rows, cols, fmt)
+    rng = np.random.default_rng(rows * cols + fmt)
+    x = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+    if fmt == B.F32:
+        xs, y = dev(x), torch.zeros(x.shape, dtype=torch.float32, device="cuda")
+        hip.softmax(xs, y, fmt=fmt)
+        ref = oracle.softmax(x, fmt=oracle.F32)
+        assert np.allclose(host(y), ref, rtol=2e-5, atol=1e-8)
+        return
+    xb = oracle.f32_to_bf16(x).reshape(x.shape) if fmt == B.BF16 else x.astype(np.float16).view(np.uint16)
+    y = torch.zeros(x.shape, dtype=torch.int16, device="cuda")
+    hip.softmax(u16(xb), y, fmt=fmt)
+    attention_gate(oracle.to_float(fmt, from_u16(y)).reshape(x.shape),
+                   oracle.to_float(fmt, oracle.softmax(xb, fmt=fmt)).reshape(x.shape), what="softmax")
+
+
+@pytest.mark.parametrize("T,H,D", [(300, 1, 128), (64, 32, 128), (129, 5, 16), (77, 3, 64), (10, 2, 6)])
+def test_rope_shapes(hip, B, oracle, T, H, D):
+    """RoPE with the angles taken once per (token, frequency) and applied to
+    every head: one head, 32 heads, head_dim 16 (one 8-frequency group),
+    64, and the scalar kernel (head_dim 6)."""
+    say("rope", T, H, D)
+    rng = np.random.default_rng(T * H + D)
+    x = rng.standard_normal((T, H, D)).astype(np.float32)
+    xb = oracle.f32_to_bf16(x).reshape(x.shape)
+    pos = rng.integers(0, 4096, T).astype(np.int32)
+    y = torch.zeros(x.shape, dtype=torch.int16, device="cuda")
+    hip.rope(u16(xb), y, dev(pos), 1e4, fmt=B.BF16)
+    attention_gate(oracle.bf16_to_f32(from_u16(y)).reshape(x.shape),
+                   oracle.bf16_to_f32(oracle.rope(xb, pos, 1e4)).reshape(x.shape), what="rope")
+    # f32: positions below 32, where one ulp of the device powf in the
+    # inverse frequency moves the angle by < 2e-6 (at position 4096 it moves
+    # it by ~2.4e-4, beyond any f32 bound)
+    pos_s = (pos % 32).astype(np.int32)
+    yf = torch.zeros(x.shape, dtype=torch.float32, device="cuda")
+    hip.rope(dev(x), yf, dev(pos_s), 1e4, fmt=B.F32)
+    rf = oracle.rope(x, pos_s, 1e4, fmt=oracle.F32)
+    assert np.allclose(host(yf), rf, rtol=1e-5, atol=1e-5)
+
+
 def test_invalid_arguments_fail_without_launch(hip, B):
     t96 = torch.zeros(96, dtype=torch.int16, device="cuda")
     with pytest.raises(B.WaferHipError) as e:

@@ -86,7 +86,67 @@ __global__ __launch_bounds__(RT) void rmsnorm_kernel(const void *__restrict__ x,
   }
 }
 
-// e = ExpLp(x - rowmax); y = e * Recip(Sum(e))
+// e = ExpLp(x - rowmax); y = e * Recip(Sum(e)).  Rows of at most
+// 8 * RT * NCH columns (cols % 8 == 0, 16-byte aligned): the row is read
+// once into registers (NCH 16-byte chunks per thread) and each e is taken
+// once; the scalar kernel below re-reads the row for each pass.  The grid
+// has one workgroup per row.
+template <uint32_t F, int NCH>
+__device__ inline void softmax_vec_body(const void *__restrict__ x, void *__restrict__ y, int64_t cols, float *red) {
+  const int64_t base = (int64_t)blockIdx.x * cols;
+  float v[NCH][8];
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    const int64_t c = 8 * ((int64_t)threadIdx.x + ch * RT);
+    if (c < cols) {
+      load8<F>(x, base + c, v[ch]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m = fmaxf(m, v[ch][e]);
+    }
+  }
+  m = block_max(m, red);
+  float s = 0.0f;
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    if (8 * ((int64_t)threadIdx.x + ch * RT) < cols) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[ch][e] = explp_acc(v[ch][e] - m);
+        s += v[ch][e];
+      }
+    }
+  }
+  s = block_sum(s, red);
+  const float rc = 1.0f / s;
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    const int64_t c = 8 * ((int64_t)threadIdx.x + ch * RT);
+    if (c < cols) {
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = v[ch][e] * rc;
+      store8<F>(y, base + c, o);
+    }
+  }
+}
+// (single-parameter kernel names for DISPATCH_F)
+template <uint32_t F>
+__global__ __launch_bounds__(RT) void softmax_vec1(const void *__restrict__ x, void *__restrict__ y, int64_t cols) {
+  __shared__ float red[RT / 64];
+  softmax_vec_body<F, 1>(x, y, cols, red);
+}
+template <uint32_t F>
+__global__ __launch_bounds__(RT) void softmax_vec2(const void *__restrict__ x, void *__restrict__ y, int64_t cols) {
+  __shared__ float red[RT / 64];
+  softmax_vec_body<F, 2>(x, y, cols, red);
+}
+template <uint32_t F>
+__global__ __launch_bounds__(RT) void softmax_vec4(const void *__restrict__ x, void *__restrict__ y, int64_t cols) {
+  __shared__ float red[RT / 64];
+  softmax_vec_body<F, 4>(x, y, cols, red);
+}
+
 template <uint32_t F>
 __global__ __launch_bounds__(RT) void softmax_kernel(const void *__restrict__ x,
                                                      void *__restrict__ y, int64_t cols) {
@@ -176,22 +236,63 @@ __global__ __launch_bounds__(256) void rope_kernel(const void *x, void *y,
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if constexpr (VEC) {
-    const int64_t per_row = half / 8;
-    const int64_t groups = tokens * heads * per_row;
+    // one thread per (token, 8 frequencies, head slice): the 8 angles'
+    // cos / sin are taken once and applied to heads slice, slice + ns, ...
+    // (the same values rope_pair computes per element); with ns slices of
+    // per_tok groups filling a wave, one wave covers ns whole heads of one
+    // token per step, contiguous in memory
+    const int64_t per_tok = half / 8;
+    const int64_t ns = (per_tok <= 64 && 64 % per_tok == 0) ? 64 / per_tok : 1;
+    const int64_t groups = tokens * per_tok * ns;
     for (int64_t e = gid; e < groups; e += stride) {
-      const int64_t i0 = (e % per_row) * 8;
-      const int64_t rowi = e / per_row;  // (token, head)
-      const float pos = (float)positions[rowi / heads];
-      const int64_t lo = rowi * head_dim + i0, hi = lo + half;
-      float xl[8], xh[8], yl[8], yh[8];
-      load8<F>(x, lo, xl);
-      load8<F>(x, hi, xh);
+      const int64_t t = e / (per_tok * ns);
+      const int64_t r = e - t * (per_tok * ns);
+      const int64_t hs = r / per_tok, i0 = (r - hs * per_tok) * 8;
+      const float pos = (float)positions[t];
+      float cs[8], sn[8];
+      if (ns >= 8) {
+        // the slices' lanes share the 8 angles of their group: lane slice k
+        // (k < 8) takes angle k once, and every lane gathers all 8 (a wave
+        // holds whole tokens: groups and the stride are multiples of 64)
+        const int64_t g = r - hs * per_tok;
+        const int kk = (int)(hs & 7);
+        const float angle = pos * rope_inv_freq(theta, i0 + kk, head_dim);
+        const float c1 = cosf(angle), s1 = sinf(angle);
+        const int lane = (int)(threadIdx.x & 63);
+        const int base_lane = lane - (int)r;  // lane of (slice 0, group 0) of this token
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        rope_pair(xl[k], xh[k], pos * rope_inv_freq(theta, i0 + k, head_dim), yl[k], yh[k]);
+        for (int k = 0; k < 8; ++k) {
+          const int src = base_lane + k * (int)per_tok + (int)g;
+          cs[k] = __shfl(c1, src);
+          sn[k] = __shfl(s1, src);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float angle = pos * rope_inv_freq(theta, i0 + k, head_dim);
+          cs[k] = cosf(angle);
+          sn[k] = sinf(angle);
+        }
       }
-      store8<F>(y, lo, yl);
-      store8<F>(y, hi, yh);
+      if (hs >= heads) continue;
+      auto one = [&](int64_t h) __attribute__((always_inline)) {
+        const int64_t lo = (t * heads + h) * head_dim + i0, hi = lo + half;
+        float xl[8], xh[8], yl[8], yh[8];
+        load8<F>(x, lo, xl);
+        load8<F>(x, hi, xh);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) rope_rot(xl[k], xh[k], cs[k], sn[k], yl[k], yh[k]);
+        store8<F>(y, lo, yl);
+        store8<F>(y, hi, yh);
+      };
+      int64_t h = hs;
+      for (; h + 3 * ns < heads; h += 4 * ns) {  // four heads' loads in flight
+        one(h);
+        one(h + ns);
+        one(h + 2 * ns);
+        one(h + 3 * ns);
+      }
+      for (; h < heads; h += ns) one(h);
     }
   } else {
     const int64_t pairs = tokens * heads * half;
@@ -343,6 +444,17 @@ extern "C" int wafer_hip_softmax(wafer_hip_context *ctx, uint32_t format, const 
   if (rows == 0 || cols == 0) return WAFER_HIP_OK;
   if (!x || !y) return fail(WAFER_HIP_E_INVALID_FIELD, "softmax: null tensor");
   if (rows > 0x7fffffffull) return fail(WAFER_HIP_E_INVALID_FIELD, "softmax: too many rows");
+  if (cols % 8 == 0 && cols <= 8 * RT * 4 && aligned16(x) && aligned16(y)) {
+    const dim3 grid((unsigned)rows);
+    if (cols <= 8 * RT) {
+      DISPATCH_F(format, softmax_vec1, grid, dim3(RT), x, y, (int64_t)cols);
+    } else if (cols <= 16 * RT) {
+      DISPATCH_F(format, softmax_vec2, grid, dim3(RT), x, y, (int64_t)cols);
+    } else {
+      DISPATCH_F(format, softmax_vec4, grid, dim3(RT), x, y, (int64_t)cols);
+    }
+    return launch_status("softmax_vec");
+  }
   DISPATCH_F(format, softmax_kernel, dim3((unsigned)rows), dim3(RT), x, y, (int64_t)cols);
   return launch_status("softmax_kernel");
 }
@@ -378,7 +490,9 @@ extern "C" int wafer_hip_rope(wafer_hip_context *ctx, uint32_t format, const voi
   if (count == 0) return WAFER_HIP_OK;
   if (!x || !y || !positions) return fail(WAFER_HIP_E_INVALID_FIELD, "rope: null tensor");
   const bool vec = head_dim % 16 == 0 && aligned16(x) && aligned16(y);
-  DISPATCH_FB(format, vec, rope_kernel, dim3(grid_for(vec ? count / 16 : count / 2)), dim3(256), x, y,
+  const uint64_t per_tok = vec ? head_dim / 16 : 1;  // (>= 1: vec needs head_dim % 16 == 0)
+  const uint64_t ns = (per_tok <= 64 && 64 % per_tok == 0) ? 64 / per_tok : 1;
+  DISPATCH_FB(format, vec, rope_kernel, dim3(grid_for(vec ? tokens * per_tok * ns : count / 2)), dim3(256), x, y,
               (int64_t)tokens, (int64_t)heads, (int64_t)head_dim, positions, theta);
   return launch_status("rope_kernel");
 }
