@@ -59,6 +59,9 @@ def _declare(L: ctypes.CDLL) -> None:
     L.oracle_gemm_formal.argtypes = [i32, i32, vp, vp, vp, vp, i64, i64, i64, i64, i32, i32, i32]
     L.oracle_gemm_i8.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i32, i32]
     L.oracle_elementwise.argtypes = [i32, i32, vp, vp, vp, i64]
+    L.oracle_elementwise_formal.argtypes = [i32, i32, i32, ctypes.c_uint32, ctypes.c_uint32, i32, ctypes.c_uint32,
+                                            vp, vp, vp, i64]
+    L.oracle_pool.argtypes = [i32, i32, vp, vp, vp, vp, vp]
     u32p = ctypes.POINTER(ctypes.c_uint32)
     L.oracle_strided_copy.argtypes = [vp, vp, ctypes.c_uint32, u32p, u32p, u32p, u32p]
     L.oracle_memset.argtypes = [vp, i32, ctypes.c_uint32, i64]
@@ -194,6 +197,42 @@ def elementwise(op: int, fmt: int, a, b=None):
     out = np.zeros(a.size, dtype=storage_dtype(fmt))
     _check(lib().oracle_elementwise(op, fmt, _p(a), _p(b), _p(out), a.size), "elementwise")
     return out.reshape(a.shape)
+
+
+BOOL = 7
+RELATIONS = range(12, 18)
+
+
+def formal_storage(fmt: int):
+    """Storage dtype of a formal-lane logical tensor (raw bits; Bool one byte)."""
+    return {F16: np.uint16, BF16: np.uint16, F32: np.uint32, BOOL: np.uint8}[fmt]
+
+
+def elementwise_formal(op: int, fmt: int, lhs, rhs=None, *, scalar=None, unit=0, group=0, numeric=False):
+    """Formal-lane elementwise command on raw bits; returns the result bits
+    (Bool results as uint8 0 / 1, numeric results in the input storage)."""
+    lhs = np.ascontiguousarray(lhs, dtype=formal_storage(fmt))
+    count = lhs.size
+    rhs_a = None if rhs is None else np.ascontiguousarray(rhs, dtype=formal_storage(fmt))
+    bool_out = fmt == BOOL or (op in RELATIONS and not numeric)
+    dst = np.zeros(count, dtype=np.uint8 if bool_out else formal_storage(fmt))
+    rc = lib().oracle_elementwise_formal(op, fmt, int(bool(numeric)), unit, group, scalar is not None,
+                                         0 if scalar is None else int(scalar), _p(lhs), _p(rhs_a), _p(dst), count)
+    _check(rc, "elementwise_formal")
+    return dst
+
+
+def pool(op: int, fmt: int, src, dst_hw, kernel_strides):
+    """Plain NHWC pooling on raw bits.  src is [N, H, W, C]; dst_hw = (H', W');
+    kernel_strides = (kernel W, kernel H, stride W, stride H)."""
+    src = np.ascontiguousarray(src, dtype=formal_storage(fmt))
+    n, h, w, c = src.shape
+    sshape = np.array([n, h, w, c], dtype=np.uint32)
+    dshape = np.array([n, dst_hw[0], dst_hw[1], c], dtype=np.uint32)
+    ks = np.ascontiguousarray(kernel_strides, dtype=np.uint32)
+    dst = np.zeros((n, dst_hw[0], dst_hw[1], c), dtype=formal_storage(fmt))
+    _check(lib().oracle_pool(op, fmt, _p(sshape), _p(dshape), _p(ks), _p(src), _p(dst)), "pool")
+    return dst
 
 
 def convert(opcode: int, src, dst_fmt: int):

@@ -1344,3 +1344,194 @@ int oracle_compare_statistics(int dtype, const void *actual, const void *expecte
   free(abs_err); free(ulps);
   return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* formal-lane elementwise and pooling                                       */
+/* ------------------------------------------------------------------------ */
+/* Values are held as doubles and every result is rounded once from the
+ * double by round_binary below.  Double holds the exact sum, difference or
+ * product of two F32 values' nearest-even rounding well enough: with
+ * 53 >= 2 * 24 + 2 bits the double-rounded result of +, -, *, / equals the
+ * correctly rounded one (Figueroa, "When is double rounding innocuous?",
+ * 1995), which is what llvm::APFloat computes in
+ * evaluateFormalElementwiseLLVM (FormalNumericElementwise.cpp:160-238). */
+typedef struct { int precision, emin, emax, width; } binary_desc;
+
+static binary_desc describe(int format) {
+  binary_desc d;
+  if (format == F_F16) { d.precision = 11; d.emin = -14; d.emax = 15; d.width = 16; }
+  else if (format == F_BF16) { d.precision = 8; d.emin = -126; d.emax = 127; d.width = 16; }
+  else { d.precision = 24; d.emin = -126; d.emax = 127; d.width = 32; }
+  return d;
+}
+
+static uint32_t formal_sign_bit(int format) { return format == F_F32 ? 0x80000000u : 0x8000u; }
+
+/* canonicalPositiveQuietNaNBits: exponent all ones, top fraction bit set */
+static uint32_t formal_nan(int format) {
+  return format == F_F32 ? 0x7fc00000u : (format == F_F16 ? 0x7e00u : 0x7fc0u);
+}
+
+/* x rounded to nearest, ties to even, in the binary format: the quantum of
+ * x's binade (or of the subnormal range) scales x to an integer part that
+ * nearbyint rounds in the default rounding mode, then the bits are built
+ * from the definition of the encoding. */
+static uint32_t round_binary(int format, double x) {
+  const binary_desc d = describe(format);
+  if (isnan(x)) return formal_nan(format);
+  const uint32_t sign = signbit(x) ? formal_sign_bit(format) : 0u;
+  const int fraction_bits = d.precision - 1, exponent_bits = d.width - 1 - fraction_bits;
+  const uint32_t inf = (((1u << exponent_bits) - 1u) << fraction_bits);
+  double a = fabs(x);
+  if (a == 0.0) return sign;
+  if (isinf(a)) return sign | inf;
+  int k;
+  frexp(a, &k); /* a in [2^(k-1), 2^k) */
+  int e = k - 1;
+  if (e < d.emin) e = d.emin;
+  double n = nearbyint(ldexp(a, fraction_bits - e)); /* integer significand at quantum 2^(e-p+1) */
+  if (n >= ldexp(1.0, d.precision)) { n = ldexp(n, -1); e += 1; } /* a carry into the next binade (n = 2^p) */
+  if (e > d.emax) return sign | inf;
+  const uint64_t m = (uint64_t)n;
+  if (m < (1ull << fraction_bits)) return sign | (uint32_t)m; /* subnormal (or zero) */
+  return sign | ((uint32_t)(e + (1 << (exponent_bits - 1)) - 1) << fraction_bits) |
+         (uint32_t)(m - (1ull << fraction_bits));
+}
+
+static double formal_decode(int format, uint32_t bits) {
+  if (format == F_F32) return (double)u2f(bits);
+  if (format == F_BF16) return (double)u2f(bits << 16);
+  return (double)oracle_f16_to_f32((uint16_t)bits);
+}
+
+static uint32_t formal_one(int format) {
+  return format == F_F32 ? 0x3f800000u : (format == F_F16 ? 0x3c00u : 0x3f80u);
+}
+
+enum { E_ABS = 0, E_RECIP = 1, E_SQUARE = 2, E_NEG = 5, E_MAX = 6, E_MIN = 7, E_ADD = 8, E_SUB = 9, E_MUL = 10,
+       E_EQ = 12, E_NE = 13, E_GE = 14, E_GT = 15, E_LE = 16, E_LT = 17, E_NOT = 18, E_AND = 19, E_OR = 20,
+       E_XOR = 21, E_RELU = 31 };
+
+static int formal_binary(int op) {
+  return op == E_MAX || op == E_MIN || op == E_ADD || op == E_SUB || op == E_MUL || (op >= E_EQ && op <= E_LT) ||
+         op == E_AND || op == E_OR || op == E_XOR;
+}
+
+/* One scalar evaluation (FormalNumericElementwise.cpp:47-247); `numeric`
+ * selects a relation result of 1.0 / +0 in the input format over Bool 1 / 0.
+ * Returns -1 for an operation outside the formal subset. */
+static int64_t formal_scalar(int op, int format, int numeric, uint32_t lb, uint32_t rb) {
+  if (op >= E_NOT && op <= E_XOR) {
+    const int l = lb != 0, r = rb != 0;
+    return op == E_NOT ? !l : op == E_AND ? (l && r) : op == E_OR ? (l || r) : (l != r);
+  }
+  const double a = formal_decode(format, lb), b = formal_binary(op) ? formal_decode(format, rb) : 0.0;
+  const int has_nan = isnan(a) || (formal_binary(op) && isnan(b));
+  if (op >= E_EQ && op <= E_LT) {
+    int r;
+    if (has_nan) r = op == E_NE;
+    else if (op == E_EQ) r = a == b;
+    else if (op == E_NE) r = a != b;
+    else if (op == E_GE) r = a > b || a == b;
+    else if (op == E_GT) r = a > b;
+    else if (op == E_LE) r = a < b || a == b;
+    else r = a < b;
+    return numeric ? (r ? formal_one(format) : 0u) : (uint32_t)r;
+  }
+  const uint32_t sb = formal_sign_bit(format);
+  switch (op) {
+  case E_ABS: return has_nan ? formal_nan(format) : (lb & ~sb);
+  case E_NEG: return has_nan ? formal_nan(format) : (lb ^ sb);
+  case E_RELU: return has_nan ? formal_nan(format) : ((lb & sb) && a != 0.0 ? 0u : lb);
+  case E_MAX:
+  case E_MIN:
+    if (has_nan) return formal_nan(format);
+    if (a == 0.0 && b == 0.0) {
+      const int na = (lb & sb) != 0, nb = (rb & sb) != 0;
+      return (op == E_MAX ? (na && nb) : (na || nb)) ? sb : 0u;
+    }
+    return (op == E_MAX ? a < b : a > b) ? rb : lb;
+  case E_RECIP: return round_binary(format, 1.0 / a);
+  case E_SQUARE: return round_binary(format, a * a);
+  case E_ADD: return round_binary(format, a + b);
+  case E_SUB: return round_binary(format, a - b);
+  case E_MUL: return round_binary(format, a * b);
+  default: return -1;
+  }
+}
+
+static uint32_t raw_load(int format, const void *p, int64_t i) {
+  if (format == F_F32) return ((const uint32_t *)p)[i];
+  if (format == F_BOOL) return ((const uint8_t *)p)[i];
+  return ((const uint16_t *)p)[i];
+}
+
+int oracle_elementwise_formal(int op, int format, int relation_numeric, uint32_t unit, uint32_t group,
+                              int has_scalar, uint32_t scalar, const void *lhs, const void *rhs, void *dst,
+                              int64_t count) {
+  const int bin = formal_binary(op);
+  /* the right operand expanded to `count` values first, as executeElementwise
+   * does (TargetModelTensorNumeric.cpp:350-369) */
+  uint32_t *expanded = NULL;
+  if (bin) {
+    expanded = (uint32_t *)malloc((size_t)(count > 0 ? count : 1) * sizeof(uint32_t));
+    if (!expanded) return -2;
+    for (int64_t i = 0; i < count; ++i) {
+      if (has_scalar) expanded[i] = scalar;
+      else if (group) expanded[i] = raw_load(format, rhs, i / group * 64 + i % 64);
+      else if (unit) expanded[i] = raw_load(format, rhs, i % unit);
+      else expanded[i] = raw_load(format, rhs, i);
+    }
+  }
+  const int bool_out = format == F_BOOL || (op >= E_EQ && op <= E_LT && !relation_numeric);
+  int rc = 0;
+  for (int64_t i = 0; i < count && rc == 0; ++i) {
+    const uint32_t lb = raw_load(format, lhs, i), rb = bin ? expanded[i] : 0u;
+    if (format == F_BOOL && (lb > 1u || rb > 1u)) { rc = -3; break; } /* validateOperand */
+    const int64_t r = formal_scalar(op, format, relation_numeric, lb, rb);
+    if (r < 0) { rc = -1; break; }
+    if (bool_out) ((uint8_t *)dst)[i] = (uint8_t)r;
+    else if (format == F_F32) ((uint32_t *)dst)[i] = (uint32_t)r;
+    else ((uint16_t *)dst)[i] = (uint16_t)r;
+  }
+  free(expanded);
+  return rc;
+}
+
+/* executePool (TargetModelTensorNumeric.cpp:540-570): per window offset
+ * (kernel row outer, kernel column inner) the strided window of every output
+ * position is gathered into a vector and combined with the running result;
+ * Max / Min start from the first window, Sum from +0. */
+int oracle_pool(int op, int format, const uint32_t *src_shape, const uint32_t *dst_shape,
+                const uint32_t *kernel_strides, const void *src, void *dst) {
+  const int combine = op == 117 ? E_MAX : op == 119 ? E_MIN : op == 116 ? E_ADD : -1;
+  if (combine < 0) return -1;
+  const int64_t count = (int64_t)dst_shape[0] * dst_shape[1] * dst_shape[2] * dst_shape[3];
+  uint32_t *result = (uint32_t *)calloc((size_t)(count > 0 ? count : 1), sizeof(uint32_t));
+  uint32_t *window = (uint32_t *)malloc((size_t)(count > 0 ? count : 1) * sizeof(uint32_t));
+  if (!result || !window) { free(result); free(window); return -2; }
+  for (uint32_t kh = 0; kh < kernel_strides[1]; ++kh)
+    for (uint32_t kw = 0; kw < kernel_strides[0]; ++kw) {
+      int64_t o = 0;
+      for (uint32_t n = 0; n < dst_shape[0]; ++n)
+        for (uint32_t h = 0; h < dst_shape[1]; ++h)
+          for (uint32_t w = 0; w < dst_shape[2]; ++w)
+            for (uint32_t c = 0; c < dst_shape[3]; ++c) {
+              const int64_t sh = (int64_t)h * kernel_strides[3] + kh, sw = (int64_t)w * kernel_strides[2] + kw;
+              window[o++] = raw_load(format, src, (((int64_t)n * src_shape[1] + sh) * src_shape[2] + sw) *
+                                                      src_shape[3] + c);
+            }
+      if (kh == 0 && kw == 0 && combine != E_ADD) {
+        memcpy(result, window, (size_t)count * sizeof(uint32_t));
+        continue;
+      }
+      for (int64_t i = 0; i < count; ++i) result[i] = (uint32_t)formal_scalar(combine, format, 0, result[i], window[i]);
+    }
+  for (int64_t i = 0; i < count; ++i) {
+    if (format == F_F32) ((uint32_t *)dst)[i] = result[i];
+    else ((uint16_t *)dst)[i] = (uint16_t)result[i];
+  }
+  free(result);
+  free(window);
+  return 0;
+}

@@ -48,6 +48,7 @@ EXPORTS = (
     "wafer_hip_strided_copy", "wafer_hip_memset", "wafer_hip_bit2fp", "wafer_hip_mask_move",
     "wafer_hip_compare_expected", "wafer_hip_compare_statistics", "wafer_hip_environment",
     "wafer_hip_first_nan", "wafer_hip_attention_decode_noalloc", "wafer_hip_attention_prefill_masked",
+    "wafer_hip_elementwise_formal", "wafer_hip_pool",
 )
 
 # wafer_hip_attention_mask flags
@@ -59,6 +60,25 @@ class AttentionMask(ctypes.Structure):
     _fields_ = [("flags", ctypes.c_uint32), ("kv_capacity", ctypes.c_uint32), ("causal_diagonal", ctypes.c_int64),
                 ("window", ctypes.c_int64), ("bias", ctypes.c_void_p), ("bias_strides", ctypes.c_int64 * 3),
                 ("keep", ctypes.c_void_p), ("keep_strides", ctypes.c_int64 * 3)]
+
+class ElementwiseCommand(ctypes.Structure):
+    """wafer_hip_elementwise_command (include/wafer_hip.h)."""
+    _fields_ = [("operation", ctypes.c_uint32), ("format", ctypes.c_uint32), ("relation_numeric", ctypes.c_uint32),
+                ("rhs_unit_elements", ctypes.c_uint32), ("rhs_group_elements", ctypes.c_uint32),
+                ("has_rhs_scalar", ctypes.c_uint32), ("rhs_scalar", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+                ("element_count", ctypes.c_uint64)]
+
+
+class PoolCommand(ctypes.Structure):
+    """wafer_hip_pool_command (include/wafer_hip.h)."""
+    _fields_ = [("operation", ctypes.c_uint32), ("format", ctypes.c_uint32),
+                ("source_shape", ctypes.c_uint32 * 4), ("destination_shape", ctypes.c_uint32 * 4),
+                ("pads", ctypes.c_uint32 * 4), ("kernel_strides", ctypes.c_uint32 * 4),
+                ("has_index_destination", ctypes.c_uint32)]
+
+
+# TargetPoolingOperation (include/Wafer/Target/TargetOperation.h:149-156)
+POOL = dict(Average=115, Sum=116, Maximum=117, IndexedMaximum=118, Minimum=119, IndexedMinimum=120)
 
 # ProgramElementType codes (the comparator's dtypes) and verdicts
 # (ProgramTensorComparisonErrorCode + 1; 0 = accepted).
@@ -155,6 +175,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wafer_hip_bit2fp.argtypes = [vp, vp, vp, u32, u64]
     L.wafer_hip_mask_move.argtypes = [vp, vp, vp, vp, u32, u64]
     L.wafer_hip_first_nan.argtypes = [vp, u32, vp, u64, ctypes.POINTER(u64)]
+    L.wafer_hip_elementwise_formal.argtypes = [vp, ctypes.POINTER(ElementwiseCommand), vp, vp, vp]
+    L.wafer_hip_pool.argtypes = [vp, ctypes.POINTER(PoolCommand), vp, vp]
     pt = ctypes.POINTER(ProgramTensorDesc)
     L.wafer_hip_compare_expected.argtypes = [vp, pt, pt, ctypes.POINTER(ComparisonPolicy), u32p, ctypes.c_char_p,
                                              ctypes.c_size_t]
@@ -571,6 +593,36 @@ class Context:
         if (count + 7) // 8 > bits.numel() * bits.element_size() or count > dst.numel():
             raise ValueError("bit2fp: count exceeds a tensor")
         _check(self._L.wafer_hip_bit2fp(self._bind(), _p(bits), _p(dst), fmt, count))
+
+    def elementwise_formal(self, op, fmt, lhs, dst, rhs=None, *, scalar=None, unit=0, group=0, numeric=False,
+                           count=None):
+        """Formal-lane elementwise command (wafer_hip_elementwise_formal).
+        Bool operands and Bool results are uint8 tensors of 0 / 1."""
+        op = EW[op] if isinstance(op, str) else op
+        n = lhs.numel() if count is None else count
+        _arg("elementwise_formal", "lhs", lhs, fmt, n)
+        bool_out = fmt == BOOL or (12 <= op <= 17 and not numeric)
+        _arg("elementwise_formal", "dst", dst, BOOL if bool_out else fmt, n)
+        if rhs is not None:
+            need = n // group * 64 if group else (unit if unit else n)
+            _arg("elementwise_formal", "rhs", rhs, fmt, need)
+        cmd = ElementwiseCommand(op, fmt, int(bool(numeric)), unit, group, int(scalar is not None),
+                                 0 if scalar is None else int(scalar), 0, n)
+        _check(self._L.wafer_hip_elementwise_formal(self._bind(), ctypes.byref(cmd), _p(lhs), _p(rhs), _p(dst)))
+
+    def pool(self, op, fmt, src, dst, kernel_strides, *, pads=(0, 0, 0, 0), indexed_destination=False):
+        """Plain NHWC pooling (wafer_hip_pool); src [N, H, W, C] and dst
+        [N, H', W', C] tensors; kernel_strides (kernel W, kernel H, stride W,
+        stride H)."""
+        op = POOL[op] if isinstance(op, str) else op
+        if src.dim() != 4 or dst.dim() != 4:
+            raise ValueError("pool: src and dst must be 4-d NHWC tensors")
+        _arg("pool", "src", src, fmt, src.numel())
+        _arg("pool", "dst", dst, fmt, dst.numel())
+        u4 = ctypes.c_uint32 * 4
+        cmd = PoolCommand(op, fmt, u4(*src.shape), u4(*dst.shape), u4(*pads), u4(*kernel_strides),
+                          int(bool(indexed_destination)))
+        _check(self._L.wafer_hip_pool(self._bind(), ctypes.byref(cmd), _p(src), _p(dst)))
 
     def mask_move(self, src, mask, dst, fmt):
         if fmt in (F16, BF16, F32):
