@@ -54,6 +54,7 @@ def torch():
     (77, 3, 64, 200, 8, "bf16"),           # ragged: odd tokens and heads, head groups of 1
     (300, 6, 32, 192, 0, "f16"),
     (64, 5, 16, 96, 16, "f32"),
+    (64, 3, 256, 800, 0, "bf16"),         # head_dim above 128: the per-thread kernel
 ])
 def test_head_permute_rope_bit_exact(hip, torch, tokens, heads, head_dim, stride, offset, fmt):
     """The fused kernel against head_permute followed by rope, bit for bit

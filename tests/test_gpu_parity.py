@@ -391,6 +391,70 @@ def test_mfma_gemm_256_tiles_vs_formal(hip, B, oracle, rt, fmt, out):
         assert int(np.count_nonzero(got_all.view(np.uint16) == 0x1234)) < 64
 
 
+@pytest.mark.parametrize("m,n,out", [(1024, 6144, 3), (1024, 6144, 5), (512, 12288, 3)])
+def test_mfma_gemm_192_tiles_vs_formal(hip, B, oracle, m, n, out):
+    """Shapes that take the 128x192 tiles (one round of 256 workgroups where
+    128x128 tiles need two: the decoder layer's QKV projection), k = 256.
+    Sampled rows against the GPU formal lane (pinned to the CPU oracle on two
+    rows), every output written; MFMA GEMM tolerances."""
+    say("mfma gemm 128x192 tiles", m, n, out)
+    rng = np.random.default_rng(m + n + out)
+    K = 256
+    a = oracle.f32_to_bf16(rng.standard_normal((m, K)).astype(np.float32)).reshape(m, K)
+    bt = oracle.f32_to_bf16((rng.standard_normal((n, K)) / math.sqrt(K)).astype(np.float32)).reshape(n, K)
+    ad, bd = u16(a), u16(bt)
+    if out == B.F32:
+        dst = torch.full((m, n), 7.5, dtype=torch.float32, device="cuda")
+    else:
+        dst = torch.full((m, n), 0x1234, dtype=torch.int16, device="cuda")
+    hip.gemm_mfma(ad, bd, dst, m, K, n, in_fmt=B.BF16, out_fmt=out, rhs_t=True)
+    got_all = host(dst)
+    rows = np.concatenate([[0, 1, 127, 128, m - 1], rng.choice(m, 27, replace=False)])
+    sub = np.ascontiguousarray(a[rows])
+    ref_d = torch.zeros((len(rows), n), dtype=torch.float32, device="cuda")
+    hip.gemm(u16(sub), bd, ref_d, len(rows), K, n, in_fmt=B.BF16, out_fmt=B.F32, rhs_t=True)
+    ref = host(ref_d)
+    cpu = oracle.gemm_formal(B.BF16, oracle.F32, np.ascontiguousarray(sub[:2]), bt, 2, K, n, rhs_t=True)
+    assert np.array_equal(cpu.reshape(2, n).view(np.uint32), ref[:2].view(np.uint32))
+    if out == B.F32:
+        got = got_all[rows]
+        tol_rel, tol_max = 1e-5, 1e-4
+        assert not np.any(got_all == 7.5)
+    else:
+        got = oracle.to_float(B.BF16, got_all[rows].view(np.uint16)).reshape(len(rows), n)
+        tol_rel, tol_max = 2e-3, 2e-2
+        assert int(np.count_nonzero(got_all.view(np.uint16) == 0x1234)) < 64
+    rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert rel <= tol_rel and np.abs(got - ref).max() <= tol_max * np.abs(ref).max(), (rel,)
+
+
+@pytest.mark.parametrize("m,k,n", [(1024, 128, 6144), (1024, 128, 28672)])
+def test_i8_gemm_192_tiles_and_strips_bit_exact(hip, B, oracle, m, k, n):
+    """int8 on the 128x192 tiles (n 6144) and on 448 256x256 tiles, whose
+    workgroups walk per-XCD column strips (n 28672): y-only and acc_out runs,
+    bit-exact against int64 products on sampled rows and a column checksum of
+    the whole accumulator."""
+    say("i8 gemm 192 tiles / strips", m, k, n)
+    rng = np.random.default_rng(m + k + n)
+    a = rng.integers(-128, 128, size=(m, k), dtype=np.int64).astype(np.int8)
+    bt = rng.integers(-128, 128, size=(n, k), dtype=np.int64).astype(np.int8)
+    scale = rng.uniform(0.001, 0.01, size=n).astype(np.float32)
+    ad, bd, sd = dev(a), dev(bt), dev(scale)
+    y = torch.full((m, n), 0x1234, dtype=torch.int16, device="cuda")
+    hip.gemm_i8(ad, bd, sd, y, m, k, n, rhs_t=True)
+    acc = torch.zeros((m, n), dtype=torch.int32, device="cuda")
+    y2 = torch.zeros((m, n), dtype=torch.int16, device="cuda")
+    hip.gemm_i8(ad, bd, sd, y2, m, k, n, acc_out=acc, rhs_t=True)
+    gy, gy2, gacc = host(y).view(np.uint16), host(y2).view(np.uint16), host(acc)
+    assert np.array_equal(gy, gy2)
+    assert np.array_equal(gacc.astype(np.int64).sum(axis=0), a.astype(np.int64).sum(axis=0) @ bt.T.astype(np.int64))
+    rows = np.concatenate([[0, 1, 127, 128, m - 1], rng.choice(m, 11, replace=False)])
+    sub = np.ascontiguousarray(a[rows])
+    acc_ref, y_ref = oracle.gemm_i8(sub, bt, scale, len(rows), k, n, rhs_t=True)
+    assert np.array_equal(gacc[rows], acc_ref)
+    assert np.array_equal(gy[rows], y_ref)
+
+
 @pytest.mark.parametrize("m,k,n,rt,fmt", [(100, 96, 130, 0, 3), (1, 32, 1, 1, 2), (300, 256, 257, 1, 3),
                                           (77, 512, 384, 0, 2), (200, 160, 72, 0, 3), (513, 64, 129, 1, 3)])
 def test_mfma_gemm_ragged_vs_formal(hip, B, oracle, m, k, n, rt, fmt):
@@ -746,6 +810,32 @@ def test_softmax_shapes(hip, B, oracle, rows, cols, fmt):
     hip.softmax(u16(xb), y, fmt=fmt)
     attention_gate(oracle.to_float(fmt, from_u16(y)).reshape(x.shape),
                    oracle.to_float(fmt, oracle.softmax(xb, fmt=fmt)).reshape(x.shape), what="softmax")
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 8), (67, 520), (5, 1024), (33, 2056), (1024, 4096), (3, 4104), (9, 33)])
+@pytest.mark.parametrize("fmt", [3, 5, 2])
+def test_rmsnorm_shapes(hip, B, oracle, rows, cols, fmt):
+    """The wave-per-row RMSNorm at 1, 2, 4 and 8 chunks per lane (cols a
+    multiple of 8 up to 4096, partial last chunks, row counts that leave a
+    workgroup's last waves idle), the workgroup kernel beyond (4104) and
+    the scalar kernel (33); all three float formats against the oracle."""
+    say("rmsnorm", rows, cols, fmt)
+    rng = np.random.default_rng(rows * cols + fmt)
+    x = (rng.standard_normal((rows, cols)) * 2).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    if fmt == B.F32:
+        y = torch.zeros(x.shape, dtype=torch.float32, device="cuda")
+        hip.rmsnorm(dev(x), dev(w), y, 1e-5, fmt=fmt)
+        ref = oracle.rmsnorm(x, w, 1e-5, fmt=oracle.F32)
+        assert np.allclose(host(y), ref, rtol=2e-6, atol=1e-7)
+        return
+    cv = (lambda a: oracle.f32_to_bf16(a).reshape(a.shape)) if fmt == B.BF16 else \
+        (lambda a: a.astype(np.float16).view(np.uint16))
+    xb, wb = cv(x), cv(w)
+    y = torch.zeros(x.shape, dtype=torch.int16, device="cuda")
+    hip.rmsnorm(u16(xb), u16(wb), y, 1e-5, fmt=fmt)
+    attention_gate(oracle.to_float(fmt, from_u16(y)).reshape(x.shape),
+                   oracle.to_float(fmt, oracle.rmsnorm(xb, wb, 1e-5, fmt=fmt)).reshape(x.shape), what="rmsnorm")
 
 
 @pytest.mark.parametrize("T,H,D", [(300, 1, 128), (64, 32, 128), (129, 5, 16), (77, 3, 64), (10, 2, 6)])

@@ -17,8 +17,12 @@
 // chunks of each LDS row are XOR-swizzled so that the rows one fragment
 // read touches hit distinct bank groups (conflict-free ds_read_b128).  A normal
 // (K-major) rhs is first re-laid out to Bt by a transpose kernel into
-// context scratch.  Workgroup ids are mapped so that the 32 tiles served by
-// one XCD form a 4x8 block of the output, bounding that XCD's L2 working set.
+// context scratch.  Workgroup ids are mapped so that the 32 tiles one XCD
+// runs at a time form a 4x8 block of the output (whole rounds of 256 tiles),
+// or walk that XCD's own column strip in 4-row groups (other grids whose tile
+// rows divide by 4 and tile columns by 8), bounding the XCD's L2 working set.
+// Tiles are 256x256 when they fill the chip, 128x192 where that saves a round
+// of workgroups, else 128x128.
 //
 // int8 semantics (no reference implementation exists; the closed form on the
 // reference's conversion routes): acc = sum_k int32(a)*int32(b) exactly
@@ -78,10 +82,17 @@ struct GemmArgs {
 // columns.  Those tiles load their last real A row (Bt row) again in place of
 // the missing ones, so every load stays inside the operands, and store only
 // the outputs that exist.
-template <int KIND, int BM, int BN, int OUT, bool TAIL, int SB>
-__global__ __launch_bounds__(512) void gemm_nt_kernel(GemmArgs args) {
-  // 8 waves as 2 (M) x 4 (N); each wave owns a (BM/2) x (BN/4) sub-tile
-  constexpr int NT = 512, WM = 2, WN = 4;
+//
+//
+// WM x WN waves, each owning a (BM/WM) x (BN/WN) sub-tile: 2 x 4 (8 waves,
+// two per SIMD) by default; 4 x 2 serves tiles whose width is not a multiple
+// of 128 (128 x 192, 128 x 384); 2 x 2 (4 waves, one per SIMD with all 512
+// registers) halves the LDS fragment traffic per MFMA.
+template <int KIND, int BM, int BN, int OUT, bool TAIL, int SB, int WM = 2, int WN = 4>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(1, WM * WN == 4 ? 1 : 2))) void
+gemm_nt_kernel(GemmArgs args) {
+  constexpr int NT = 64 * WM * WN, NW = WM * WN;
+  static_assert(BM % (32 * WM) == 0 && BN % (32 * WN) == 0, "whole 32x32 MFMA tiles per wave");
   constexpr int WTM = BM / WM / 32, WTN = BN / WN / 32;  // 32x32 MFMA tiles per wave
   // SB bytes of K per stage (2 or 4 MFMA k-steps); NS stages fill 128 KiB
   constexpr int CH = SB / 16, KS = SB / 32;
@@ -111,6 +122,15 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmArgs args) {
       const int bm = blk / gn, bn = blk % gn;
       tm = bm * 4 + j / 8;
       tn = bn * 8 + j % 8;
+    } else if (tiles_m % 4 == 0 && tiles_n % 8 == 0) {
+      // XCD x owns the column strip [x sw, (x + 1) sw) of the grid, walked
+      // in groups of 4 tile rows, column by column within a group: the 32
+      // tiles an XCD runs at once span 4 rows and 8 columns
+      const int xcd = bid % 8, j = bid / 8;
+      const int sw = tiles_n / 8, per_group = 4 * sw;
+      const int grp = j / per_group, w = j % per_group;
+      tm = grp * 4 + w % 4;
+      tn = xcd * sw + w / 4;
     } else {
       tm = bid / tiles_n;
       tn = bid % tiles_n;
@@ -254,24 +274,31 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmArgs args) {
   // a row XOR-swizzled by (row / 4) % CPR, so the two row groups of one
   // ds_write_b16 land in distinct banks), then reads it back 16 bytes per
   // lane and stores whole 16-byte row segments (64 lanes cover 1 KiB of
-  // consecutive rows) instead of scattered 2-byte stores.  Waves 0-3 stage
-  // in sA, 4-7 in sB, after a barrier that retires every wave's fragment
+  // consecutive rows) instead of scattered 2-byte stores.  The sub-tiles are
+  // staged in sA, then sB, after a barrier that retires every wave's fragment
   // reads and stage moves.
   if constexpr (OUT != OUT_F32) {
     constexpr int OR = BM / WM;                                     // rows per wave
     constexpr int OC = OUT == OUT_SWIGLU ? BN / WN / 2 : BN / WN;   // output columns per wave
     constexpr int CPR = OC * 2 / 16;                                // 16-byte chunks per row
-    static_assert(4 * OR * OC * 2 <= NS * BM * CH * 16 && 4 * OR * OC * 2 <= NS * BN * CH * 16,
-                  "a wave's staged sub-tile fits its quarter of sA / sB");
+    static_assert(OR * CPR % 64 == 0, "whole 16-byte store rounds");
+    // position of 16-byte chunk c in a staged row: XOR when CPR is a power of
+    // two, else a rotation; either way rows 4 apart put a chunk in different
+    // positions
+    auto spos = [](int row, int c) __attribute__((always_inline)) {
+      return (CPR & (CPR - 1)) == 0 ? c ^ ((row >> 2) & (CPR - 1)) : (c + (row >> 2)) % CPR;
+    };
+    // the first IN_A waves stage in sA, the others in sB
+    constexpr int PER = OR * OC * 2, IN_A = (NS * BM * CH * 16) / PER < NW ? (NS * BM * CH * 16) / PER : NW;
+    static_assert((NW - IN_A) * PER <= NS * BN * CH * 16, "the staged sub-tiles fit in sA and sB");
     const int ldy = OUT == OUT_SWIGLU ? args.n / 2 : args.n;
     const bool staged = !TAIL && ldy % 8 == 0 && (((uintptr_t)args.y) & 15) == 0 &&
                         (OUT != OUT_I8_DEQUANT || args.acc_out == nullptr);
     if (staged) {
       __syncthreads();
-      char *stage = (char *)(wave < 4 ? &sA[0][0] : &sB[0][0]) + (wave & 3) * (OR * OC * 2);
+      char *stage = wave < IN_A ? (char *)&sA[0][0] + wave * PER : (char *)&sB[0][0] + (wave - IN_A) * PER;
       auto put = [&](int row, int col, uint16_t v) __attribute__((always_inline)) {
-        const int sw = (row >> 2) & (CPR - 1);
-        *(uint16_t *)(stage + row * (CPR * 16) + (((col >> 3) ^ sw) << 4) + (col & 7) * 2) = v;
+        *(uint16_t *)(stage + row * (CPR * 16) + (spos(row, col >> 3) << 4) + (col & 7) * 2) = v;
       };
       if constexpr (OUT == OUT_SWIGLU) {
         static_assert(KIND == KIND_BF16, "the fused epilogue serves bf16");
@@ -309,7 +336,7 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(GemmArgs args) {
 #pragma unroll
       for (int q = 0; q < OR * CPR / 64; ++q) {
         const int idx = q * 64 + lane, row = idx / CPR, c = idx % CPR;
-        const u32x4 v = *(const u32x4 *)(stage + row * (CPR * 16) + ((c ^ ((row >> 2) & (CPR - 1))) << 4));
+        const u32x4 v = *(const u32x4 *)(stage + row * (CPR * 16) + (spos(row, c) << 4));
         *(u32x4 *)(ybase + (size_t)row * ldy + c * 8) = v;
       }
       return;
@@ -490,15 +517,33 @@ int launch_gemm_tiles(hipStream_t st, GemmArgs args) {
     args.tiles_n = args.n / 256;
     hipLaunchKernelGGL((gemm_nt_kernel<KIND, 256, 256, OUT, false, SB>), dim3(args.tiles_m * args.tiles_n),
                        dim3(512), 0, st, args);
-  } else {
-    args.tiles_m = (args.m + 127) / 128;
-    args.tiles_n = (args.n + 127) / 128;
-    const dim3 grid(args.tiles_m * args.tiles_n);
-    if (args.m % 128 == 0 && args.n % 128 == 0)
-      hipLaunchKernelGGL((gemm_nt_kernel<KIND, 128, 128, OUT, false, SB>), grid, dim3(512), 0, st, args);
-    else
-      hipLaunchKernelGGL((gemm_nt_kernel<KIND, 128, 128, OUT, true, SB>), grid, dim3(512), 0, st, args);
+    return launch_status("gemm_nt_kernel");
   }
+  // 128x192 tiles where they need fewer rounds of 256 workgroups for 1.5x
+  // the work per tile (QKV at M = 1024: 256 tiles against 384 of 128x128)
+  // (128-byte K stages only: 64-byte stages would not split 320 rows of DMA
+  // evenly over 8 waves)
+  const long t128 = (long)((args.m + 127) / 128) * ((args.n + 127) / 128);
+  if (SB == 128 && args.m % 128 == 0 && args.n % 192 == 0) {
+    const long t192 = (long)(args.m / 128) * (args.n / 192);
+    if (3 * ((t192 + 255) / 256) < 2 * ((t128 + 255) / 256)) {
+      args.tiles_m = args.m / 128;
+      args.tiles_n = args.n / 192;
+      if constexpr (SB == 128) {
+        hipLaunchKernelGGL((gemm_nt_kernel<KIND, 128, 192, OUT, false, SB, 4, 2>),
+                           dim3(args.tiles_m * args.tiles_n), dim3(512), 0, st, args);
+        return launch_status("gemm_nt_kernel");
+      }
+    }
+  }
+  args.tiles_m = (args.m + 127) / 128;
+  args.tiles_n = (args.n + 127) / 128;
+  const dim3 grid(args.tiles_m * args.tiles_n);
+  // 4 x 2 waves (each 32 x 64) measured 2-3 % faster than 2 x 4 on 128x128 tiles
+  if (args.m % 128 == 0 && args.n % 128 == 0)
+    hipLaunchKernelGGL((gemm_nt_kernel<KIND, 128, 128, OUT, false, SB, 4, 2>), grid, dim3(512), 0, st, args);
+  else
+    hipLaunchKernelGGL((gemm_nt_kernel<KIND, 128, 128, OUT, true, SB, 4, 2>), grid, dim3(512), 0, st, args);
   return launch_status("gemm_nt_kernel");
 }
 

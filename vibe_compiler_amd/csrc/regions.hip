@@ -86,6 +86,49 @@ __global__ __launch_bounds__(RT) void rmsnorm_kernel(const void *__restrict__ x,
   }
 }
 
+// The same row region with one wave per row for rows of at most 512 * NCH
+// columns (cols % 8 == 0, 16-byte aligned): the row stays in registers
+// between the sum and the scaling (one read of x), the sum is a wave
+// reduction (no LDS, no barrier), and a 256-thread workgroup serves 4 rows.
+template <uint32_t F, int NCH>
+__global__ __launch_bounds__(256) void rmsnorm_wave_kernel(const void *__restrict__ x, const void *__restrict__ w,
+                                                           void *__restrict__ y, int64_t rows, int64_t cols,
+                                                           float inv_n, float eps) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole waves
+  const int lane = threadIdx.x & 63;
+  const int64_t base = row * cols;
+  float v[NCH][8];
+  float s = 0.0f;
+  // every chunk load is issued before any is used: a chunk past the row
+  // end loads the row's last chunk again and adds nothing
+#pragma unroll
+  for (int q = 0; q < NCH; ++q) {
+    const int64_t c = 8 * (lane + 64 * q);
+    load8<F>(x, base + (c < cols ? c : cols - 8), v[q]);
+  }
+#pragma unroll
+  for (int q = 0; q < NCH; ++q) {
+    const bool in_row = 8 * (lane + 64 * q) < cols;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += in_row ? v[q][e] * v[q][e] : 0.0f;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+  const float rs = 1.0f / sqrtf(s * inv_n + eps);
+#pragma unroll
+  for (int q = 0; q < NCH; ++q) {
+    const int64_t c = 8 * (lane + 64 * q);
+    if (c < cols) {
+      float wv[8], o[8];
+      load8<F>(w, c, wv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = v[q][e] * rs * wv[e];
+      store8<F>(y, base + c, o);
+    }
+  }
+}
+
 // e = ExpLp(x - rowmax); y = e * Recip(Sum(e)).  Rows of at most
 // 8 * RT * NCH columns (cols % 8 == 0, 16-byte aligned): the row is read
 // once into registers (NCH 16-byte chunks per thread) and each e is taken
@@ -356,6 +399,51 @@ __global__ __launch_bounds__(256) void permute_rope_kernel(const void *x, void *
   }
 }
 
+// The same re-layout with one wave per (token, group of 64 / CPH heads),
+// CPH = head_dim / 16 chunks of 8 frequencies per head: lane hh * CPH + c
+// rotates chunk c of head hh of the group.  Every lane takes the cos / sin
+// of one angle (frequency 8 c + hh % 8) and the 8 angles of its chunk come
+// from the lanes of the same c through shuffles, so each angle is computed
+// once per token and head group rather than per head and chunk.  A wave
+// reads whole 64 / CPH-head spans of one token row and writes whole rows of
+// each head.  head_dim 16 .. 128, a multiple of 16.
+template <uint32_t F>
+__global__ __launch_bounds__(256) void permute_rope_lanes_kernel(const void *x, void *y, int64_t tokens,
+                                                                 int64_t heads, int64_t head_dim, int64_t ts,
+                                                                 const int32_t *__restrict__ positions,
+                                                                 float theta) {
+  const int cph = (int)(head_dim / 16), hpw = 64 / cph;  // chunks per head, heads per wave
+  const int64_t groups = (heads + hpw - 1) / hpw;
+  const int64_t waves = tokens * groups;
+  const int lane = threadIdx.x & 63;
+  const int c = lane % cph, hh = lane / cph;
+  const int64_t half = head_dim / 2, i0 = 8 * c;
+  const int64_t wstride = (int64_t)gridDim.x * (blockDim.x / 64);
+  for (int64_t w = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); w < waves; w += wstride) {
+    const int64_t t = w / groups, h = (w % groups) * hpw + hh;
+    const float pos = (float)positions[t];
+    const float angle = pos * rope_inv_freq(theta, i0 + (hh & 7), head_dim);
+    const float mc = cosf(angle), ms = sinf(angle);
+    float cs[8], sn[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {  // every lane takes part, also past the last head
+      cs[k] = __shfl(mc, k * cph + c);
+      sn[k] = __shfl(ms, k * cph + c);
+    }
+    if (h < heads) {
+      const int64_t src = t * ts + h * head_dim + i0;
+      const int64_t dst = (h * tokens + t) * head_dim + i0;
+      float xl[8], xh[8], yl[8], yh[8];
+      load8<F>(x, src, xl);
+      load8<F>(x, src + half, xh);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) rope_rot(xl[k], xh[k], cs[k], sn[k], yl[k], yh[k]);
+      store8<F>(y, dst, yl);
+      store8<F>(y, dst + half, yh);
+    }
+  }
+}
+
 // VEC: 8 columns per thread (cols % 8 == 0, tensors 16-byte aligned)
 template <uint32_t F, bool VEC>
 __global__ __launch_bounds__(256) void bias_add_kernel(const void *__restrict__ x,
@@ -382,6 +470,19 @@ __global__ __launch_bounds__(256) void bias_add_kernel(const void *__restrict__ 
 
 unsigned grid_for(uint64_t count) {
   return (unsigned)std::min<uint64_t>((count + 255) / 256, 65536);
+}
+
+template <uint32_t F>
+void launch_rmsnorm_wave(hipStream_t st, int nch, dim3 grid, const void *x, const void *w, void *y, int64_t rows,
+                         int64_t cols, float inv_n, float eps) {
+  if (nch == 1)
+    hipLaunchKernelGGL((rmsnorm_wave_kernel<F, 1>), grid, dim3(256), 0, st, x, w, y, rows, cols, inv_n, eps);
+  else if (nch == 2)
+    hipLaunchKernelGGL((rmsnorm_wave_kernel<F, 2>), grid, dim3(256), 0, st, x, w, y, rows, cols, inv_n, eps);
+  else if (nch == 4)
+    hipLaunchKernelGGL((rmsnorm_wave_kernel<F, 4>), grid, dim3(256), 0, st, x, w, y, rows, cols, inv_n, eps);
+  else
+    hipLaunchKernelGGL((rmsnorm_wave_kernel<F, 8>), grid, dim3(256), 0, st, x, w, y, rows, cols, inv_n, eps);
 }
 
 #define DISPATCH_F(format, KERNEL, GRID, BLOCK, ...)                                           \
@@ -434,6 +535,18 @@ extern "C" int wafer_hip_rmsnorm(wafer_hip_context *ctx, uint32_t format, const 
   if (rows > 0x7fffffffull) return fail(WAFER_HIP_E_INVALID_FIELD, "rmsnorm: too many rows");
   const float inv_n = 1.0f / (float)cols;
   const bool vec = cols % 8 == 0 && aligned16(x) && aligned16(w) && aligned16(y);
+  if (vec && cols <= 4096) {
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    const int64_t r = (int64_t)rows, c = (int64_t)cols;
+    const int nch = cols <= 512 ? 1 : cols <= 1024 ? 2 : cols <= 2048 ? 4 : 8;
+    if (format == WAFER_FMT_F32)
+      launch_rmsnorm_wave<WAFER_FMT_F32>(ctx->stream, nch, grid, x, w, y, r, c, inv_n, eps);
+    else if (format == WAFER_FMT_BF16)
+      launch_rmsnorm_wave<WAFER_FMT_BF16>(ctx->stream, nch, grid, x, w, y, r, c, inv_n, eps);
+    else
+      launch_rmsnorm_wave<WAFER_FMT_F16>(ctx->stream, nch, grid, x, w, y, r, c, inv_n, eps);
+    return launch_status("rmsnorm_wave_kernel");
+  }
   DISPATCH_FB(format, vec, rmsnorm_kernel, dim3((unsigned)rows), dim3(RT), x, w, y, (int64_t)cols, inv_n, eps);
   return launch_status("rmsnorm_kernel");
 }
@@ -527,9 +640,24 @@ extern "C" int wafer_hip_head_permute_rope(wafer_hip_context *ctx, uint32_t form
     return fail(WAFER_HIP_E_INVALID_FIELD, "head_permute_rope: token_stride < heads * head_dim");
   if (!aligned16(src) || !aligned16(dst))
     return fail(WAFER_HIP_E_INVALID_FIELD, "head_permute_rope: tensors must be 16-byte aligned");
-  // the largest head group (8, 4, 2, 1) that keeps the grid at 32768
-  // threads or more: the cos/sin work shrinks with the group, the memory
-  // parallelism with the thread count
+  if (head_dim <= 128) {  // one wave per (token, head group); the loop keeps the grid bounded
+    const uint64_t waves = tokens * ((heads + 64 / (head_dim / 16) - 1) / (64 / (head_dim / 16)));
+    const dim3 grid((unsigned)std::min<uint64_t>((waves + 3) / 4, 65536));
+    const int64_t a0 = (int64_t)tokens, a1 = (int64_t)heads, a2 = (int64_t)head_dim, a3 = (int64_t)token_stride;
+    if (format == WAFER_FMT_F32)
+      hipLaunchKernelGGL(permute_rope_lanes_kernel<WAFER_FMT_F32>, grid, dim3(256), 0, ctx->stream, src, dst, a0, a1,
+                         a2, a3, positions, theta);
+    else if (format == WAFER_FMT_BF16)
+      hipLaunchKernelGGL(permute_rope_lanes_kernel<WAFER_FMT_BF16>, grid, dim3(256), 0, ctx->stream, src, dst, a0,
+                         a1, a2, a3, positions, theta);
+    else
+      hipLaunchKernelGGL(permute_rope_lanes_kernel<WAFER_FMT_F16>, grid, dim3(256), 0, ctx->stream, src, dst, a0, a1,
+                         a2, a3, positions, theta);
+    return launch_status("permute_rope_lanes_kernel");
+  }
+  // head_dim above 128: the largest head group (8, 4, 2, 1) that keeps the
+  // grid at 32768 threads or more: the cos/sin work shrinks with the group,
+  // the memory parallelism with the thread count
   const uint64_t rows = tokens * (head_dim / 16);
   int hg = 8;
   while (hg > 1 && rows * ((heads + hg - 1) / hg) < 32768) hg /= 2;
