@@ -381,6 +381,15 @@ int wafer_hip_attention_decode_noalloc(wafer_hip_context *ctx, uint32_t format,
 int wafer_hip_rmsnorm(wafer_hip_context *ctx, uint32_t format, const void *x,
                       const void *w, void *y, uint64_t rows, uint64_t cols,
                       float eps);
+/* The residual Add command followed by the RMSNorm region, in one pass:
+ * sum = x + r (CT Add, ManagedReferenceTargetModel.cpp:230-299, narrowed to
+ * `format`) and y = rmsnorm(sum, w) as wafer_hip_rmsnorm computes it from the
+ * stored sum; both outputs equal the two separate commands'.  No reference
+ * counterpart as one command (the decoder block's x1 = x + attn; h2 =
+ * RMSNorm(x1) pair).  sum and y must be distinct buffers. */
+int wafer_hip_add_rmsnorm(wafer_hip_context *ctx, uint32_t format, const void *x,
+                          const void *r, const void *w, void *sum, void *y,
+                          uint64_t rows, uint64_t cols, float eps);
 /* e = ExpLp(x - rowmax); y = e * Recip(Sum(e)). */
 int wafer_hip_softmax(wafer_hip_context *ctx, uint32_t format, const void *x,
                       void *y, uint64_t rows, uint64_t cols);

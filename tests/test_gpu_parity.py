@@ -812,13 +812,15 @@ def test_softmax_shapes(hip, B, oracle, rows, cols, fmt):
                    oracle.to_float(fmt, oracle.softmax(xb, fmt=fmt)).reshape(x.shape), what="softmax")
 
 
-@pytest.mark.parametrize("rows,cols", [(1, 8), (67, 520), (5, 1024), (33, 2056), (1024, 4096), (3, 4104), (9, 33)])
+@pytest.mark.parametrize("rows,cols", [(1, 8), (67, 520), (1024, 4096), (3, 4104), (9, 33), (4096, 8), (4097, 520),
+                                       (4099, 1024), (4098, 2056), (4096, 4096)])
 @pytest.mark.parametrize("fmt", [3, 5, 2])
 def test_rmsnorm_shapes(hip, B, oracle, rows, cols, fmt):
-    """The wave-per-row RMSNorm at 1, 2, 4 and 8 chunks per lane (cols a
-    multiple of 8 up to 4096, partial last chunks, row counts that leave a
-    workgroup's last waves idle), the workgroup kernel beyond (4104) and
-    the scalar kernel (33); all three float formats against the oracle."""
+    """The workgroup RMSNorm below 4096 rows and beyond 4096 columns, the
+    scalar kernel (33 columns), and from 4096 rows the wave-per-row kernel at
+    1, 2, 4 and 8 chunks per lane (partial last chunks, row counts that leave
+    a workgroup's last waves idle); all three float formats against the
+    oracle."""
     say("rmsnorm", rows, cols, fmt)
     rng = np.random.default_rng(rows * cols + fmt)
     x = (rng.standard_normal((rows, cols)) * 2).astype(np.float32)
@@ -836,6 +838,31 @@ def test_rmsnorm_shapes(hip, B, oracle, rows, cols, fmt):
     hip.rmsnorm(u16(xb), u16(wb), y, 1e-5, fmt=fmt)
     attention_gate(oracle.to_float(fmt, from_u16(y)).reshape(x.shape),
                    oracle.to_float(fmt, oracle.rmsnorm(xb, wb, 1e-5, fmt=fmt)).reshape(x.shape), what="rmsnorm")
+
+
+@pytest.mark.parametrize("rows,cols", [(1024, 4096), (67, 520), (5, 2056), (3, 4104), (9, 33), (4097, 520),
+                                       (4096, 4096)])
+@pytest.mark.parametrize("fmt", [3, 5, 2])
+def test_add_rmsnorm_equals_add_then_rmsnorm(hip, B, rows, cols, fmt):
+    """The fused residual Add + RMSNorm gives the bits of the Add command
+    followed by the RMSNorm region, for both outputs: the workgroup kernel
+    (below 4096 rows or above 4096 columns), the wave-per-row kernel (from
+    4096 rows), and the two-launch path for columns not a multiple of 8."""
+    say("add_rmsnorm", rows, cols, fmt)
+    dt = {3: torch.bfloat16, 5: torch.float32, 2: torch.float16}[fmt]
+    iv = torch.int32 if fmt == 5 else torch.int16
+    gen = torch.Generator(device="cuda").manual_seed(rows * 7 + cols + fmt)
+    x = torch.randn(rows, cols, generator=gen, device="cuda").to(dt)
+    r = (0.5 * torch.randn(rows, cols, generator=gen, device="cuda")).to(dt)
+    w = (1 + 0.1 * torch.randn(cols, generator=gen, device="cuda")).to(dt)
+    s_ref, y_ref = torch.empty_like(x), torch.empty_like(x)
+    hip.elementwise(B.EW["Add"], fmt, x, s_ref, r)
+    hip.rmsnorm(s_ref, w, y_ref, 1e-5, fmt=fmt)
+    s, y = torch.full_like(x, 3.0), torch.full_like(x, 3.0)
+    hip.add_rmsnorm(x, r, w, s, y, 1e-5, fmt=fmt)
+    torch.cuda.synchronize()
+    assert torch.equal(s.view(iv), s_ref.view(iv))
+    assert torch.equal(y.view(iv), y_ref.view(iv))
 
 
 @pytest.mark.parametrize("T,H,D", [(300, 1, 128), (64, 32, 128), (129, 5, 16), (77, 3, 64), (10, 2, 6)])

@@ -48,7 +48,7 @@ EXPORTS = (
     "wafer_hip_strided_copy", "wafer_hip_memset", "wafer_hip_bit2fp", "wafer_hip_mask_move",
     "wafer_hip_compare_expected", "wafer_hip_compare_statistics", "wafer_hip_environment",
     "wafer_hip_first_nan", "wafer_hip_attention_decode_noalloc", "wafer_hip_attention_prefill_masked",
-    "wafer_hip_elementwise_formal", "wafer_hip_pool",
+    "wafer_hip_elementwise_formal", "wafer_hip_pool", "wafer_hip_add_rmsnorm",
 )
 
 # wafer_hip_attention_mask flags
@@ -158,6 +158,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wafer_hip_attention_decode_noalloc.argtypes = [vp, u32, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32, u32]
     L.wafer_hip_rmsnorm.argtypes = [vp, u32, vp, vp, vp, u64, u64, f32]
     L.wafer_hip_softmax.argtypes = [vp, u32, vp, vp, u64, u64]
+    L.wafer_hip_add_rmsnorm.argtypes = [vp, u32, vp, vp, vp, vp, vp, u64, u64, f32]
     L.wafer_hip_silu_mul.argtypes = [vp, u32, vp, vp, vp, u64]
     L.wafer_hip_gelu_tanh.argtypes = [vp, u32, vp, vp, u64]
     L.wafer_hip_rope.argtypes = [vp, u32, vp, vp, u64, u64, u64, vp, f32]
@@ -503,6 +504,15 @@ class Context:
         _arg("rmsnorm", "y", y, fmt, x.numel())
         _check(self._L.wafer_hip_rmsnorm(self._bind(), fmt, _p(x), _p(w), _p(y), x.numel() // cols, cols,
                                          float(eps)))
+
+    def add_rmsnorm(self, x, r, w, s, y, eps, fmt=BF16):
+        """s = x + r (the Add command) and y = rmsnorm(s, w) in one pass."""
+        cols = x.shape[-1]
+        n = x.numel()
+        for name, t, cnt in (("x", x, n), ("r", r, n), ("w", w, cols), ("s", s, n), ("y", y, n)):
+            _arg("add_rmsnorm", name, t, fmt, cnt)
+        _check(self._L.wafer_hip_add_rmsnorm(self._bind(), fmt, _p(x), _p(r), _p(w), _p(s), _p(y), n // cols, cols,
+                                             float(eps)))
 
     def softmax(self, x, y, fmt=BF16):
         cols = x.shape[-1]

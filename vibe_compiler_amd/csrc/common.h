@@ -205,6 +205,13 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // Eight consecutive elements from element index i (a multiple of 8) with
 // 16-byte accesses: one for 16-bit formats, two for F32.  The caller checks
 // 16-byte alignment of the base.
+// v rounded to the storage format F and widened back (what a store then a
+// load of v gives)
+template <uint32_t F> __device__ inline float round_to(float v) {
+  if constexpr (F == WAFER_FMT_BF16) return bf16_to_f32(f32_to_bf16(v));
+  else if constexpr (F == WAFER_FMT_F16) return f16_to_f32(f32_to_f16(v));
+  else return v;
+}
 template <uint32_t F> __device__ inline void load8(const void *b, int64_t i, float (&v)[8]) {
   if constexpr (F == WAFER_FMT_F32) {
     const u32x4 lo = ((const u32x4 *)b)[i / 4], hi = ((const u32x4 *)b)[i / 4 + 1];

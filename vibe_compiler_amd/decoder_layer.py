@@ -9,8 +9,8 @@ backend, each one a C-ABI call of ``libwafer_hip.so`` on the caller's stream:
     v    -> head-major       [Hkv, T, D]              wafer_hip_head_permute
     o    = causal GQA attention(q, k, v)              wafer_hip_attention_prefill (FA)
     a    = o -> token-major  [T, Hq D]                wafer_hip_head_permute
-    x1   = x + a . Wo^T                               wafer_hip_gemm_mfma, wafer_hip_elementwise(Add)
-    h2   = RMSNorm(x1) * w_post
+    x1   = x + a . Wo^T                               wafer_hip_gemm_mfma, wafer_hip_add_rmsnorm (Add
+    h2   = RMSNorm(x1) * w_post                         and the norm in one pass)
     act  = silu(h2 . Wg^T) * (h2 . Wu^T)              wafer_hip_gemm_mfma_swiglu
     y    = x1 + act . Wd^T                            wafer_hip_gemm_mfma, Add
 
@@ -107,8 +107,7 @@ class DecoderLayer:
                               self.o.view(1, Hq, T, D), 1.0 / math.sqrt(D), causal=True)
         hip.head_permute(self.o, self.attn, T, Hq, D, Hd, 1)
         hip.gemm_mfma(self.attn, self.wo, self.proj, T, Hd, Hd, out_fmt=B.BF16, rhs_t=True)
-        hip.elementwise(ADD, B.BF16, x, self.x1, self.proj)
-        hip.rmsnorm(self.x1, self.w_post, self.h, self.eps)
+        hip.add_rmsnorm(x, self.proj, self.w_post, self.x1, self.h, self.eps)
         hip.gemm_mfma_swiglu(self.h, self.wgu, self.act, T, Hd, F)
         hip.gemm_mfma(self.act, self.wd, self.down, T, F, Hd, out_fmt=B.BF16, rhs_t=True)
         hip.elementwise(ADD, B.BF16, self.x1, y, self.down)
