@@ -263,13 +263,11 @@ def test_reference_pool_windows(hip, width, kind):
     assert (got.view(np.uint32) == want.view(np.uint32)).all()
 
 
-@pytest.mark.parametrize("fmt", FLOATS)
-@pytest.mark.parametrize("kind", (117, 119, 116))
+# Sum pooling is F32-only (the other formats are refused: test_pool_rejections)
+@pytest.mark.parametrize("fmt,kind", [(f, k) for f in FLOATS for k in (117, 119)] + [(F32, 116)])
 @pytest.mark.parametrize("geom", ((2, 17, 23, 5, 3, 2, 2, 3), (1, 9, 9, 64, 3, 3, 1, 1), (3, 6, 40, 2, 1, 1, 3, 2),
                                   (1, 64, 64, 16, 2, 2, 2, 2)))
 def test_pool_random(hip, oracle, fmt, kind, geom):
-    if kind == 116 and fmt != F32:
-        pytest.skip("Sum pooling is F32-only (unsupported otherwise, covered by test_pool_rejections)")
     n, h, w, c, kw, kh, sw, sh = geom
     say("pool random", fmt, kind, geom)
     rng = np.random.default_rng(sum(geom) + kind + fmt)
