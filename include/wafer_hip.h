@@ -293,6 +293,25 @@ int wafer_hip_attention_prefill(wafer_hip_context *ctx, uint32_t format,
                                 uint32_t kv_heads, uint32_t q_len,
                                 uint32_t kv_len, uint32_t head_dim,
                                 float scale, uint32_t causal);
+/* The same FA prefill on tensors addressed by element strides (batch, head,
+ * row) for each of Q, K, V and O, so a caller can pass head slices of a
+ * token-major projection ([T, heads * 128] rows) and receive a token-major
+ * output without re-layout steps.  Same kernel walk, so the bits equal
+ * wafer_hip_attention_prefill on the densely re-laid-out tensors.  BF16,
+ * head_dim 128; strides non-negative multiples of 8, row strides >= 128,
+ * 16-byte aligned tensors.  Additive (the reference's attention op has no
+ * layout operands); a decoder block's V and O re-layouts are what it removes. */
+typedef struct wafer_hip_attention_strides {
+  int64_t q[3], k[3], v[3], o[3]; /* elements: batch, head, row */
+} wafer_hip_attention_strides;
+int wafer_hip_attention_prefill_strided(wafer_hip_context *ctx, uint32_t format,
+                                        const void *q, const void *k,
+                                        const void *v, void *o, uint32_t batch,
+                                        uint32_t q_heads, uint32_t kv_heads,
+                                        uint32_t q_len, uint32_t kv_len,
+                                        uint32_t head_dim, float scale,
+                                        uint32_t causal,
+                                        const wafer_hip_attention_strides *strides);
 
 /* FA prefill with the attention op's optional mask operand, its graph-defined
  * score region and its position bias (include/Wafer/IR/LinalgExt/AttentionOps.td:42-64;

@@ -323,3 +323,45 @@ def test_fd_decode_storage_formats(hip, oracle, fmt, Bn, Hq, Hkv, L, cap, chunks
     o2 = torch.full((Bn, Hq, 1, D), 0x7E00, dtype=torch.int16, device="cuda")
     hip.attention_decode_noalloc(u16(q), u16(k), u16(v), o2, scale, chunks=chunks, kv_len=L, fmt=fmt)
     assert np.array_equal(back(o2), got)
+
+
+# ---------------------------------------------------------------- strided FA
+@pytest.mark.parametrize("Bn,Hq,Hkv,S,causal", [(1, 32, 8, 1024, True), (2, 4, 2, 300, True), (1, 2, 1, 130, False)])
+def test_strided_prefill_equals_dense(hip, B, Bn, Hq, Hkv, S, causal):
+    """wafer_hip_attention_prefill_strided on head slices of token-major
+    projection rows (Q, K, V inside one [B, S, (Hq + 2 Hkv) 128] buffer, O
+    written into token-major [B, S, Hq 128] rows) gives the bits of the dense
+    entry on the re-laid-out tensors (same kernel walk)."""
+    say("strided prefill", Bn, Hq, Hkv, S, causal)
+    D = 128
+    gen = torch.Generator(device="cuda").manual_seed(Bn * 1000 + Hq * 10 + S)
+    n = (Hq + 2 * Hkv) * D
+    qkv = torch.randn(Bn, S, n, generator=gen, device="cuda").to(torch.bfloat16)
+    qv = qkv[:, :, :Hq * D].view(Bn, S, Hq, D).permute(0, 2, 1, 3)
+    kv_ = qkv[:, :, Hq * D:(Hq + Hkv) * D].view(Bn, S, Hkv, D).permute(0, 2, 1, 3)
+    vv = qkv[:, :, (Hq + Hkv) * D:].view(Bn, S, Hkv, D).permute(0, 2, 1, 3)
+    out = torch.full((Bn, S, Hq * D + 8), 5.0, dtype=torch.bfloat16, device="cuda")  # padded rows
+    ov = out[:, :, :Hq * D].view(Bn, S, Hq, D).permute(0, 2, 1, 3)
+    scale = 1 / math.sqrt(D)
+    hip.attention_prefill_strided(qv, kv_, vv, ov, scale, causal=causal)
+    od = torch.empty(Bn, Hq, S, D, dtype=torch.bfloat16, device="cuda")
+    hip.attention_prefill(qv.contiguous(), kv_.contiguous(), vv.contiguous(), od, scale, causal=causal)
+    torch.cuda.synchronize()
+    assert torch.equal(ov.contiguous().view(torch.int16), od.view(torch.int16))
+    assert torch.all(out[:, :, Hq * D:] == 5.0)  # the row padding is untouched
+
+
+def test_strided_prefill_rejections(hip, B):
+    say("strided prefill rejections")
+    D = 128
+    q = torch.zeros(1, 2, 64, D, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(B.WaferHipError) as e:  # F16 storage: not served by this entry
+        hip.attention_prefill_strided(q, q, q, q.clone(), 0.1, fmt=B.F16)
+    assert e.value.status == -3
+    big = torch.zeros(64, 2 * D + 4, dtype=torch.bfloat16, device="cuda")  # row stride 260: not a multiple of 8
+    v = big[:, :2 * D].view(64, 2, D).permute(1, 0, 2)[None]
+    with pytest.raises(B.WaferHipError) as e:
+        hip.attention_prefill_strided(q, q, v, q.clone(), 0.1)
+    assert e.value.status == -1
+    with pytest.raises(ValueError):  # head_dim must have unit stride
+        hip.attention_prefill_strided(q, q, q.transpose(2, 3), q.clone(), 0.1)

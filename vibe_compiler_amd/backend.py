@@ -48,7 +48,7 @@ EXPORTS = (
     "wafer_hip_strided_copy", "wafer_hip_memset", "wafer_hip_bit2fp", "wafer_hip_mask_move",
     "wafer_hip_compare_expected", "wafer_hip_compare_statistics", "wafer_hip_environment",
     "wafer_hip_first_nan", "wafer_hip_attention_decode_noalloc", "wafer_hip_attention_prefill_masked",
-    "wafer_hip_elementwise_formal", "wafer_hip_pool", "wafer_hip_add_rmsnorm",
+    "wafer_hip_elementwise_formal", "wafer_hip_pool", "wafer_hip_add_rmsnorm", "wafer_hip_attention_prefill_strided",
 )
 
 # wafer_hip_attention_mask flags
@@ -60,6 +60,13 @@ class AttentionMask(ctypes.Structure):
     _fields_ = [("flags", ctypes.c_uint32), ("kv_capacity", ctypes.c_uint32), ("causal_diagonal", ctypes.c_int64),
                 ("window", ctypes.c_int64), ("bias", ctypes.c_void_p), ("bias_strides", ctypes.c_int64 * 3),
                 ("keep", ctypes.c_void_p), ("keep_strides", ctypes.c_int64 * 3)]
+
+class AttentionStrides(ctypes.Structure):
+    """wafer_hip_attention_strides (include/wafer_hip.h): element strides
+    (batch, head, row) of q, k, v and o."""
+    _fields_ = [("q", ctypes.c_int64 * 3), ("k", ctypes.c_int64 * 3), ("v", ctypes.c_int64 * 3),
+                ("o", ctypes.c_int64 * 3)]
+
 
 class ElementwiseCommand(ctypes.Structure):
     """wafer_hip_elementwise_command (include/wafer_hip.h)."""
@@ -155,6 +162,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wafer_hip_attention_decode.argtypes = [vp, u32, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32, u32]
     L.wafer_hip_attention_prefill_masked.argtypes = [vp, u32, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32,
                                                      ctypes.POINTER(AttentionMask)]
+    L.wafer_hip_attention_prefill_strided.argtypes = [vp, u32, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32, u32,
+                                                      ctypes.POINTER(AttentionStrides)]
     L.wafer_hip_attention_decode_noalloc.argtypes = [vp, u32, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32, u32]
     L.wafer_hip_rmsnorm.argtypes = [vp, u32, vp, vp, vp, u64, u64, f32]
     L.wafer_hip_softmax.argtypes = [vp, u32, vp, vp, u64, u64]
@@ -422,6 +431,33 @@ class Context:
             _arg("attention_prefill", name, t, fmt, n)
         _check(self._L.wafer_hip_attention_prefill(self._bind(), fmt, _p(q), _p(k), _p(v), _p(o), B, Hq,
                                                    Hkv, Sq, Skv, D, float(scale), int(causal)))
+
+    def attention_prefill_strided(self, q, k, v, o, scale, causal=True, fmt=BF16):
+        """FA prefill on 4-D [batch, heads, len, head_dim] views with any
+        element strides (unit stride along head_dim), e.g. head slices of a
+        token-major projection; o may be such a view too."""
+        W = "attention_prefill_strided"
+        for name, t in (("q", q), ("k", k), ("v", v), ("o", o)):
+            if t.dim() != 4 or t.stride(3) != 1:
+                raise ValueError(f"{W}: {name} must be a 4-D view with unit stride along head_dim")
+            if str(t.dtype) != "torch.bfloat16" and t.element_size() != 2:
+                raise ValueError(f"{W}: {name} must hold 16-bit elements")
+            if not t.is_cuda:
+                raise ValueError(f"{W}: {name} must live on the GPU")
+            # every element the strides reach lies inside the tensor's storage
+            last = t.storage_offset() + sum((n - 1) * st for n, st in zip(t.shape, t.stride()))
+            if t.numel() and (last + 1) * t.element_size() > t.untyped_storage().nbytes():
+                raise ValueError(f"{W}: {name} reaches past its storage")
+        B, Hq, Sq, D = q.shape
+        _, Hkv, Skv, _ = k.shape
+        if tuple(v.shape) != tuple(k.shape) or k.shape[0] != B or k.shape[3] != D or tuple(o.shape) != tuple(q.shape):
+            raise ValueError(f"{W}: k, v [batch, kv_heads, kv_len, head_dim] and o shaped like q")
+        st = AttentionStrides((ctypes.c_int64 * 3)(*q.stride()[:3]), (ctypes.c_int64 * 3)(*k.stride()[:3]),
+                              (ctypes.c_int64 * 3)(*v.stride()[:3]), (ctypes.c_int64 * 3)(*o.stride()[:3]))
+        ptr = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        _check(self._L.wafer_hip_attention_prefill_strided(self._bind(), fmt, ptr(q), ptr(k), ptr(v), ptr(o), B, Hq,
+                                                           Hkv, Sq, Skv, D, float(scale), int(causal),
+                                                           ctypes.byref(st)))
 
     def attention_prefill_masked(self, q, k, v, o, scale, *, kv_len=None, causal=False, diagonal=0, window=0,
                                  bias=None, keep=None, round_scaled=False, round_biased=False, fmt=BF16):

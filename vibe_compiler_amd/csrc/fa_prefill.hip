@@ -101,11 +101,17 @@ __device__ inline float xor16_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <bool CAUSAL>
+// Element strides (batch, head, row) of Q, K, V and O for the STRIDED
+// instantiation; the other reads the dense [B, H, S, 128] layout.
+struct FaStrides {
+  int64_t q[3], k[3], v[3], o[3];
+};
+
+template <bool CAUSAL, bool STRIDED = false>
 __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, uint16_t *__restrict__ O, int q_heads, int kv_heads,
-    int q_len, int kv_len, float c, int bh_count, int n_qblocks) {
+    int q_len, int kv_len, float c, int bh_count, int n_qblocks, const FaStrides st = FaStrides{}) {
   // two stages of [K half 0 | K half 1 | V half 0 | V half 1], 16 KiB each:
   // rows of 256 bytes (64 keys x 128 d), 16-byte chunk ch of row r stored at
   // chunk position ch ^ swz(r)
@@ -117,9 +123,11 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
   const int b = bh / q_heads;
   const int h = bh - b * q_heads;
   const int kvh = h / (q_heads / kv_heads);
-  const uint16_t *Qp = Q + ((size_t)bh * q_len) * D;
-  const uint16_t *Kp = K + ((size_t)(b * kv_heads + kvh) * kv_len) * D;
-  const uint16_t *Vp = V + ((size_t)(b * kv_heads + kvh) * kv_len) * D;
+  const uint16_t *Qp = STRIDED ? Q + b * st.q[0] + h * st.q[1] : Q + ((size_t)bh * q_len) * D;
+  const uint16_t *Kp = STRIDED ? K + b * st.k[0] + kvh * st.k[1] : K + ((size_t)(b * kv_heads + kvh) * kv_len) * D;
+  const uint16_t *Vp = STRIDED ? V + b * st.v[0] + kvh * st.v[1] : V + ((size_t)(b * kv_heads + kvh) * kv_len) * D;
+  // row strides in elements (D in the dense layout)
+  const int64_t q_rs = STRIDED ? st.q[2] : D, k_rs = STRIDED ? st.k[2] : D, v_rs = STRIDED ? st.v[2] : D;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -144,7 +152,7 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     const int row = min(q0 + l16, q_len - 1);
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      qreg[s] = *(const bf16x8 *)(Qp + (size_t)row * D + s * 32 + g * 8);
+      qreg[s] = *(const bf16x8 *)(Qp + (size_t)row * q_rs + s * 32 + g * 8);
   };
   load_q();
 
@@ -158,14 +166,19 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
   // One buffer resource per block, based at the block and sized to its rows
   // (the hardware range check covers the lane offset, not the scalar one), so
   // rows of a partial last block past kv_len read as zero.
-  auto block_rsrc = [&](const uint16_t *base, int kb) __attribute__((always_inline)) {
+  auto block_rsrc = [&](const uint16_t *base, int64_t rs, int kb) __attribute__((always_inline)) {
     const int rows = min(BK, kv_len - kb * BK);
-    return __builtin_amdgcn_make_buffer_rsrc((void *)(base + (size_t)kb * BK * D), 0, rows * D * 2, 0x00020000);
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(base + (size_t)kb * BK * rs), 0,
+                                             (int)(((int64_t)(rows - 1) * rs + D) * 2), 0x00020000);
   };
-  uint32_t dma_off[4];
+  uint32_t dma_off_k[4], dma_off_v[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    dma_off[j] = (uint32_t)((16 * qt + 4 * j + (lane >> 4)) * 256 + (((lane & 15) ^ (8 * (j & 1) + 2 * (lane >> 4))) << 4));
+  for (int j = 0; j < 4; ++j) {
+    const int row = 16 * qt + 4 * j + (lane >> 4);
+    const uint32_t chunk = (uint32_t)(((lane & 15) ^ (8 * (j & 1) + 2 * (lane >> 4))) << 4);
+    dma_off_k[j] = (uint32_t)(row * k_rs * 2) + chunk;
+    dma_off_v[j] = (uint32_t)(row * v_rs * 2) + chunk;
+  }
   // key block of iteration t for this half (t clamped to the last iteration,
   // the block to the phase's last block: loads past the end are harmless)
   auto block_of = [&](int t) __attribute__((always_inline)) {
@@ -173,20 +186,20 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     return t < ta ? min(2 * t + half, nk_a - 1) : min(2 * (t - ta) + half, nk_b - 1);
   };
   auto dma_k = [&](int kb, int buf) __attribute__((always_inline)) {
-    const __amdgpu_buffer_rsrc_t rsrc = block_rsrc(Kp, __builtin_amdgcn_readfirstlane(kb));
+    const __amdgpu_buffer_rsrc_t rsrc = block_rsrc(Kp, k_rs, __builtin_amdgcn_readfirstlane(kb));
     uint16_t *dk = sbuf[buf][half] + qt * 4 * 512;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)(dk + j * 512), 16,
-                                               dma_off[j], 0, 0, 0);
+                                               dma_off_k[j], 0, 0, 0);
   };
   auto dma_v = [&](int kb, int buf) __attribute__((always_inline)) {
-    const __amdgpu_buffer_rsrc_t rsrc = block_rsrc(Vp, __builtin_amdgcn_readfirstlane(kb));
+    const __amdgpu_buffer_rsrc_t rsrc = block_rsrc(Vp, v_rs, __builtin_amdgcn_readfirstlane(kb));
     uint16_t *dv = sbuf[buf][2 + half] + qt * 4 * 512;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)(dv + j * 512), 16,
-                                               dma_off[j], 0, 0, 0);
+                                               dma_off_v[j], 0, 0, 0);
   };
 
   // LDS read offsets (bytes within a 16 KiB block), per lane:
@@ -351,7 +364,8 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     const float l = xor16_sum(xor32_sum(l_part * s0 + l1 * s1));
     // finalize: coefficient = Recip(l) (0 for an empty row), out = bf16(acc * coef)
     const float coef = (l == 0.0f) ? 0.0f : 1.0f / l;
-    uint16_t *orow = O + ((size_t)bh * q_len + q0 + l16) * D + 4 * g;
+    uint16_t *orow = (STRIDED ? O + b * st.o[0] + h * st.o[1] + (int64_t)(q0 + l16) * st.o[2]
+                              : O + ((size_t)bh * q_len + q0 + l16) * D) + 4 * g;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int dt = 4 * H + i;
@@ -465,5 +479,57 @@ extern "C" int wafer_hip_attention_prefill(wafer_hip_context *ctx, uint32_t form
     hipLaunchKernelGGL(fa_prefill_bf16_d128<false>, grid, dim3(THREADS), 0, ctx->stream,
                        (const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)v, (uint16_t *)o,
                        (int)q_heads, (int)kv_heads, (int)q_len, (int)kv_len, c, bh_count, n_qblocks);
+  return launch_status("fa_prefill_bf16_d128");
+}
+
+extern "C" int wafer_hip_attention_prefill_strided(wafer_hip_context *ctx, uint32_t format, const void *q,
+                                                   const void *k, const void *v, void *o, uint32_t batch,
+                                                   uint32_t q_heads, uint32_t kv_heads, uint32_t q_len,
+                                                   uint32_t kv_len, uint32_t head_dim, float scale,
+                                                   uint32_t causal, const wafer_hip_attention_strides *strides) {
+  WAFER_CHECK_CTX(ctx);
+  if (format != WAFER_FMT_BF16 || head_dim != D)
+    return fail(WAFER_HIP_E_UNSUPPORTED, "attention_prefill_strided: BF16 with head_dim 128 only");
+  if (!q || !k || !v || !o || !strides) return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill_strided: null tensor");
+  if (batch == 0 || q_heads == 0 || kv_heads == 0 || q_len == 0 || kv_len == 0)
+    return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill_strided: empty dimension");
+  if (q_heads % kv_heads != 0)
+    return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill_strided: q_heads % kv_heads != 0");
+  if (!(scale > 0.0f)) return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill_strided: scale must be positive");
+  const int64_t *all[4] = {strides->q, strides->k, strides->v, strides->o};
+  for (const int64_t *t : all)
+    for (int i = 0; i < 3; ++i)
+      if (t[i] < 0 || t[i] % 8) return fail(WAFER_HIP_E_INVALID_FIELD,
+                                            "attention_prefill_strided: strides must be non-negative multiples of 8");
+  if (strides->q[2] < D || strides->k[2] < D || strides->v[2] < D || strides->o[2] < D)
+    return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill_strided: row strides below head_dim");
+  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) & 15)
+    return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill_strided: tensors must be 16-byte aligned");
+  // one key block's buffer range and the DMA lane offsets are 32-bit
+  if (((int64_t)(BK - 1) * std::max(strides->k[2], strides->v[2]) + D) * 2 > 0x7fffffffll)
+    return fail(WAFER_HIP_E_UNSUPPORTED, "attention_prefill_strided: key row stride too large");
+  const uint64_t n_qblocks64 = (q_len + QB - 1) / QB;
+  if ((uint64_t)batch * q_heads * ((n_qblocks64 + 1) / 2) > 0x7fffffffull)
+    return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill_strided: grid too large");
+  WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
+  FaStrides st{};
+  for (int i = 0; i < 3; ++i) {
+    st.q[i] = strides->q[i];
+    st.k[i] = strides->k[i];
+    st.v[i] = strides->v[i];
+    st.o[i] = strides->o[i];
+  }
+  const int n_qblocks = (int)n_qblocks64;
+  const int bh_count = (int)(batch * q_heads);
+  const float c = scale * 0x1.715476p+0f;
+  dim3 grid((unsigned)(bh_count * ((n_qblocks + 1) / 2)));
+  if (causal)
+    hipLaunchKernelGGL((fa_prefill_bf16_d128<true, true>), grid, dim3(THREADS), 0, ctx->stream, (const uint16_t *)q,
+                       (const uint16_t *)k, (const uint16_t *)v, (uint16_t *)o, (int)q_heads, (int)kv_heads,
+                       (int)q_len, (int)kv_len, c, bh_count, n_qblocks, st);
+  else
+    hipLaunchKernelGGL((fa_prefill_bf16_d128<false, true>), grid, dim3(THREADS), 0, ctx->stream, (const uint16_t *)q,
+                       (const uint16_t *)k, (const uint16_t *)v, (uint16_t *)o, (int)q_heads, (int)kv_heads,
+                       (int)q_len, (int)kv_len, c, bh_count, n_qblocks, st);
   return launch_status("fa_prefill_bf16_d128");
 }

@@ -6,9 +6,8 @@ backend, each one a C-ABI call of ``libwafer_hip.so`` on the caller's stream:
     h    = RMSNorm(x) * w_in                          wafer_hip_rmsnorm
     qkv  = h . Wqkv^T        [T, (Hq + 2 Hkv) D]      wafer_hip_gemm_mfma (bf16 MFMA)
     q,k  = RoPE(q), RoPE(k) -> head-major [H, T, D]  wafer_hip_head_permute_rope
-    v    -> head-major       [Hkv, T, D]              wafer_hip_head_permute
-    o    = causal GQA attention(q, k, v)              wafer_hip_attention_prefill (FA)
-    a    = o -> token-major  [T, Hq D]                wafer_hip_head_permute
+    a    = causal GQA attention(q, k, v)              wafer_hip_attention_prefill_strided (FA; V read
+                                                      from the QKV rows, a written token-major [T, Hq D])
     x1   = x + a . Wo^T                               wafer_hip_gemm_mfma, wafer_hip_add_rmsnorm (Add
     h2   = RMSNorm(x1) * w_post                         and the norm in one pass)
     act  = silu(h2 . Wg^T) * (h2 . Wu^T)              wafer_hip_gemm_mfma_swiglu
@@ -85,9 +84,10 @@ class DecoderLayer:
         # Hq + Hkv heads, which sit side by side in each QKV row
         self.qk = e(q_heads + kv_heads, T, head_dim)
         self.q, self.k = self.qk[:q_heads], self.qk[q_heads:]
-        self.v = e(kv_heads, T, head_dim)
-        self.o = e(q_heads, T, head_dim)
         self.attn = e(T, hidden)
+        # [1, heads, T, D] views: V inside the QKV rows, O inside the token-major attention rows
+        self.v_view = self.qkv[:, (q_heads + kv_heads) * head_dim:].view(T, kv_heads, head_dim).permute(1, 0, 2)[None]
+        self.attn_view = self.attn.view(T, q_heads, head_dim).permute(1, 0, 2)[None]
         self.proj = e(T, hidden)
         self.x1 = e(T, hidden)
         self.act = e(T, ffn)
@@ -102,10 +102,10 @@ class DecoderLayer:
         hip.rmsnorm(x, self.w_in, self.h, self.eps)
         hip.gemm_mfma(self.h, self.wqkv, self.qkv, T, Hd, qkv_n, out_fmt=B.BF16, rhs_t=True)
         hip.head_permute_rope(self.qkv, self.qk, T, Hq + Hkv, D, qkv_n, self.pos, self.theta)
-        hip.head_permute(self.qkv, self.v, T, Hkv, D, qkv_n, 0, src_offset=(Hq + Hkv) * D)
-        hip.attention_prefill(self.q.view(1, Hq, T, D), self.k.view(1, Hkv, T, D), self.v.view(1, Hkv, T, D),
-                              self.o.view(1, Hq, T, D), 1.0 / math.sqrt(D), causal=True)
-        hip.head_permute(self.o, self.attn, T, Hq, D, Hd, 1)
+        # V read in place from the QKV rows and O written token-major: head
+        # slices addressed by strides, no re-layout steps
+        hip.attention_prefill_strided(self.q.view(1, Hq, T, D), self.k.view(1, Hkv, T, D), self.v_view,
+                                      self.attn_view, 1.0 / math.sqrt(D), causal=True)
         hip.gemm_mfma(self.attn, self.wo, self.proj, T, Hd, Hd, out_fmt=B.BF16, rhs_t=True)
         hip.add_rmsnorm(x, self.proj, self.w_post, self.x1, self.h, self.eps)
         hip.gemm_mfma_swiglu(self.h, self.wgu, self.act, T, Hd, F)
