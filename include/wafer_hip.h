@@ -131,6 +131,17 @@ int wafer_hip_gemm_mfma(wafer_hip_context *ctx, const void *lhs,
                         uint32_t n, uint32_t in_format, uint32_t out_format,
                         uint32_t rhs_orientation);
 
+/* MFMA GEMM with a residual add fused into the epilogue: dst = Add(narrow(lhs .
+ * rhs), residual), the narrowed product of wafer_hip_gemm_mfma followed by the
+ * CT Add command (ManagedReferenceTargetModel.cpp:230-299), same bits.
+ * residual and dst [m, n] in the input format (BF16 or F16); dst may be the
+ * residual buffer itself.  A decoder block's x + proj(a) after the down (or
+ * O) projection. */
+int wafer_hip_gemm_mfma_residual(wafer_hip_context *ctx, const void *lhs,
+                                 const void *rhs, const void *residual,
+                                 void *dst, uint32_t m, uint32_t k, uint32_t n,
+                                 uint32_t in_format, uint32_t rhs_orientation);
+
 /* MFMA GEMM with SwiGLU fused into the epilogue: rhs_gu is [2*features, k]
  * (Transposed orientation) with rows in 64-row groups, rows 64j + [0,32) the
  * gate rows 32j + [0,32) and rows 64j + 32 + [0,32) the up rows of the same

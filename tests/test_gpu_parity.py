@@ -428,6 +428,45 @@ def test_mfma_gemm_192_tiles_vs_formal(hip, B, oracle, m, n, out):
     assert rel <= tol_rel and np.abs(got - ref).max() <= tol_max * np.abs(ref).max(), (rel,)
 
 
+@pytest.mark.parametrize("m,k,n,fmt,inplace,special", [
+    (1024, 512, 4096, 3, False, False), (1024, 256, 6144, 3, True, False), (4096, 256, 4096, 3, False, True),
+    (300, 128, 257, 3, False, True), (512, 256, 1024, 2, True, False), (4096, 256, 4096, 2, False, True),
+    (1024, 256, 6144, 2, False, True), (77, 64, 130, 2, False, True)])
+def test_mfma_gemm_residual_equals_gemm_then_add(hip, B, m, k, n, fmt, inplace, special):
+    """wafer_hip_gemm_mfma_residual gives the bits of the narrowed MFMA GEMM
+    followed by the Add command: 128x128, 128x192 and 256x256 tiles with the
+    staged epilogue, ragged shapes with the per-element one, in place
+    (dst = residual) and not.  The special cases plant residuals at the
+    format's largest finite value (sums that round to inf), infinities, NaNs
+    and subnormals, so the epilogue's narrowing meets every rounding edge."""
+    say("gemm residual", m, k, n, fmt, inplace, special)
+    dt = torch.bfloat16 if fmt == B.BF16 else torch.float16
+    gen = torch.Generator(device="cuda").manual_seed(m + k + n + fmt)
+    a = torch.randn(m, k, generator=gen, device="cuda").to(dt)
+    bt = (torch.randn(n, k, generator=gen, device="cuda") / math.sqrt(k)).to(dt)
+    res = torch.randn(m, n, generator=gen, device="cuda").to(dt)
+    if special:
+        fi = torch.finfo(dt)
+        res[0::7, 0::5] = fi.max
+        res[1::7, 1::5] = -fi.max
+        res[2::7, 2::5] = float("inf")
+        res[3::7, 3::5] = float("nan")
+        res[4::7, 0::3] = fi.smallest_normal / 4
+        res[5::7, 1::3] = -fi.smallest_normal * 3 / 8
+    prod = torch.empty(m, n, dtype=dt, device="cuda")
+    hip.gemm_mfma(a, bt, prod, m, k, n, in_fmt=fmt, out_fmt=fmt, rhs_t=True)
+    ref = torch.empty_like(prod)
+    hip.elementwise(B.EW["Add"], fmt, prod, ref, res)
+    if inplace:
+        out = res.clone()
+        hip.gemm_mfma_residual(a, bt, out, out, m, k, n, in_fmt=fmt, rhs_t=True)
+    else:
+        out = torch.full_like(res, 7.0)
+        hip.gemm_mfma_residual(a, bt, res, out, m, k, n, in_fmt=fmt, rhs_t=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
 @pytest.mark.parametrize("m,k,n", [(1024, 128, 6144), (1024, 128, 28672)])
 def test_i8_gemm_192_tiles_and_strips_bit_exact(hip, B, oracle, m, k, n):
     """int8 on the 128x192 tiles (n 6144) and on 448 256x256 tiles, whose

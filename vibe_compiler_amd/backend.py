@@ -49,6 +49,7 @@ EXPORTS = (
     "wafer_hip_compare_expected", "wafer_hip_compare_statistics", "wafer_hip_environment",
     "wafer_hip_first_nan", "wafer_hip_attention_decode_noalloc", "wafer_hip_attention_prefill_masked",
     "wafer_hip_elementwise_formal", "wafer_hip_pool", "wafer_hip_add_rmsnorm", "wafer_hip_attention_prefill_strided",
+    "wafer_hip_gemm_mfma_residual",
 )
 
 # wafer_hip_attention_mask flags
@@ -150,6 +151,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wafer_hip_synchronize.argtypes = [vp]
     L.wafer_hip_gemm.argtypes = [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32, u32, u32]
     L.wafer_hip_gemm_mfma.argtypes = [vp, vp, vp, vp, u32, u32, u32, u32, u32, u32]
+    L.wafer_hip_gemm_mfma_residual.argtypes = [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32]
     L.wafer_hip_gemm_mfma_swiglu.argtypes = [vp, vp, vp, vp, u32, u32, u32, u32]
     L.wafer_hip_gemm_i8.argtypes = [vp, vp, vp, vp, vp, vp, u32, u32, u32, u32]
     L.wafer_hip_elementwise.argtypes = [vp, u32, u32, vp, vp, vp, u64]
@@ -329,6 +331,16 @@ class Context:
         _arg("gemm_mfma", "dst", dst, out_fmt, m * n)
         _check(self._L.wafer_hip_gemm_mfma(self._bind(), _p(lhs), _p(rhs), _p(dst), m, k, n, in_fmt,
                                            out_fmt, int(rhs_t)))
+
+    def gemm_mfma_residual(self, lhs, rhs, residual, dst, m, k, n, in_fmt=BF16, rhs_t=False):
+        """dst = narrow(lhs . rhs) + residual (the Add command), in the input
+        format; dst may be residual."""
+        _arg("gemm_mfma_residual", "lhs", lhs, in_fmt, m * k)
+        _arg("gemm_mfma_residual", "rhs", rhs, in_fmt, k * n)
+        _arg("gemm_mfma_residual", "residual", residual, in_fmt, m * n)
+        _arg("gemm_mfma_residual", "dst", dst, in_fmt, m * n)
+        _check(self._L.wafer_hip_gemm_mfma_residual(self._bind(), _p(lhs), _p(rhs), _p(residual), _p(dst), m, k, n,
+                                                    in_fmt, int(rhs_t)))
 
     def gemm_mfma_swiglu(self, lhs, rhs_gu, dst, m, k, features, in_fmt=BF16):
         """dst [m, features] = silu_mul(gate, up) of the gate/up products, with

@@ -66,7 +66,23 @@ __device__ inline i32x16 mfma<KIND_I8>(u32x4 a, u32x4 b, i32x16 c) {
 // then the 32 up rows of the same features, and y[m, f] =
 // bf16(silu_mul(bf16(gate), bf16(up))) over N/2 features (the narrowed
 // products, then the silu_mul region).
-enum { OUT_F32 = 0, OUT_NARROW = 1, OUT_I8_DEQUANT = 2, OUT_SWIGLU = 3 };
+// OUT_NARROW_RES: the narrowed product plus a residual tensor of the same
+// format and shape, y = Add(narrow(acc), res) -- the GEMM's narrow output
+// followed by the CT Add command, bit for bit (y may be res itself: every
+// element is read before it is written, by the same lane).
+enum { OUT_F32 = 0, OUT_NARROW = 1, OUT_I8_DEQUANT = 2, OUT_SWIGLU = 3, OUT_NARROW_RES = 4 };
+
+// f16 -> f32 by v_cvt_f32_f16: exact for every finite f16 (subnormals
+// included, f16 denormals are on); a NaN keeps a NaN, and the sum it enters
+// narrows to the canonical f16 NaN either way, so the residual sum matches
+// the portable widening bit for bit.
+__device__ inline float widen_f16(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+// f32 -> f16 by v_cvt_f16_f32 in the default round-to-nearest-even mode, with
+// gradual underflow and overflow to +-inf; a NaN narrows to the canonical
+// 0x7e00 as f32_to_f16 does.
+__device__ inline uint16_t narrow_f16(float x) {
+  return x != x ? (uint16_t)0x7e00u : __builtin_bit_cast(uint16_t, (_Float16)x);
+}
 
 struct GemmArgs {
   const uint8_t *a;    // [M, K] elements, K-contiguous
@@ -76,6 +92,7 @@ struct GemmArgs {
   const float *scale;  // int8 only, [N]
   int m, n, kbytes;    // K in bytes
   int tiles_m, tiles_n;  // ceil(M / BM), ceil(N / BN)
+  const uint16_t *res;   // OUT_NARROW_RES only, [M, N]
 };
 
 // TAIL: the grid's last tile row / column may hold fewer than BM / BN rows /
@@ -293,8 +310,22 @@ gemm_nt_kernel(GemmArgs args) {
     static_assert((NW - IN_A) * PER <= NS * BN * CH * 16, "the staged sub-tiles fit in sA and sB");
     const int ldy = OUT == OUT_SWIGLU ? args.n / 2 : args.n;
     const bool staged = !TAIL && ldy % 8 == 0 && (((uintptr_t)args.y) & 15) == 0 &&
+                        (OUT != OUT_NARROW_RES || (((uintptr_t)args.res) & 15) == 0) &&
                         (OUT != OUT_I8_DEQUANT || args.acc_out == nullptr);
     if (staged) {
+      // the residual chunks this lane stores load first, behind the staging
+      // (up to 8 per lane; the 256x256 tiles' 16 load in the store loop)
+      constexpr int NQ = OR * CPR / 64;
+      constexpr bool PRE = OUT == OUT_NARROW_RES && NQ <= 8;
+      const int col0 = OUT == OUT_SWIGLU ? (n0 + wn * (BN / WN)) / 2 : n0 + wn * (BN / WN);
+      u32x4 rr[PRE ? NQ : 1];
+      if constexpr (PRE) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          const int idx = q * 64 + lane, row = idx / CPR, c = idx % CPR;
+          rr[q] = *(const u32x4 *)(args.res + (size_t)(m0 + wm * OR + row) * ldy + col0 + c * 8);
+        }
+      }
       __syncthreads();
       char *stage = wave < IN_A ? (char *)&sA[0][0] + wave * PER : (char *)&sB[0][0] + (wave - IN_A) * PER;
       auto put = [&](int row, int col, uint16_t v) __attribute__((always_inline)) {
@@ -322,8 +353,8 @@ gemm_nt_kernel(GemmArgs args) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               uint16_t v;
-              if (OUT == OUT_NARROW)
-                v = KIND == KIND_F16 ? f32_to_f16((float)acc[i][j][r]) : f32_to_bf16((float)acc[i][j][r]);
+              if (OUT == OUT_NARROW || OUT == OUT_NARROW_RES)
+                v = KIND == KIND_F16 ? narrow_f16((float)acc[i][j][r]) : f32_to_bf16((float)acc[i][j][r]);
               else
                 v = f32_to_bf16((float)(int32_t)acc[i][j][r] * sc);
               put(i * 32 + 8 * (r >> 2) + 4 * g + (r & 3), j * 32 + l32, v);
@@ -331,13 +362,28 @@ gemm_nt_kernel(GemmArgs args) {
         }
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's own sub-tile
-      const int col0 = OUT == OUT_SWIGLU ? (n0 + wn * (BN / WN)) / 2 : n0 + wn * (BN / WN);
       uint16_t *ybase = (uint16_t *)args.y + (size_t)(m0 + wm * OR) * ldy + col0;
 #pragma unroll
-      for (int q = 0; q < OR * CPR / 64; ++q) {
+      for (int q = 0; q < NQ; ++q) {
         const int idx = q * 64 + lane, row = idx / CPR, c = idx % CPR;
-        const u32x4 v = *(const u32x4 *)(stage + row * (CPR * 16) + (spos(row, c) << 4));
+        u32x4 v = *(const u32x4 *)(stage + row * (CPR * 16) + (spos(row, c) << 4));
+        if constexpr (OUT == OUT_NARROW_RES) {  // + the residual chunk at the same place
+          const u32x4 rq =
+              PRE ? rr[PRE ? q : 0] : *(const u32x4 *)(args.res + (size_t)(m0 + wm * OR + row) * ldy + col0 + c * 8);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t a = v[e], b = rq[e];
+            const float lo = KIND == KIND_F16 ? widen_f16((uint16_t)a) + widen_f16((uint16_t)b)
+                                              : bf16_to_f32((uint16_t)a) + bf16_to_f32((uint16_t)b);
+            const float hi = KIND == KIND_F16 ? widen_f16((uint16_t)(a >> 16)) + widen_f16((uint16_t)(b >> 16))
+                                              : bf16_to_f32((uint16_t)(a >> 16)) + bf16_to_f32((uint16_t)(b >> 16));
+            v[e] = KIND == KIND_F16 ? ((uint32_t)narrow_f16(lo) | ((uint32_t)narrow_f16(hi) << 16))
+                                    : ((uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16));
+          }
+        }
         *(u32x4 *)(ybase + (size_t)row * ldy + c * 8) = v;
+        // keep the in-loop residual loads from all hoisting at once
+        if constexpr (OUT == OUT_NARROW_RES && !PRE) __builtin_amdgcn_sched_barrier(0);
       }
       return;
     }
@@ -384,7 +430,12 @@ gemm_nt_kernel(GemmArgs args) {
           ((float *)args.y)[o] = (float)acc[i][j][r];
         } else if (OUT == OUT_NARROW) {
           const float v = (float)acc[i][j][r];
-          ((uint16_t *)args.y)[o] = KIND == KIND_F16 ? f32_to_f16(v) : f32_to_bf16(v);
+          ((uint16_t *)args.y)[o] = KIND == KIND_F16 ? narrow_f16(v) : f32_to_bf16(v);
+        } else if (OUT == OUT_NARROW_RES) {
+          const float v = (float)acc[i][j][r];
+          const float nv = KIND == KIND_F16 ? widen_f16(narrow_f16(v)) : bf16_to_f32(f32_to_bf16(v));
+          const float rv = KIND == KIND_F16 ? widen_f16(args.res[o]) : bf16_to_f32(args.res[o]);
+          ((uint16_t *)args.y)[o] = KIND == KIND_F16 ? narrow_f16(nv + rv) : f32_to_bf16(nv + rv);
         } else {
           const int32_t a32 = (int32_t)acc[i][j][r];
           if (args.acc_out) args.acc_out[o] = a32;
@@ -622,6 +673,24 @@ extern "C" int wafer_hip_gemm_mfma(wafer_hip_context *ctx, const void *lhs, cons
                : launch_gemm<KIND_BF16, OUT_NARROW>(ctx->stream, args);
   return f32 ? launch_gemm<KIND_F16, OUT_F32>(ctx->stream, args)
              : launch_gemm<KIND_F16, OUT_NARROW>(ctx->stream, args);
+}
+
+extern "C" int wafer_hip_gemm_mfma_residual(wafer_hip_context *ctx, const void *lhs, const void *rhs,
+                                            const void *residual, void *dst, uint32_t m, uint32_t k, uint32_t n,
+                                            uint32_t in_format, uint32_t rhs_orientation) {
+  WAFER_CHECK_CTX(ctx);
+  if (in_format != WAFER_FMT_BF16 && in_format != WAFER_FMT_F16)
+    return fail(WAFER_HIP_E_UNSUPPORTED, "gemm_mfma_residual: input format must be BF16 or F16");
+  if (rhs_orientation > 1) return fail(WAFER_HIP_E_INVALID_FIELD, "gemm_mfma_residual: bad orientation");
+  if (!lhs || !rhs || !residual || !dst) return fail(WAFER_HIP_E_INVALID_FIELD, "gemm_mfma_residual: null tensor");
+  WAFER_TRY(check_shape(m, k, n, 2, "gemm_mfma_residual"));
+  WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
+  const uint8_t *bt = (const uint8_t *)rhs;
+  if (rhs_orientation == WAFER_GEMM_NORMAL) WAFER_TRY(relayout_rhs(ctx, rhs, k, n, 2, &bt));
+  GemmArgs args{(const uint8_t *)lhs, bt, dst, nullptr, nullptr, (int)m, (int)n, (int)(k * 2), 0, 0,
+                (const uint16_t *)residual};
+  return in_format == WAFER_FMT_BF16 ? launch_gemm<KIND_BF16, OUT_NARROW_RES>(ctx->stream, args)
+                                     : launch_gemm<KIND_F16, OUT_NARROW_RES>(ctx->stream, args);
 }
 
 extern "C" int wafer_hip_gemm_mfma_swiglu(wafer_hip_context *ctx, const void *lhs, const void *rhs_gu,

@@ -11,7 +11,8 @@ backend, each one a C-ABI call of ``libwafer_hip.so`` on the caller's stream:
     x1   = x + a . Wo^T                               wafer_hip_gemm_mfma, wafer_hip_add_rmsnorm (Add
     h2   = RMSNorm(x1) * w_post                         and the norm in one pass)
     act  = silu(h2 . Wg^T) * (h2 . Wu^T)              wafer_hip_gemm_mfma_swiglu
-    y    = x1 + act . Wd^T                            wafer_hip_gemm_mfma, Add
+    y    = x1 + act . Wd^T                            wafer_hip_gemm_mfma_residual (the Add in the
+                                                      GEMM's epilogue)
 
 The fused SwiGLU GEMM gives the same bits as the unfused sequence (gate and
 up GEMMs with narrow outputs, then the silu_mul region): its epilogue rounds
@@ -91,7 +92,6 @@ class DecoderLayer:
         self.proj = e(T, hidden)
         self.x1 = e(T, hidden)
         self.act = e(T, ffn)
-        self.down = e(T, hidden)
         self.pos = torch.arange(T, dtype=torch.int32, device=dev)
 
     def forward(self, x, y):
@@ -109,8 +109,7 @@ class DecoderLayer:
         hip.gemm_mfma(self.attn, self.wo, self.proj, T, Hd, Hd, out_fmt=B.BF16, rhs_t=True)
         hip.add_rmsnorm(x, self.proj, self.w_post, self.x1, self.h, self.eps)
         hip.gemm_mfma_swiglu(self.h, self.wgu, self.act, T, Hd, F)
-        hip.gemm_mfma(self.act, self.wd, self.down, T, F, Hd, out_fmt=B.BF16, rhs_t=True)
-        hip.elementwise(ADD, B.BF16, self.x1, y, self.down)
+        hip.gemm_mfma_residual(self.act, self.wd, self.x1, y, T, F, Hd, rhs_t=True)
         return y
 
 
