@@ -154,6 +154,29 @@ int wafer_hip_gemm_mfma_swiglu(wafer_hip_context *ctx, const void *lhs,
                                uint32_t k, uint32_t features,
                                uint32_t in_format);
 
+/* ---- f32 MFMA GEMM (tolerance parity) with a fused bias / GELU epilogue ----
+ * Replaces the oneDNN lane's f32 matmul for F32 operands, executeOneDNN
+ * (lib/Wafer/Simulator/OneDNN/OneDNNGemmAdapter.cpp:278-420: deterministic,
+ * strict f32 math, an accumulation order of its own), with the bias_add and
+ * gelu_tanh regions of an MLP block optionally fused after it.  dst [m,n] =
+ * epilogue(lhs [m,k] . rhs), rhs [k,n] Normal or [n,k] Transpose, on
+ * v_mfma_f32_32x32x2_f32 (f32 products, f32 accumulation in a fixed order:
+ * results repeat bit for bit and match the formal lane within tolerance).
+ * epilogue: NONE; BIAS (dst = acc + bias[n], the bias_add region's F32 add);
+ * BIAS_GELU_TANH (gelu_tanh of that sum, the gelu_tanh region's formula).
+ * Any m, n; k a multiple of 8; lhs, dst and a Transposed rhs 16-byte aligned.
+ * Small grids split k over workgroups through a context-owned partial-tile
+ * area (grown on first use; growing is refused on a capturing stream). */
+enum {
+  WAFER_HIP_EPILOGUE_NONE = 0,
+  WAFER_HIP_EPILOGUE_BIAS = 1,
+  WAFER_HIP_EPILOGUE_BIAS_GELU_TANH = 2
+};
+int wafer_hip_gemm_f32_mfma(wafer_hip_context *ctx, const float *lhs,
+                            const float *rhs, const float *bias, float *dst,
+                            uint32_t m, uint32_t k, uint32_t n,
+                            uint32_t rhs_orientation, uint32_t epilogue);
+
 /* ---- int8 GEMM -------------------------------------------------------------
  * No reference implementation exists (the formal and oneDNN lanes reject I8:
  * lib/Wafer/Simulator/Reference/Formal/FormalNumericValidation.cpp:78-83,

@@ -201,6 +201,94 @@ def test_fp32_mlp_block_config0(hip, B, oracle):
     assert np.abs(gh - h1).max() <= 1e-5
 
 
+def test_fp32_mlp_block_config0_mfma(hip, B, oracle):
+    """BASELINE config 0 on the f32 MFMA lane: two wafer_hip_gemm_f32_mfma
+    calls (bias + tanh-GELU fused into the first, bias into the second)
+    against the formal CPU composition, to C1's 1e-4 relative bound: relative
+    L2 <= 1e-5, and per element rtol 1e-4 with atol 1e-5 * max|ref| (the f32
+    sums run in another order: about 1e-6 absolute on outputs of order 1,
+    which a pure per-element rtol cannot hold near zero)."""
+    say("fp32 mlp block, f32 mfma")
+    rng = np.random.default_rng(20260803)
+    x = rng.standard_normal((128, 512)).astype(np.float32)
+    w1 = (rng.standard_normal((512, 2048)) / math.sqrt(512)).astype(np.float32)
+    b1 = (rng.standard_normal(2048) * 0.02).astype(np.float32)
+    w2 = (rng.standard_normal((2048, 512)) / math.sqrt(2048)).astype(np.float32)
+    b2 = (rng.standard_normal(512) * 0.02).astype(np.float32)
+    h1 = oracle.gemm_formal(oracle.F32, oracle.F32, x, w1, 128, 512, 2048).reshape(128, 2048)
+    h1 = oracle.gelu_tanh(oracle.bias_add(h1, b1), fmt=oracle.F32)
+    y = oracle.gemm_formal(oracle.F32, oracle.F32, h1, w2, 128, 2048, 512).reshape(128, 512)
+    y = oracle.bias_add(y, b2)
+    hd = torch.empty((128, 2048), dtype=torch.float32, device="cuda")
+    yd = torch.empty((128, 512), dtype=torch.float32, device="cuda")
+    hip.gemm_f32_mfma(dev(x), dev(w1), hd, 128, 512, 2048, bias=dev(b1), epilogue=B.EPILOGUE_BIAS_GELU_TANH)
+    hip.gemm_f32_mfma(hd, dev(w2), yd, 128, 2048, 512, bias=dev(b2), epilogue=B.EPILOGUE_BIAS)
+    got = host(yd)
+    assert np.linalg.norm(got - y) / np.linalg.norm(y) <= 1e-5
+    assert np.all(np.abs(got - y) <= 1e-4 * np.abs(y) + 1e-5 * np.abs(y).max())
+    assert np.abs(host(hd) - h1).max() <= 1e-5
+
+
+@pytest.mark.parametrize("m,k,n,rt", [(128, 512, 2048, False), (128, 2048, 512, False), (128, 2048, 512, True),
+                                      (77, 72, 130, False), (300, 1000, 257, True), (1024, 256, 1024, False),
+                                      (33, 4096, 40, False), (8, 8, 8, True), (200, 512, 330, True),
+                                      (200, 512, 330, False)])
+def test_gemm_f32_mfma_vs_formal_and_unfused(hip, B, oracle, m, k, n, rt):
+    """wafer_hip_gemm_f32_mfma: the product against the formal lane (f32
+    accumulation in another order: relative L2 <= 1e-5, max |d| <= 5e-5 *
+    max |ref|); the bias and bias + tanh-GELU epilogues bit-identical to the
+    plain product followed by the bias_add and gelu_tanh regions; a repeated
+    call bit-identical.  Shapes cover 32x32 tiles with one split (n 2048,
+    1024 tiles), 16x16 tiles (n 512 and the ragged 200 x 330), k split over
+    workgroups with a fold launch (n 40, the ragged 300 x 257 with k 1000),
+    ragged m, n and k."""
+    say("gemm f32 mfma", m, k, n, rt)
+    rng = np.random.default_rng(m * 7 + k * 3 + n + rt)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = (rng.standard_normal((k, n)) / math.sqrt(k)).astype(np.float32)
+    bias = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    ref = oracle.gemm_formal(oracle.F32, oracle.F32, a, b, m, k, n).reshape(m, n)
+    ad, bd, biasd = dev(a), dev(np.ascontiguousarray(b.T) if rt else b), dev(bias)
+    plain = torch.full((m, n), 7.5, dtype=torch.float32, device="cuda")
+    hip.gemm_f32_mfma(ad, bd, plain, m, k, n, rhs_t=rt)
+    got = host(plain)
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-5
+    assert np.abs(got - ref).max() <= 5e-5 * np.abs(ref).max()
+    again = torch.empty_like(plain)
+    hip.gemm_f32_mfma(ad, bd, again, m, k, n, rhs_t=rt)
+    assert torch.equal(again.view(torch.int32), plain.view(torch.int32))
+    # fused epilogues against the unfused regions on the same product
+    want_b = torch.empty_like(plain)
+    hip.bias_add(plain, biasd, want_b, fmt=B.F32)
+    want_g = torch.empty_like(plain)
+    hip.gelu_tanh(want_b, want_g, fmt=B.F32)
+    got_b = torch.empty_like(plain)
+    hip.gemm_f32_mfma(ad, bd, got_b, m, k, n, bias=biasd, epilogue=B.EPILOGUE_BIAS, rhs_t=rt)
+    got_g = torch.empty_like(plain)
+    hip.gemm_f32_mfma(ad, bd, got_g, m, k, n, bias=biasd, epilogue=B.EPILOGUE_BIAS_GELU_TANH, rhs_t=rt)
+    torch.cuda.synchronize()
+    assert torch.equal(got_b.view(torch.int32), want_b.view(torch.int32))
+    assert torch.equal(got_g.view(torch.int32), want_g.view(torch.int32))
+
+
+def test_gemm_f32_mfma_rejections(hip, B):
+    """k not a multiple of 8, a missing bias for a bias epilogue, an unknown
+    epilogue and a misaligned lhs are refused before any launch."""
+    say("gemm f32 mfma rejections")
+    a = torch.zeros(64 * 64 + 4, dtype=torch.float32, device="cuda")
+    b = torch.zeros(64 * 64, dtype=torch.float32, device="cuda")
+    y = torch.zeros(64 * 64, dtype=torch.float32, device="cuda")
+    with pytest.raises(B.WaferHipError) as e:
+        hip.gemm_f32_mfma(a, b, y, 64, 60, 64)
+    assert e.value.status == -3  # UnsupportedCommand
+    for bad in (dict(epilogue=B.EPILOGUE_BIAS), dict(epilogue=3, bias=b)):
+        with pytest.raises((B.WaferHipError, ValueError)):
+            hip.gemm_f32_mfma(a, b, y, 64, 64, 64, **bad)
+    with pytest.raises(B.WaferHipError) as e:
+        hip.gemm_f32_mfma(a[1:], b, y, 64, 64, 64)
+    assert e.value.status == -3  # UnsupportedCommand
+
+
 # ------------------------------------------------------------------ int8 GEMM
 @pytest.mark.parametrize("m,k,n", [(256, 256, 256), (128, 640, 384), (512, 4096, 256)])
 @pytest.mark.parametrize("rt", [0, 1])

@@ -49,8 +49,11 @@ EXPORTS = (
     "wafer_hip_compare_expected", "wafer_hip_compare_statistics", "wafer_hip_environment",
     "wafer_hip_first_nan", "wafer_hip_attention_decode_noalloc", "wafer_hip_attention_prefill_masked",
     "wafer_hip_elementwise_formal", "wafer_hip_pool", "wafer_hip_add_rmsnorm", "wafer_hip_attention_prefill_strided",
-    "wafer_hip_gemm_mfma_residual",
+    "wafer_hip_gemm_mfma_residual", "wafer_hip_gemm_f32_mfma",
 )
+
+# wafer_hip_gemm_f32_mfma epilogues
+EPILOGUE_NONE, EPILOGUE_BIAS, EPILOGUE_BIAS_GELU_TANH = 0, 1, 2
 
 # wafer_hip_attention_mask flags
 ATT_CAUSAL, ATT_WINDOW, ATT_ROUND_SCALED, ATT_ROUND_BIASED = 1, 2, 4, 8
@@ -153,6 +156,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wafer_hip_gemm_mfma.argtypes = [vp, vp, vp, vp, u32, u32, u32, u32, u32, u32]
     L.wafer_hip_gemm_mfma_residual.argtypes = [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32]
     L.wafer_hip_gemm_mfma_swiglu.argtypes = [vp, vp, vp, vp, u32, u32, u32, u32]
+    L.wafer_hip_gemm_f32_mfma.argtypes = [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32]
     L.wafer_hip_gemm_i8.argtypes = [vp, vp, vp, vp, vp, vp, u32, u32, u32, u32]
     L.wafer_hip_elementwise.argtypes = [vp, u32, u32, vp, vp, vp, u64]
     L.wafer_hip_convert.argtypes = [vp, u32, u32, vp, vp, u64]
@@ -341,6 +345,18 @@ class Context:
         _arg("gemm_mfma_residual", "dst", dst, in_fmt, m * n)
         _check(self._L.wafer_hip_gemm_mfma_residual(self._bind(), _p(lhs), _p(rhs), _p(residual), _p(dst), m, k, n,
                                                     in_fmt, int(rhs_t)))
+
+    def gemm_f32_mfma(self, lhs, rhs, dst, m, k, n, bias=None, epilogue=EPILOGUE_NONE, rhs_t=False):
+        """dst [m, n] = epilogue(lhs [m, k] . rhs) in f32 on the f32 MFMA
+        (rhs [k, n], or [n, k] with rhs_t); epilogue EPILOGUE_BIAS adds
+        bias [n], EPILOGUE_BIAS_GELU_TANH applies tanh-GELU to that sum."""
+        _arg("gemm_f32_mfma", "lhs", lhs, F32, m * k)
+        _arg("gemm_f32_mfma", "rhs", rhs, F32, k * n)
+        _arg("gemm_f32_mfma", "dst", dst, F32, m * n)
+        if epilogue != EPILOGUE_NONE:
+            _arg("gemm_f32_mfma", "bias", bias, F32, n)
+        _check(self._L.wafer_hip_gemm_f32_mfma(self._bind(), _p(lhs), _p(rhs), _p(bias), _p(dst), m, k, n,
+                                               int(rhs_t), epilogue))
 
     def gemm_mfma_swiglu(self, lhs, rhs_gu, dst, m, k, features, in_fmt=BF16):
         """dst [m, features] = silu_mul(gate, up) of the gate/up products, with

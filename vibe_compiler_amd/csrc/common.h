@@ -23,6 +23,9 @@ struct wafer_hip_context {
   // Scratch for operand re-layout (transposed rhs), grown on demand.
   void *relayout = nullptr;
   size_t relayout_bytes = 0;
+  // Split-K partial tiles of the f32 GEMM, grown on demand.
+  void *partials = nullptr;
+  size_t partials_bytes = 0;
   int cu_count = 0;
 };
 
@@ -161,6 +164,13 @@ __device__ inline float explp_acc(float x) { return exp2f(x * 0x1.715476p+0f); }
 __device__ inline float silu_mul_1(float g, float u) {
   const float sig = 1.0f / (1.0f + explp_acc(-g));
   return g * sig * u;
+}
+// y = 0.5*x*(1 + Tanh(sqrt(2/pi)*(x + 0.044715*x^3))); shared by the
+// gelu_tanh region and the f32 GEMM's fused epilogue (same bits).
+__device__ inline float gelu_tanh_1(float v) {
+  const float k0 = 0.7978845608028654f, k1 = 0.044715f;
+  const float inner = k0 * (v + k1 * (v * v * v));
+  return 0.5f * v * (1.0f + tanhf(inner));
 }
 
 template <uint32_t F> __device__ inline float load_as_f32(const void *base, int64_t i);

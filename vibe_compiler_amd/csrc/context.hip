@@ -100,12 +100,13 @@ extern "C" int wafer_hip_context_create(int device, wafer_hip_context **out) {
 extern "C" int wafer_hip_context_destroy(wafer_hip_context *ctx) {
   if (!ctx) return WAFER_HIP_OK;
   int st = WAFER_HIP_OK;
-  if (ctx->workspace || ctx->relayout || ctx->status) {
+  if (ctx->workspace || ctx->relayout || ctx->status || ctx->partials) {
     st = check_hip(hipSetDevice(ctx->device), "hipSetDevice");
     if (st == WAFER_HIP_OK) st = check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     if (ctx->workspace) st = check_hip(hipFree(ctx->workspace), "hipFree(workspace)");
     if (ctx->relayout) st = check_hip(hipFree(ctx->relayout), "hipFree(relayout)");
     if (ctx->status) st = check_hip(hipFree(ctx->status), "hipFree(status)");
+    if (ctx->partials) st = check_hip(hipFree(ctx->partials), "hipFree(partials)");
   }
   delete ctx;
   return st;

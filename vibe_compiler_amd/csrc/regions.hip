@@ -269,12 +269,6 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const void *__restrict__ 
     store_from_f32<F>(y, (int64_t)i, silu_mul_1(load_as_f32<F>(gate, (int64_t)i), load_as_f32<F>(up, (int64_t)i)));
 }
 
-// y = 0.5*x*(1 + Tanh(sqrt(2/pi)*(x + 0.044715*x^3)))
-__device__ inline float gelu_tanh_1(float v) {
-  const float k0 = 0.7978845608028654f, k1 = 0.044715f;
-  const float inner = k0 * (v + k1 * (v * v * v));
-  return 0.5f * v * (1.0f + tanhf(inner));
-}
 template <uint32_t F, bool VEC>
 __global__ __launch_bounds__(256) void gelu_tanh_kernel(const void *__restrict__ x,
                                                         void *__restrict__ y, uint64_t count) {
