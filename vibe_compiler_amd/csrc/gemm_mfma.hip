@@ -32,6 +32,8 @@
 // order-independent, so the result is bit-exact.
 #include "common.h"
 
+#include <type_traits>
+
 namespace wafer {
 namespace {
 
@@ -95,6 +97,215 @@ struct GemmArgs {
   const uint16_t *res;   // OUT_NARROW_RES only, [M, N]
 };
 
+// XCD-aware tile order: workgroup ids are dealt round-robin over the 8
+// XCDs; the ids one XCD receives cover a 4 x 8 block of output tiles when the
+// grid is whole rounds of 256 tiles, else (tile rows divisible by 4, tile
+// columns by 8) the XCD's own column strip walked in 4-row groups.
+__device__ inline void tile_coords(const GemmArgs &args, int &tm, int &tn) {
+  const int tiles_m = args.tiles_m, tiles_n = args.tiles_n;
+  const int bid = blockIdx.x;
+  const int total = tiles_m * tiles_n;
+  if (total % 256 == 0 && tiles_m % 4 == 0 && tiles_n % 8 == 0) {
+    const int group = bid / 256, inner = bid % 256;  // 256 tiles per round
+    const int xcd = inner % 8, j = inner / 8;        // 32 tiles per XCD
+    const int gn = tiles_n / 8;                      // 4x8 blocks across the grid
+    const int blk = group * 8 + xcd;                 // which 4x8 block
+    const int bm = blk / gn, bn = blk % gn;
+    tm = bm * 4 + j / 8;
+    tn = bn * 8 + j % 8;
+  } else if (tiles_m % 4 == 0 && tiles_n % 8 == 0) {
+    // XCD x owns the column strip [x sw, (x + 1) sw) of the grid, walked in
+    // groups of 4 tile rows, column by column within a group: the 32 tiles
+    // an XCD runs at once span 4 rows and 8 columns
+    const int xcd = bid % 8, j = bid / 8;
+    const int sw = tiles_n / 8, per_group = 4 * sw;
+    const int grp = j / per_group, w = j % per_group;
+    tm = grp * 4 + w % 4;
+    tn = xcd * sw + w / 4;
+  } else {
+    tm = bid / tiles_n;
+    tn = bid % tiles_n;
+  }
+}
+
+// Epilogue shared by the GEMM kernels: lane holds column l32 and rows
+// 8*(r/4) + 4*g + r%4 of each 32x32 tile of its wave's sub-tile.  `stage` is
+// this wave's LDS staging area of (BM/WM) x (output columns per wave) 16-bit
+// values, used after a barrier that retires every wave's main-loop LDS
+// traffic.
+template <int KIND, int BM, int BN, int OUT, bool TAIL, int WM, int WN, bool STAGE = true>
+__device__ __attribute__((always_inline)) inline void gemm_store(
+    const GemmArgs &args, typename Acc<KIND>::T (&acc)[BM / WM / 32][BN / WN / 32], int m0, int n0,
+    char *stage) {
+  constexpr int WTM = BM / WM / 32, WTN = BN / WN / 32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int l32 = lane & 31, g = lane >> 5;
+  // Staged epilogue (16-bit outputs of full tiles): each wave narrows its
+  // sub-tile into LDS as row-major [OR][OC] 16-bit values (16-byte chunks of
+  // a row XOR-swizzled by (row / 4) % CPR, so the two row groups of one
+  // ds_write_b16 land in distinct banks), then reads it back 16 bytes per
+  // lane and stores whole 16-byte row segments (64 lanes cover 1 KiB of
+  // consecutive rows) instead of scattered 2-byte stores.  The sub-tiles are
+  // staged in sA, then sB, after a barrier that retires every wave's fragment
+  // reads and stage moves.
+  if constexpr (OUT != OUT_F32) {
+    constexpr int OR = BM / WM;                                     // rows per wave
+    constexpr int OC = OUT == OUT_SWIGLU ? BN / WN / 2 : BN / WN;   // output columns per wave
+    constexpr int CPR = OC * 2 / 16;                                // 16-byte chunks per row
+    static_assert(OR * CPR % 64 == 0, "whole 16-byte store rounds");
+    // position of 16-byte chunk c in a staged row: XOR when CPR is a power of
+    // two, else a rotation; either way rows 4 apart put a chunk in different
+    // positions
+    auto spos = [](int row, int c) __attribute__((always_inline)) {
+      return (CPR & (CPR - 1)) == 0 ? c ^ ((row >> 2) & (CPR - 1)) : (c + (row >> 2)) % CPR;
+    };
+    // the first IN_A waves stage in sA, the others in sB
+    const int ldy = OUT == OUT_SWIGLU ? args.n / 2 : args.n;
+    const bool staged = STAGE && !TAIL && ldy % 8 == 0 && (((uintptr_t)args.y) & 15) == 0 &&
+                        (OUT != OUT_NARROW_RES || (((uintptr_t)args.res) & 15) == 0) &&
+                        (OUT != OUT_I8_DEQUANT || args.acc_out == nullptr);
+    if (staged) {
+      // the residual chunks this lane stores load first, behind the staging
+      // (up to 8 per lane; the 256x256 tiles' 16 load in the store loop)
+      constexpr int NQ = OR * CPR / 64;
+      constexpr bool PRE = OUT == OUT_NARROW_RES && NQ <= 8;
+      const int col0 = OUT == OUT_SWIGLU ? (n0 + wn * (BN / WN)) / 2 : n0 + wn * (BN / WN);
+      u32x4 rr[PRE ? NQ : 1];
+      if constexpr (PRE) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          const int idx = q * 64 + lane, row = idx / CPR, c = idx % CPR;
+          rr[q] = *(const u32x4 *)(args.res + (size_t)(m0 + wm * OR + row) * ldy + col0 + c * 8);
+        }
+      }
+      __syncthreads();
+      auto put = [&](int row, int col, uint16_t v) __attribute__((always_inline)) {
+        *(uint16_t *)(stage + row * (CPR * 16) + (spos(row, col >> 3) << 4) + (col & 7) * 2) = v;
+      };
+      if constexpr (OUT == OUT_SWIGLU) {
+        static_assert(KIND == KIND_BF16, "the fused epilogue serves bf16");
+#pragma unroll
+        for (int i = 0; i < WTM; ++i)
+#pragma unroll
+          for (int jp = 0; jp < WTN / 2; ++jp)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const float gv = bf16_to_f32(f32_to_bf16((float)acc[i][2 * jp][r]));
+              const float uv = bf16_to_f32(f32_to_bf16((float)acc[i][2 * jp + 1][r]));
+              put(i * 32 + 8 * (r >> 2) + 4 * g + (r & 3), jp * 32 + l32, f32_to_bf16(silu_mul_1(gv, uv)));
+            }
+      } else {
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) {
+          float sc = 0.0f;
+          if (OUT == OUT_I8_DEQUANT) sc = args.scale[n0 + wn * (BN / WN) + j * 32 + l32];
+#pragma unroll
+          for (int i = 0; i < WTM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              uint16_t v;
+              if (OUT == OUT_NARROW || OUT == OUT_NARROW_RES)
+                v = KIND == KIND_F16 ? narrow_f16((float)acc[i][j][r]) : f32_to_bf16((float)acc[i][j][r]);
+              else
+                v = f32_to_bf16((float)(int32_t)acc[i][j][r] * sc);
+              put(i * 32 + 8 * (r >> 2) + 4 * g + (r & 3), j * 32 + l32, v);
+            }
+          // 128-row sub-tiles: bound the accumulators read out at once
+          if constexpr (WTM * WTN > 8) __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's own sub-tile
+      uint16_t *ybase = (uint16_t *)args.y + (size_t)(m0 + wm * OR) * ldy + col0;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const int idx = q * 64 + lane, row = idx / CPR, c = idx % CPR;
+        u32x4 v = *(const u32x4 *)(stage + row * (CPR * 16) + (spos(row, c) << 4));
+        if constexpr (OUT == OUT_NARROW_RES) {  // + the residual chunk at the same place
+          const u32x4 rq =
+              PRE ? rr[PRE ? q : 0] : *(const u32x4 *)(args.res + (size_t)(m0 + wm * OR + row) * ldy + col0 + c * 8);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t a = v[e], b = rq[e];
+            const float lo = KIND == KIND_F16 ? widen_f16((uint16_t)a) + widen_f16((uint16_t)b)
+                                              : bf16_to_f32((uint16_t)a) + bf16_to_f32((uint16_t)b);
+            const float hi = KIND == KIND_F16 ? widen_f16((uint16_t)(a >> 16)) + widen_f16((uint16_t)(b >> 16))
+                                              : bf16_to_f32((uint16_t)(a >> 16)) + bf16_to_f32((uint16_t)(b >> 16));
+            v[e] = KIND == KIND_F16 ? ((uint32_t)narrow_f16(lo) | ((uint32_t)narrow_f16(hi) << 16))
+                                    : ((uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16));
+          }
+        }
+        *(u32x4 *)(ybase + (size_t)row * ldy + c * 8) = v;
+        // keep the in-loop residual loads (and, past 16 rounds, the staged
+        // reads) from all hoisting at once
+        if constexpr (OUT == OUT_NARROW_RES && !PRE) __builtin_amdgcn_sched_barrier(0);
+        else if constexpr (NQ > 16) {
+          if ((q & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      return;
+    }
+  }
+  // epilogue: lane holds column l32 and rows 8*(r/4) + 4*g + r%4 of each tile
+  if constexpr (OUT == OUT_SWIGLU) {
+    // a wave's 32-column tiles 2 jp and 2 jp + 1 are the gate and up columns
+    // of the same 32 features
+    static_assert(WTN % 2 == 0, "SwiGLU pairs need two 32-column tiles per wave");
+    static_assert(KIND == KIND_BF16, "the fused epilogues serve bf16");
+    const int nf = args.n / 2;
+#pragma unroll
+    for (int i = 0; i < WTM; ++i)
+#pragma unroll
+      for (int jp = 0; jp < WTN / 2; ++jp) {
+        const int feat = (n0 + wn * (BN / WN) + jp * 64) / 2 + l32;
+        const bool col_ok = !TAIL || feat < nf;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (TAIL && !(col_ok && row < args.m)) continue;
+          const float gv = bf16_to_f32(f32_to_bf16((float)acc[i][2 * jp][r]));
+          const float uv = bf16_to_f32(f32_to_bf16((float)acc[i][2 * jp + 1][r]));
+          ((uint16_t *)args.y)[(size_t)row * nf + feat] = f32_to_bf16(silu_mul_1(gv, uv));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < WTM; ++i)
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) {
+      const int col = n0 + wn * (BN / WN) + j * 32 + l32;
+      const bool col_ok = !TAIL || col < args.n;
+      float sc = 0.0f;
+      if (OUT == OUT_I8_DEQUANT && col_ok) sc = args.scale[col];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (TAIL && !(col_ok && row < args.m)) continue;
+        const size_t o = (size_t)row * args.n + col;
+        if (OUT == OUT_F32) {
+          ((float *)args.y)[o] = (float)acc[i][j][r];
+        } else if (OUT == OUT_NARROW) {
+          const float v = (float)acc[i][j][r];
+          ((uint16_t *)args.y)[o] = KIND == KIND_F16 ? narrow_f16(v) : f32_to_bf16(v);
+        } else if (OUT == OUT_NARROW_RES) {
+          const float v = (float)acc[i][j][r];
+          const float nv = KIND == KIND_F16 ? widen_f16(narrow_f16(v)) : bf16_to_f32(f32_to_bf16(v));
+          const float rv = KIND == KIND_F16 ? widen_f16(args.res[o]) : bf16_to_f32(args.res[o]);
+          ((uint16_t *)args.y)[o] = KIND == KIND_F16 ? narrow_f16(nv + rv) : f32_to_bf16(nv + rv);
+        } else {
+          const int32_t a32 = (int32_t)acc[i][j][r];
+          if (args.acc_out) args.acc_out[o] = a32;
+          ((uint16_t *)args.y)[o] = f32_to_bf16((float)a32 * sc);
+        }
+      }
+      // keep the scheduler from hoisting every tile's conversion at once
+      __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+
 // TAIL: the grid's last tile row / column may hold fewer than BM / BN rows /
 // columns.  Those tiles load their last real A row (Bt row) again in place of
 // the missing ones, so every load stays inside the operands, and store only
@@ -124,35 +335,8 @@ gemm_nt_kernel(GemmArgs args) {
     return SB == 64 ? chunk ^ ((row >> 2) & 3) : chunk ^ (((row >> 1) ^ (row >> 4)) & 7);
   };
 
-  // XCD-aware tile order: ids are dealt round-robin over 8 XCDs; the ids one
-  // XCD receives cover a 4 x 8 block of output tiles when the grid allows it.
-  const int tiles_m = args.tiles_m, tiles_n = args.tiles_n;
   int tm, tn;
-  {
-    const int bid = blockIdx.x;
-    const int total = tiles_m * tiles_n;
-    if (total % 256 == 0 && tiles_m % 4 == 0 && tiles_n % 8 == 0) {
-      const int group = bid / 256, inner = bid % 256;  // 256 tiles per round
-      const int xcd = inner % 8, j = inner / 8;        // 32 tiles per XCD
-      const int gn = tiles_n / 8;                      // 4x8 blocks across the grid
-      const int blk = group * 8 + xcd;                 // which 4x8 block
-      const int bm = blk / gn, bn = blk % gn;
-      tm = bm * 4 + j / 8;
-      tn = bn * 8 + j % 8;
-    } else if (tiles_m % 4 == 0 && tiles_n % 8 == 0) {
-      // XCD x owns the column strip [x sw, (x + 1) sw) of the grid, walked
-      // in groups of 4 tile rows, column by column within a group: the 32
-      // tiles an XCD runs at once span 4 rows and 8 columns
-      const int xcd = bid % 8, j = bid / 8;
-      const int sw = tiles_n / 8, per_group = 4 * sw;
-      const int grp = j / per_group, w = j % per_group;
-      tm = grp * 4 + w % 4;
-      tn = xcd * sw + w / 4;
-    } else {
-      tm = bid / tiles_n;
-      tn = bid % tiles_n;
-    }
-  }
+  tile_coords(args, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -286,165 +470,161 @@ gemm_nt_kernel(GemmArgs args) {
   // the clamped tail loads are still in flight: drain before the LDS goes away
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // Staged epilogue (16-bit outputs of full tiles): each wave narrows its
-  // sub-tile into LDS as row-major [OR][OC] 16-bit values (16-byte chunks of
-  // a row XOR-swizzled by (row / 4) % CPR, so the two row groups of one
-  // ds_write_b16 land in distinct banks), then reads it back 16 bytes per
-  // lane and stores whole 16-byte row segments (64 lanes cover 1 KiB of
-  // consecutive rows) instead of scattered 2-byte stores.  The sub-tiles are
-  // staged in sA, then sB, after a barrier that retires every wave's fragment
-  // reads and stage moves.
-  if constexpr (OUT != OUT_F32) {
-    constexpr int OR = BM / WM;                                     // rows per wave
-    constexpr int OC = OUT == OUT_SWIGLU ? BN / WN / 2 : BN / WN;   // output columns per wave
-    constexpr int CPR = OC * 2 / 16;                                // 16-byte chunks per row
-    static_assert(OR * CPR % 64 == 0, "whole 16-byte store rounds");
-    // position of 16-byte chunk c in a staged row: XOR when CPR is a power of
-    // two, else a rotation; either way rows 4 apart put a chunk in different
-    // positions
-    auto spos = [](int row, int c) __attribute__((always_inline)) {
-      return (CPR & (CPR - 1)) == 0 ? c ^ ((row >> 2) & (CPR - 1)) : (c + (row >> 2)) % CPR;
-    };
-    // the first IN_A waves stage in sA, the others in sB
+  {
+    constexpr int OR = BM / WM, OC = OUT == OUT_SWIGLU ? BN / WN / 2 : BN / WN;
     constexpr int PER = OR * OC * 2, IN_A = (NS * BM * CH * 16) / PER < NW ? (NS * BM * CH * 16) / PER : NW;
-    static_assert((NW - IN_A) * PER <= NS * BN * CH * 16, "the staged sub-tiles fit in sA and sB");
-    const int ldy = OUT == OUT_SWIGLU ? args.n / 2 : args.n;
-    const bool staged = !TAIL && ldy % 8 == 0 && (((uintptr_t)args.y) & 15) == 0 &&
-                        (OUT != OUT_NARROW_RES || (((uintptr_t)args.res) & 15) == 0) &&
-                        (OUT != OUT_I8_DEQUANT || args.acc_out == nullptr);
-    if (staged) {
-      // the residual chunks this lane stores load first, behind the staging
-      // (up to 8 per lane; the 256x256 tiles' 16 load in the store loop)
-      constexpr int NQ = OR * CPR / 64;
-      constexpr bool PRE = OUT == OUT_NARROW_RES && NQ <= 8;
-      const int col0 = OUT == OUT_SWIGLU ? (n0 + wn * (BN / WN)) / 2 : n0 + wn * (BN / WN);
-      u32x4 rr[PRE ? NQ : 1];
-      if constexpr (PRE) {
-#pragma unroll
-        for (int q = 0; q < NQ; ++q) {
-          const int idx = q * 64 + lane, row = idx / CPR, c = idx % CPR;
-          rr[q] = *(const u32x4 *)(args.res + (size_t)(m0 + wm * OR + row) * ldy + col0 + c * 8);
-        }
-      }
-      __syncthreads();
-      char *stage = wave < IN_A ? (char *)&sA[0][0] + wave * PER : (char *)&sB[0][0] + (wave - IN_A) * PER;
-      auto put = [&](int row, int col, uint16_t v) __attribute__((always_inline)) {
-        *(uint16_t *)(stage + row * (CPR * 16) + (spos(row, col >> 3) << 4) + (col & 7) * 2) = v;
-      };
-      if constexpr (OUT == OUT_SWIGLU) {
-        static_assert(KIND == KIND_BF16, "the fused epilogue serves bf16");
-#pragma unroll
-        for (int i = 0; i < WTM; ++i)
-#pragma unroll
-          for (int jp = 0; jp < WTN / 2; ++jp)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const float gv = bf16_to_f32(f32_to_bf16((float)acc[i][2 * jp][r]));
-              const float uv = bf16_to_f32(f32_to_bf16((float)acc[i][2 * jp + 1][r]));
-              put(i * 32 + 8 * (r >> 2) + 4 * g + (r & 3), jp * 32 + l32, f32_to_bf16(silu_mul_1(gv, uv)));
-            }
-      } else {
-#pragma unroll
-        for (int j = 0; j < WTN; ++j) {
-          float sc = 0.0f;
-          if (OUT == OUT_I8_DEQUANT) sc = args.scale[n0 + wn * (BN / WN) + j * 32 + l32];
-#pragma unroll
-          for (int i = 0; i < WTM; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              uint16_t v;
-              if (OUT == OUT_NARROW || OUT == OUT_NARROW_RES)
-                v = KIND == KIND_F16 ? narrow_f16((float)acc[i][j][r]) : f32_to_bf16((float)acc[i][j][r]);
-              else
-                v = f32_to_bf16((float)(int32_t)acc[i][j][r] * sc);
-              put(i * 32 + 8 * (r >> 2) + 4 * g + (r & 3), j * 32 + l32, v);
-            }
-        }
-      }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's own sub-tile
-      uint16_t *ybase = (uint16_t *)args.y + (size_t)(m0 + wm * OR) * ldy + col0;
-#pragma unroll
-      for (int q = 0; q < NQ; ++q) {
-        const int idx = q * 64 + lane, row = idx / CPR, c = idx % CPR;
-        u32x4 v = *(const u32x4 *)(stage + row * (CPR * 16) + (spos(row, c) << 4));
-        if constexpr (OUT == OUT_NARROW_RES) {  // + the residual chunk at the same place
-          const u32x4 rq =
-              PRE ? rr[PRE ? q : 0] : *(const u32x4 *)(args.res + (size_t)(m0 + wm * OR + row) * ldy + col0 + c * 8);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t a = v[e], b = rq[e];
-            const float lo = KIND == KIND_F16 ? widen_f16((uint16_t)a) + widen_f16((uint16_t)b)
-                                              : bf16_to_f32((uint16_t)a) + bf16_to_f32((uint16_t)b);
-            const float hi = KIND == KIND_F16 ? widen_f16((uint16_t)(a >> 16)) + widen_f16((uint16_t)(b >> 16))
-                                              : bf16_to_f32((uint16_t)(a >> 16)) + bf16_to_f32((uint16_t)(b >> 16));
-            v[e] = KIND == KIND_F16 ? ((uint32_t)narrow_f16(lo) | ((uint32_t)narrow_f16(hi) << 16))
-                                    : ((uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16));
-          }
-        }
-        *(u32x4 *)(ybase + (size_t)row * ldy + c * 8) = v;
-        // keep the in-loop residual loads from all hoisting at once
-        if constexpr (OUT == OUT_NARROW_RES && !PRE) __builtin_amdgcn_sched_barrier(0);
-      }
-      return;
-    }
+    static_assert(OUT == OUT_F32 || (NW - IN_A) * PER <= NS * BN * CH * 16, "the staged sub-tiles fit in sA and sB");
+    char *stage = wave < IN_A ? (char *)&sA[0][0] + wave * PER : (char *)&sB[0][0] + (wave - IN_A) * PER;
+    gemm_store<KIND, BM, BN, OUT, TAIL, WM, WN>(args, acc, m0, n0, stage);
   }
-  // epilogue: lane holds column l32 and rows 8*(r/4) + 4*g + r%4 of each tile
-  if constexpr (OUT == OUT_SWIGLU) {
-    // a wave's 32-column tiles 2 jp and 2 jp + 1 are the gate and up columns
-    // of the same 32 features
-    static_assert(WTN % 2 == 0, "SwiGLU pairs need two 32-column tiles per wave");
-    static_assert(KIND == KIND_BF16, "the fused epilogues serve bf16");
-    const int nf = args.n / 2;
-#pragma unroll
-    for (int i = 0; i < WTM; ++i)
-#pragma unroll
-      for (int jp = 0; jp < WTN / 2; ++jp) {
-        const int feat = (n0 + wn * (BN / WN) + jp * 64) / 2 + l32;
-        const bool col_ok = !TAIL || feat < nf;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-          if (TAIL && !(col_ok && row < args.m)) continue;
-          const float gv = bf16_to_f32(f32_to_bf16((float)acc[i][2 * jp][r]));
-          const float uv = bf16_to_f32(f32_to_bf16((float)acc[i][2 * jp + 1][r]));
-          ((uint16_t *)args.y)[(size_t)row * nf + feat] = f32_to_bf16(silu_mul_1(gv, uv));
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    return;
-  }
+}
+
+// 256 x 256 tiles on 4 waves (2 x 2, each 128 x 128, one wave per SIMD with
+// its 256 accumulators in AGPRs): half the LDS fragment reads per MFMA of
+// the 8-wave kernel.  K slices are staged global -> VGPR -> LDS (16-byte
+// buffer loads, then ds_write_b128) instead of by LDS DMA, two register sets
+// deep: the loads for stage kt+2 are issued in stage kt's first two k-steps
+// and written to LDS in stage kt+1's third, a stage and a half of lead.  LDS
+// rows are 144 bytes (128 of data, 16 of pad), so 16 consecutive rows read at
+// one 16-byte chunk hit all 64 banks once and every fragment address is a
+// per-lane base plus an immediate.  K bytes a multiple of 256 (an even number
+// of 128-byte stages); full tiles only.  16-bit operands (int8 keeps the
+// 8-wave kernel: this one measured slower for it, its dequant epilogue
+// spilling the accumulators).
+template <int KIND, int OUT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_nt_rs_kernel(GemmArgs args) {
+  constexpr int BM = 256, BN = 256, WM = 2, WN = 2, SB = 128, PITCH = 144, KS = SB / 32;
+  constexpr int WTM = BM / WM / 32, WTN = BN / WN / 32;
+  constexpr int A_INSTR = BM / 8, B_INSTR = BN / 8;  // 8 rows of 128 bytes per wave instruction
+  constexpr int PER_WAVE = (A_INSTR + B_INSTR) / 4, HALF = PER_WAVE / 2, NR = WTM + WTN;
+  __shared__ __align__(16) uint8_t lds[2 * (BM + BN) * PITCH];
+  int tm, tn;
+  tile_coords(args, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wv / WN, wn = wv % WN;
+  const int l32 = lane & 31, g = lane >> 5;
+
+  typename Acc<KIND>::T acc[WTM][WTN];
 #pragma unroll
   for (int i = 0; i < WTM; ++i)
 #pragma unroll
-    for (int j = 0; j < WTN; ++j) {
-      const int col = n0 + wn * (BN / WN) + j * 32 + l32;
-      const bool col_ok = !TAIL || col < args.n;
-      float sc = 0.0f;
-      if (OUT == OUT_I8_DEQUANT && col_ok) sc = args.scale[col];
+    for (int j = 0; j < WTN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (TAIL && !(col_ok && row < args.m)) continue;
-        const size_t o = (size_t)row * args.n + col;
-        if (OUT == OUT_F32) {
-          ((float *)args.y)[o] = (float)acc[i][j][r];
-        } else if (OUT == OUT_NARROW) {
-          const float v = (float)acc[i][j][r];
-          ((uint16_t *)args.y)[o] = KIND == KIND_F16 ? narrow_f16(v) : f32_to_bf16(v);
-        } else if (OUT == OUT_NARROW_RES) {
-          const float v = (float)acc[i][j][r];
-          const float nv = KIND == KIND_F16 ? widen_f16(narrow_f16(v)) : bf16_to_f32(f32_to_bf16(v));
-          const float rv = KIND == KIND_F16 ? widen_f16(args.res[o]) : bf16_to_f32(args.res[o]);
-          ((uint16_t *)args.y)[o] = KIND == KIND_F16 ? narrow_f16(nv + rv) : f32_to_bf16(nv + rv);
-        } else {
-          const int32_t a32 = (int32_t)acc[i][j][r];
-          if (args.acc_out) args.acc_out[o] = a32;
-          ((uint16_t *)args.y)[o] = f32_to_bf16((float)a32 * sc);
-        }
-      }
-      // keep the scheduler from hoisting every tile's conversion at once
-      __builtin_amdgcn_sched_barrier(0);
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  const int kb = args.kbytes, nkt = args.kbytes / SB;
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc((void *)(args.a + (size_t)m0 * kb), 0, BM * kb, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb =
+      __builtin_amdgcn_make_buffer_rsrc((void *)(args.bt + (size_t)n0 * kb), 0, BN * kb, 0x00020000);
+  // lane l moves 16-byte chunk l % 8 of row l / 8 of an 8-row group
+  const int voff = (lane >> 3) * kb + (lane & 7) * 16;
+  const int woff = (lane >> 3) * PITCH + (lane & 7) * 16;
+
+  u32x4 stg[2][PER_WAVE];
+  auto gload = [&](int set, int kt, int q0, int q1) __attribute__((always_inline)) {
+    const int koff = min(kt, nkt - 1) * SB;  // past the last stage: a clamped copy, never used
+#pragma unroll
+    for (int q = q0; q < q1; ++q) {
+      const int ins = wv * PER_WAVE + q;
+      const bool is_a = ins < A_INSTR;
+      const int rel = is_a ? ins : ins - A_INSTR;
+      const int soff = __builtin_amdgcn_readfirstlane(rel * 8 * kb + koff);
+      stg[set][q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(is_a ? ra : rb, voff, soff, 0));
     }
+  };
+  auto lwrite = [&](int set, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < PER_WAVE; ++q) {
+      const int ins = wv * PER_WAVE + q;
+      const bool is_a = ins < A_INSTR;
+      const int rel = is_a ? ins : ins - A_INSTR;
+      *(u32x4 *)(lds + buf * (BM + BN) * PITCH + (is_a ? 0 : BM * PITCH) + rel * 8 * PITCH + woff) = stg[set][q];
+    }
+  };
+  // fragment rows wm*(BM/WM) + 32 i + l32 (A) and wn*(BN/WN) + 32 j + l32
+  // (Bt), 16-byte chunk 2 ks + g of the stage's 128-byte slice
+  const int fa_base = (wm * (BM / WM) + l32) * PITCH + g * 16;
+  const int fb_base = (BM + wn * (BN / WN) + l32) * PITCH + g * 16;
+  u32x4 fa[2][WTM], fb[2][WTN];
+  // in the order the next k-step's MFMAs (row-major over i, j) consume them
+  auto read_frags = [&](int buf, int ks, int f) __attribute__((always_inline)) {
+    const uint8_t *base = lds + buf * (BM + BN) * PITCH + ks * 32;
+    fa[f][0] = *(const u32x4 *)(base + fa_base);
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) fb[f][j] = *(const u32x4 *)(base + fb_base + j * 32 * PITCH);
+#pragma unroll
+    for (int i = 1; i < WTM; ++i) fa[f][i] = *(const u32x4 *)(base + fa_base + i * 32 * PITCH);
+  };
+  auto mfmas = [&](int f) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < WTM; ++i)
+#pragma unroll
+      for (int j = 0; j < WTN; ++j) acc[i][j] = mfma<KIND>(fa[f][i], fb[f][j], acc[i][j]);
+  };
+
+  gload(0, 0, 0, PER_WAVE);
+  gload(1, 1, 0, PER_WAVE);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER_WAVE) : "memory");
+  lwrite(0, 0);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  read_frags(0, 0, 0);
+
+  // Stage kt reads LDS buffer kt & 1.  Its first two k-steps issue the loads
+  // of stage kt+2 into register set kt & 1; its third writes set (kt+1) & 1
+  // (stage kt+1, loaded during stage kt-1) to buffer (kt+1) & 1, which every
+  // wave finished reading before the previous stage barrier; the barrier
+  // sits before the last k-step.  Each k-step interleaves 8 x (2 MFMAs,
+  // 1 fragment read for the next k-step, 1 load or 2 LDS writes).
+  auto stage = [&](int kt, auto P) __attribute__((always_inline)) {
+    constexpr int p = decltype(P)::value;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int cur = ks & 1;
+      if (ks < KS - 1) {
+        read_frags(p, ks + 1, cur ^ 1);
+        mfmas(cur);
+        if (ks == 0) gload(p, kt + 2, 0, HALF);
+        if (ks == 1) gload(p, kt + 2, HALF, PER_WAVE);
+        if (ks == 2) {
+          // set p^1 was issued a stage before set p: only set p may be in flight
+          asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER_WAVE) : "memory");
+          lwrite(p ^ 1, p ^ 1);
+        }
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          if (ks < 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+          if (ks == 2) __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        read_frags(p ^ 1, 0, cur ^ 1);
+        mfmas(cur);
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  for (int kt = 0; kt < nkt; kt += 2) {
+    stage(kt, std::integral_constant<int, 0>{});
+    stage(kt + 1, std::integral_constant<int, 1>{});
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // per-element stores: with one wave per SIMD the LDS-staged epilogue's
+  // barrier and 2-byte LDS writes cost more than the scattered stores
+  // (bf16 4096^3: 116.3 against 113.3 us; SwiGLU 1024x28672x4096: 223.7
+  // against 220.6 us)
+  gemm_store<KIND, BM, BN, OUT, false, WM, WN, false>(args, acc, m0, n0, nullptr);
 }
 
 // Re-layout of a normal rhs B [K, N] into Bt [N, K] (the NT operand form).
@@ -549,7 +729,9 @@ int launch_gemm_sb(hipStream_t st, GemmArgs args) {
     args.tiles_m = (args.m + 255) / 256;
     args.tiles_n = (args.n + 255) / 256;
     const dim3 grid(args.tiles_m * args.tiles_n);
-    if (args.m % 256 == 0 && args.n % 256 == 0)
+    if (args.m % 256 == 0 && args.n % 256 == 0 && args.kbytes % 256 == 0)
+      hipLaunchKernelGGL((gemm_nt_rs_kernel<KIND, OUT>), grid, dim3(256), 0, st, args);  // 16-bit only
+    else if (args.m % 256 == 0 && args.n % 256 == 0)
       hipLaunchKernelGGL((gemm_nt_kernel<KIND, 256, 256, OUT, false, SB>), grid, dim3(512), 0, st, args);
     else
       hipLaunchKernelGGL((gemm_nt_kernel<KIND, 256, 256, OUT, true, SB>), grid, dim3(512), 0, st, args);
@@ -563,6 +745,14 @@ int launch_gemm_tiles(hipStream_t st, GemmArgs args) {
   if (args.m % 256 == 0 && args.n % 256 == 0 && (args.m / 256) * (args.n / 256) >= 192) {
     args.tiles_m = args.m / 256;
     args.tiles_n = args.n / 256;
+    // 16-bit operands with an even number of 128-byte K stages: 4 waves,
+    // register-staged (int8 keeps 8 waves: its 4-wave dequant epilogue spills)
+    if constexpr (KIND != KIND_I8) {
+      if (args.kbytes % 256 == 0) {
+        hipLaunchKernelGGL((gemm_nt_rs_kernel<KIND, OUT>), dim3(args.tiles_m * args.tiles_n), dim3(256), 0, st, args);
+        return launch_status("gemm_nt_rs_kernel");
+      }
+    }
     hipLaunchKernelGGL((gemm_nt_kernel<KIND, 256, 256, OUT, false, SB>), dim3(args.tiles_m * args.tiles_n),
                        dim3(512), 0, st, args);
     return launch_status("gemm_nt_kernel");
