@@ -479,24 +479,46 @@ gemm_nt_kernel(GemmArgs args) {
   }
 }
 
-// 256 x 256 tiles on 4 waves (2 x 2, each 128 x 128, one wave per SIMD with
-// its 256 accumulators in AGPRs): half the LDS fragment reads per MFMA of
-// the 8-wave kernel.  K slices are staged global -> VGPR -> LDS (16-byte
-// buffer loads, then ds_write_b128) instead of by LDS DMA, two register sets
-// deep: the loads for stage kt+2 are issued in stage kt's first two k-steps
-// and written to LDS in stage kt+1's third, a stage and a half of lead.  LDS
-// rows are 144 bytes (128 of data, 16 of pad), so 16 consecutive rows read at
-// one 16-byte chunk hit all 64 banks once and every fragment address is a
-// per-lane base plus an immediate.  K bytes a multiple of 256 (an even number
-// of 128-byte stages); full tiles only.  16-bit operands (int8 keeps the
-// 8-wave kernel: this one measured slower for it, its dequant epilogue
-// spilling the accumulators).
-template <int KIND, int OUT>
+// Scheduling pins for one k-step of the 4-wave kernel: slot t holds one
+// MFMA, then (t+1) NR / NM - t NR / NM fragment reads and the same share of X
+// other memory operations of mask XM.
+template <int T, int NM, int NR, int X, int XM>
+__device__ __attribute__((always_inline)) inline void pin_slots() {
+  if constexpr (T < NM) {
+    constexpr int nr = ((T + 1) * NR) / NM - (T * NR) / NM;
+    constexpr int nx = ((T + 1) * X) / NM - (T * X) / NM;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if constexpr (nr > 0) __builtin_amdgcn_sched_group_barrier(0x100, nr, 0);
+    if constexpr (nx > 0) __builtin_amdgcn_sched_group_barrier(XM, nx, 0);
+    pin_slots<T + 1, NM, NR, X, XM>();
+  }
+}
+
+// 4-wave tiles (2 x 2 waves, one per SIMD, the accumulators in AGPRs).
+// Against the 8-wave kernel each wave's sub-tile is twice as large, so the
+// LDS fragment reads per MFMA halve (256 x 256: 128 x 128 per wave).  K
+// slices of SB bytes are staged global -> VGPR -> LDS (16-byte buffer loads,
+// then ds_write_b128) instead of by LDS DMA, two register sets deep: the
+// loads for stage kt+2 are issued over the first half of stage kt's k-steps
+// and written to LDS in stage kt+1's second-to-last k-step, a stage and a
+// half of lead.  LDS rows are SB + 16 bytes (one 16-byte pad), so 16
+// consecutive rows read at one 16-byte chunk hit all 64 banks once and every
+// fragment address is a per-lane base plus an immediate.  K bytes a multiple
+// of 2 SB (an even number of stages); full tiles only.  16-bit operands (int8
+// keeps the 8-wave kernel: this one measured slower for it, its dequant
+// epilogue spilling the accumulators).  STAGE selects the LDS-staged
+// epilogue (else per-element stores).
+template <int KIND, int OUT, int BM, int BN, int SB, bool STAGE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_nt_rs_kernel(GemmArgs args) {
-  constexpr int BM = 256, BN = 256, WM = 2, WN = 2, SB = 128, PITCH = 144, KS = SB / 32;
+  constexpr int WM = 2, WN = 2, PITCH = SB + 16, KS = SB / 32, CH = SB / 16, RPI = 64 / CH;
   constexpr int WTM = BM / WM / 32, WTN = BN / WN / 32;
-  constexpr int A_INSTR = BM / 8, B_INSTR = BN / 8;  // 8 rows of 128 bytes per wave instruction
-  constexpr int PER_WAVE = (A_INSTR + B_INSTR) / 4, HALF = PER_WAVE / 2, NR = WTM + WTN;
+  constexpr int A_INSTR = BM / RPI, B_INSTR = BN / RPI;  // RPI rows of SB bytes per wave instruction
+  constexpr int PER_WAVE = (A_INSTR + B_INSTR) / 4, NR = WTM + WTN, NM = WTM * WTN;
+  constexpr int LK = KS / 2, LPK = PER_WAVE / LK;        // k-steps carrying loads, loads per such k-step
+  constexpr int WK = KS - 2;                             // the k-step that writes the older set to LDS
+  static_assert((A_INSTR + B_INSTR) % 4 == 0 && PER_WAVE % LK == 0, "loads split evenly");
+  constexpr int OC = OUT == OUT_SWIGLU ? BN / WN / 2 : BN / WN;
+  static_assert(!STAGE || 4 * (BM / WM) * OC * 2 <= 2 * (BM + BN) * PITCH, "staging fits in the ring");
   __shared__ __align__(16) uint8_t lds[2 * (BM + BN) * PITCH];
   int tm, tn;
   tile_coords(args, tm, tn);
@@ -519,9 +541,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       __builtin_amdgcn_make_buffer_rsrc((void *)(args.a + (size_t)m0 * kb), 0, BM * kb, 0x00020000);
   const __amdgpu_buffer_rsrc_t rb =
       __builtin_amdgcn_make_buffer_rsrc((void *)(args.bt + (size_t)n0 * kb), 0, BN * kb, 0x00020000);
-  // lane l moves 16-byte chunk l % 8 of row l / 8 of an 8-row group
-  const int voff = (lane >> 3) * kb + (lane & 7) * 16;
-  const int woff = (lane >> 3) * PITCH + (lane & 7) * 16;
+  // lane l moves 16-byte chunk l % CH of row l / CH of an RPI-row group
+  const int voff = (lane / CH) * kb + (lane % CH) * 16;
+  const int woff = (lane / CH) * PITCH + (lane % CH) * 16;
 
   u32x4 stg[2][PER_WAVE];
   auto gload = [&](int set, int kt, int q0, int q1) __attribute__((always_inline)) {
@@ -531,7 +553,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       const int ins = wv * PER_WAVE + q;
       const bool is_a = ins < A_INSTR;
       const int rel = is_a ? ins : ins - A_INSTR;
-      const int soff = __builtin_amdgcn_readfirstlane(rel * 8 * kb + koff);
+      const int soff = __builtin_amdgcn_readfirstlane(rel * RPI * kb + koff);
       stg[set][q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(is_a ? ra : rb, voff, soff, 0));
     }
   };
@@ -541,11 +563,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       const int ins = wv * PER_WAVE + q;
       const bool is_a = ins < A_INSTR;
       const int rel = is_a ? ins : ins - A_INSTR;
-      *(u32x4 *)(lds + buf * (BM + BN) * PITCH + (is_a ? 0 : BM * PITCH) + rel * 8 * PITCH + woff) = stg[set][q];
+      *(u32x4 *)(lds + buf * (BM + BN) * PITCH + (is_a ? 0 : BM * PITCH) + rel * RPI * PITCH + woff) = stg[set][q];
     }
   };
   // fragment rows wm*(BM/WM) + 32 i + l32 (A) and wn*(BN/WN) + 32 j + l32
-  // (Bt), 16-byte chunk 2 ks + g of the stage's 128-byte slice
+  // (Bt), 16-byte chunk 2 ks + g of the stage's slice
   const int fa_base = (wm * (BM / WM) + l32) * PITCH + g * 16;
   const int fb_base = (BM + wn * (BN / WN) + l32) * PITCH + g * 16;
   u32x4 fa[2][WTM], fb[2][WTN];
@@ -564,6 +586,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
       for (int j = 0; j < WTN; ++j) acc[i][j] = mfma<KIND>(fa[f][i], fb[f][j], acc[i][j]);
   };
+  // pins one k-step's order: NM slots of one MFMA followed by their share of
+  // the NR fragment reads and of X other memory operations (mask XM)
+  auto pin = [&](auto X, auto XM) __attribute__((always_inline)) {
+    pin_slots<0, NM, NR, decltype(X)::value, decltype(XM)::value>();
+    __builtin_amdgcn_sched_barrier(0);
+  };
 
   gload(0, 0, 0, PER_WAVE);
   gload(1, 1, 0, PER_WAVE);
@@ -572,12 +600,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   read_frags(0, 0, 0);
 
-  // Stage kt reads LDS buffer kt & 1.  Its first two k-steps issue the loads
-  // of stage kt+2 into register set kt & 1; its third writes set (kt+1) & 1
-  // (stage kt+1, loaded during stage kt-1) to buffer (kt+1) & 1, which every
-  // wave finished reading before the previous stage barrier; the barrier
-  // sits before the last k-step.  Each k-step interleaves 8 x (2 MFMAs,
-  // 1 fragment read for the next k-step, 1 load or 2 LDS writes).
+  // Stage kt reads LDS buffer kt & 1.  Its first KS/2 k-steps issue the
+  // loads of stage kt+2 into register set kt & 1; k-step KS-2 writes set
+  // (kt+1) & 1 (stage kt+1, loaded during stage kt-1) to buffer (kt+1) & 1,
+  // which every wave finished reading before the previous stage barrier;
+  // the barrier sits before the last k-step.
   auto stage = [&](int kt, auto P) __attribute__((always_inline)) {
     constexpr int p = decltype(P)::value;
 #pragma unroll
@@ -586,32 +613,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       if (ks < KS - 1) {
         read_frags(p, ks + 1, cur ^ 1);
         mfmas(cur);
-        if (ks == 0) gload(p, kt + 2, 0, HALF);
-        if (ks == 1) gload(p, kt + 2, HALF, PER_WAVE);
-        if (ks == 2) {
+        if (ks < LK) gload(p, kt + 2, ks * LPK, (ks + 1) * LPK);
+        if (ks == WK) {
           // set p^1 was issued a stage before set p: only set p may be in flight
           asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER_WAVE) : "memory");
           lwrite(p ^ 1, p ^ 1);
         }
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          if (ks < 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-          if (ks == 2) __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);
+        if (ks < LK) {
+          pin(std::integral_constant<int, LPK>{}, std::integral_constant<int, 0x020>{});
+        } else if (ks == WK) {
+          pin(std::integral_constant<int, PER_WAVE>{}, std::integral_constant<int, 0x200>{});
+        } else {
+          pin(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
         }
-        __builtin_amdgcn_sched_barrier(0);
       } else {
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
         read_frags(p ^ 1, 0, cur ^ 1);
         mfmas(cur);
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+        pin(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
       }
     }
   };
@@ -620,11 +640,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     stage(kt + 1, std::integral_constant<int, 1>{});
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  // per-element stores: with one wave per SIMD the LDS-staged epilogue's
-  // barrier and 2-byte LDS writes cost more than the scattered stores
-  // (bf16 4096^3: 116.3 against 113.3 us; SwiGLU 1024x28672x4096: 223.7
-  // against 220.6 us)
-  gemm_store<KIND, BM, BN, OUT, false, WM, WN, false>(args, acc, m0, n0, nullptr);
+  gemm_store<KIND, BM, BN, OUT, false, WM, WN, STAGE>(args, acc, m0, n0, (char *)lds + wv * (BM / WM) * OC * 2);
 }
 
 // Re-layout of a normal rhs B [K, N] into Bt [N, K] (the NT operand form).
@@ -730,7 +746,7 @@ int launch_gemm_sb(hipStream_t st, GemmArgs args) {
     args.tiles_n = (args.n + 255) / 256;
     const dim3 grid(args.tiles_m * args.tiles_n);
     if (args.m % 256 == 0 && args.n % 256 == 0 && args.kbytes % 256 == 0)
-      hipLaunchKernelGGL((gemm_nt_rs_kernel<KIND, OUT>), grid, dim3(256), 0, st, args);  // 16-bit only
+      hipLaunchKernelGGL((gemm_nt_rs_kernel<KIND, OUT, 256, 256, 128, false>), grid, dim3(256), 0, st, args);
     else if (args.m % 256 == 0 && args.n % 256 == 0)
       hipLaunchKernelGGL((gemm_nt_kernel<KIND, 256, 256, OUT, false, SB>), grid, dim3(512), 0, st, args);
     else
@@ -746,10 +762,12 @@ int launch_gemm_tiles(hipStream_t st, GemmArgs args) {
     args.tiles_m = args.m / 256;
     args.tiles_n = args.n / 256;
     // 16-bit operands with an even number of 128-byte K stages: 4 waves,
-    // register-staged (int8 keeps 8 waves: its 4-wave dequant epilogue spills)
-    if constexpr (KIND != KIND_I8) {
+    // register-staged (int8 keeps 8 waves: its 4-wave dequant epilogue
+    // spills; a residual keeps the 8-wave kernel's staged epilogue)
+    if constexpr (KIND != KIND_I8 && OUT != OUT_NARROW_RES) {
       if (args.kbytes % 256 == 0) {
-        hipLaunchKernelGGL((gemm_nt_rs_kernel<KIND, OUT>), dim3(args.tiles_m * args.tiles_n), dim3(256), 0, st, args);
+        hipLaunchKernelGGL((gemm_nt_rs_kernel<KIND, OUT, 256, 256, 128, false>), dim3(args.tiles_m * args.tiles_n),
+                           dim3(256), 0, st, args);
         return launch_status("gemm_nt_rs_kernel");
       }
     }
@@ -768,6 +786,16 @@ int launch_gemm_tiles(hipStream_t st, GemmArgs args) {
       args.tiles_m = args.m / 128;
       args.tiles_n = args.n / 192;
       if constexpr (SB == 128) {
+        // 16-bit operands, plain outputs: the 4-wave kernel (QKV at M = 1024:
+        // 53.3 against 55.4 us); a residual keeps the 8-wave kernel's staged
+        // epilogue
+        if constexpr (KIND != KIND_I8 && OUT != OUT_NARROW_RES) {
+          if (args.kbytes % 256 == 0) {
+            hipLaunchKernelGGL((gemm_nt_rs_kernel<KIND, OUT, 128, 192, 128, false>), dim3(args.tiles_m * args.tiles_n),
+                               dim3(256), 0, st, args);
+            return launch_status("gemm_nt_rs_kernel");
+          }
+        }
         hipLaunchKernelGGL((gemm_nt_kernel<KIND, 128, 192, OUT, false, SB, 4, 2>),
                            dim3(args.tiles_m * args.tiles_n), dim3(512), 0, st, args);
         return launch_status("gemm_nt_kernel");
