@@ -408,8 +408,11 @@ def test_i8_gemm_ragged_bit_exact(hip, B, oracle, m, k, n, rt):
 
 # ------------------------------------------------------------------ MFMA bf16 GEMM
 @pytest.mark.parametrize("m,k,n,rt,fmt", [(256, 512, 256, 0, 3), (128, 256, 384, 1, 3), (512, 1024, 512, 0, 2),
-                                          (1024, 4096, 1024, 1, 3)])
+                                          (1024, 4096, 1024, 1, 3), (256, 8192, 1024, 1, 3), (256, 8192, 1024, 0, 2)])
 def test_mfma_gemm_vs_formal(hip, B, oracle, m, k, n, rt, fmt):
+    """The MFMA GEMM against the formal lane (f32 and narrowed outputs);
+    k 8192 at 256 x 1024 takes the split-K path (256x256 tiles, K over 4
+    workgroups, fold launch)."""
     say("mfma gemm", m, k, n, rt, fmt)
     rng = np.random.default_rng(m + n + k)
     a = rng.standard_normal((m, k)).astype(np.float32)
@@ -519,12 +522,14 @@ def test_mfma_gemm_192_tiles_vs_formal(hip, B, oracle, m, n, out):
 @pytest.mark.parametrize("m,k,n,fmt,inplace,special", [
     (1024, 512, 4096, 3, False, False), (1024, 256, 6144, 3, True, False), (4096, 256, 4096, 3, False, True),
     (300, 128, 257, 3, False, True), (512, 256, 1024, 2, True, False), (4096, 256, 4096, 2, False, True),
-    (1024, 256, 6144, 2, False, True), (77, 64, 130, 2, False, True)])
+    (1024, 256, 6144, 2, False, True), (77, 64, 130, 2, False, True), (512, 8192, 1024, 3, False, True),
+    (512, 8192, 1024, 2, True, True), (1024, 14336, 4096, 3, False, False)])
 def test_mfma_gemm_residual_equals_gemm_then_add(hip, B, m, k, n, fmt, inplace, special):
     """wafer_hip_gemm_mfma_residual gives the bits of the narrowed MFMA GEMM
     followed by the Add command: 128x128, 128x192 and 256x256 tiles with the
-    staged epilogue, ragged shapes with the per-element one, in place
-    (dst = residual) and not.  The special cases plant residuals at the
+    staged epilogue, ragged shapes with the per-element one, split-K with the
+    residual added by the fold launch (k 8192 and the decoder layer's down
+    projection), in place (dst = residual) and not.  The special cases plant residuals at the
     format's largest finite value (sums that round to inf), infinities, NaNs
     and subnormals, so the epilogue's narrowing meets every rounding edge."""
     say("gemm residual", m, k, n, fmt, inplace, special)

@@ -95,15 +95,19 @@ struct GemmArgs {
   int m, n, kbytes;    // K in bytes
   int tiles_m, tiles_n;  // ceil(M / BM), ceil(N / BN)
   const uint16_t *res;   // OUT_NARROW_RES only, [M, N]
+  // split-K (4-wave kernel only): ksplit > 1 workgroups per tile each take
+  // kbytes / ksplit of K and store f32 partial tiles to part [ksplit, M, N],
+  // which a fold launch adds in split order
+  int ksplit;
+  float *part;
 };
 
 // XCD-aware tile order: workgroup ids are dealt round-robin over the 8
 // XCDs; the ids one XCD receives cover a 4 x 8 block of output tiles when the
 // grid is whole rounds of 256 tiles, else (tile rows divisible by 4, tile
 // columns by 8) the XCD's own column strip walked in 4-row groups.
-__device__ inline void tile_coords(const GemmArgs &args, int &tm, int &tn) {
+__device__ inline void tile_coords(const GemmArgs &args, int bid, int &tm, int &tn) {
   const int tiles_m = args.tiles_m, tiles_n = args.tiles_n;
-  const int bid = blockIdx.x;
   const int total = tiles_m * tiles_n;
   if (total % 256 == 0 && tiles_m % 4 == 0 && tiles_n % 8 == 0) {
     const int group = bid / 256, inner = bid % 256;  // 256 tiles per round
@@ -336,7 +340,7 @@ gemm_nt_kernel(GemmArgs args) {
   };
 
   int tm, tn;
-  tile_coords(args, tm, tn);
+  tile_coords(args, blockIdx.x, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -520,8 +524,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   constexpr int OC = OUT == OUT_SWIGLU ? BN / WN / 2 : BN / WN;
   static_assert(!STAGE || 4 * (BM / WM) * OC * 2 <= 2 * (BM + BN) * PITCH, "staging fits in the ring");
   __shared__ __align__(16) uint8_t lds[2 * (BM + BN) * PITCH];
+  // split-K: workgroup ids [s tiles, (s + 1) tiles) take split s
+  const int tiles = args.tiles_m * args.tiles_n;
+  const int split = args.ksplit > 1 ? (int)blockIdx.x / tiles : 0;
   int tm, tn;
-  tile_coords(args, tm, tn);
+  tile_coords(args, (int)blockIdx.x - split * tiles, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -536,11 +543,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-  const int kb = args.kbytes, nkt = args.kbytes / SB;
+  // row stride kb; this workgroup's K slice starts at byte k0 and spans nkt stages
+  const int kb = args.kbytes;
+  const int kchunk = args.ksplit > 1 ? kb / args.ksplit : kb;
+  const int k0 = split * kchunk, nkt = kchunk / SB;
   const __amdgpu_buffer_rsrc_t ra =
-      __builtin_amdgcn_make_buffer_rsrc((void *)(args.a + (size_t)m0 * kb), 0, BM * kb, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc((void *)(args.a + (size_t)m0 * kb + k0), 0, BM * kb - k0, 0x00020000);
   const __amdgpu_buffer_rsrc_t rb =
-      __builtin_amdgcn_make_buffer_rsrc((void *)(args.bt + (size_t)n0 * kb), 0, BN * kb, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc((void *)(args.bt + (size_t)n0 * kb + k0), 0, BN * kb - k0, 0x00020000);
   // lane l moves 16-byte chunk l % CH of row l / CH of an RPI-row group
   const int voff = (lane / CH) * kb + (lane % CH) * 16;
   const int woff = (lane / CH) * PITCH + (lane % CH) * 16;
@@ -640,7 +650,59 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     stage(kt + 1, std::integral_constant<int, 1>{});
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  gemm_store<KIND, BM, BN, OUT, false, WM, WN, STAGE>(args, acc, m0, n0, (char *)lds + wv * (BM / WM) * OC * 2);
+  if (args.ksplit > 1) {
+    GemmArgs pa = args;
+    pa.y = args.part + (size_t)split * args.m * args.n;
+    gemm_store<KIND, BM, BN, OUT_F32, false, WM, WN, false>(pa, acc, m0, n0, nullptr);
+  } else {
+    gemm_store<KIND, BM, BN, OUT, false, WM, WN, STAGE>(args, acc, m0, n0, (char *)lds + wv * (BM / WM) * OC * 2);
+  }
+}
+
+// Split-K fold: y = epilogue(part[0] + part[1] + ... + part[S-1]) per
+// element, the partial tiles added in split order; OUT_NARROW narrows to
+// the input format, OUT_NARROW_RES adds the residual as the per-element
+// epilogue does, OUT_F32 stores the sum.  8 elements per thread (M*N a
+// multiple of 8).
+template <int KIND, int OUT>
+__global__ __launch_bounds__(256) void gemm_fold_kernel(const float *__restrict__ part, int ksplit,
+                                                        const uint16_t *__restrict__ res, void *__restrict__ y,
+                                                        int64_t count) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < count / 8; q += stride) {
+    f32x4 lo = *(const f32x4 *)(part + 8 * q), hi = *(const f32x4 *)(part + 8 * q + 4);
+    for (int s = 1; s < ksplit; ++s) {
+      lo = lo + *(const f32x4 *)(part + (size_t)s * count + 8 * q);
+      hi = hi + *(const f32x4 *)(part + (size_t)s * count + 8 * q + 4);
+    }
+    const float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    if constexpr (OUT == OUT_F32) {
+      *(f32x4 *)((float *)y + 8 * q) = lo;
+      *(f32x4 *)((float *)y + 8 * q + 4) = hi;
+    } else {
+      u32x4 rv = {0, 0, 0, 0};
+      if constexpr (OUT == OUT_NARROW_RES) rv = *(const u32x4 *)(res + 8 * q);
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        uint32_t h[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const float a = v[2 * e + t];
+          uint16_t n = KIND == KIND_F16 ? narrow_f16(a) : f32_to_bf16(a);
+          if constexpr (OUT == OUT_NARROW_RES) {
+            const uint16_t r = (uint16_t)(rv[e] >> (16 * t));
+            const float nv = KIND == KIND_F16 ? widen_f16(n) : bf16_to_f32(n);
+            const float rf = KIND == KIND_F16 ? widen_f16(r) : bf16_to_f32(r);
+            n = KIND == KIND_F16 ? narrow_f16(nv + rf) : f32_to_bf16(nv + rf);
+          }
+          h[t] = n;
+        }
+        o[e] = h[0] | (h[1] << 16);
+      }
+      *(u32x4 *)((uint16_t *)y + 8 * q) = o;
+    }
+  }
 }
 
 // Re-layout of a normal rhs B [K, N] into Bt [N, K] (the NT operand form).
@@ -757,6 +819,21 @@ int launch_gemm_sb(hipStream_t st, GemmArgs args) {
 
 template <int KIND, int OUT, int SB>
 int launch_gemm_tiles(hipStream_t st, GemmArgs args) {
+  // split-K planned by the entry (plan_split, partial area in args.part)
+  if constexpr (KIND != KIND_I8 && SB == 128) {
+    if (args.ksplit > 1) {
+      args.tiles_m = args.m / 256;
+      args.tiles_n = args.n / 256;
+      hipLaunchKernelGGL((gemm_nt_rs_kernel<KIND, OUT, 256, 256, 128, false>),
+                         dim3(args.tiles_m * args.tiles_n * args.ksplit), dim3(256), 0, st, args);
+      WAFER_TRY(launch_status("gemm_nt_rs_kernel"));
+      const int64_t count = (int64_t)args.m * args.n;
+      const unsigned grid = (unsigned)std::min<int64_t>((count / 8 + 255) / 256, 8192);
+      hipLaunchKernelGGL((gemm_fold_kernel<KIND, OUT>), dim3(grid), dim3(256), 0, st, args.part, args.ksplit,
+                         args.res, args.y, count);
+      return launch_status("gemm_fold_kernel");
+    }
+  }
   // 256x256 tiles only where they divide the output and still fill the chip
   if (args.m % 256 == 0 && args.n % 256 == 0 && (args.m / 256) * (args.n / 256) >= 192) {
     args.tiles_m = args.m / 256;
@@ -811,6 +888,34 @@ int launch_gemm_tiles(hipStream_t st, GemmArgs args) {
   else
     hipLaunchKernelGGL((gemm_nt_kernel<KIND, 128, 128, OUT, true, SB, 4, 2>), grid, dim3(512), 0, st, args);
   return launch_status("gemm_nt_kernel");
+}
+
+// Split-K plan for 16-bit GEMMs whose 128x128 grid is at most one round of
+// workgroups and whose K is long: 256x256 tiles on the 4-wave kernel (half
+// the operand bytes per FLOP of 128x128 tiles), each tile's K split over
+// ksplit workgroups so that the grid still fills the CUs, plus a fold
+// launch.  Returns 1 (no split) otherwise.  The decoder layer's down
+// projection (1024 x 4096, K 14336, with the residual): 113.3 us + 14.2 us
+// fold against 136.1 us on 128x128 tiles; 256x128 tiles with two splits
+// (32 MiB of partials instead of 64) measured 138.3 + 9.3 us.
+int plan_split(int m, int n, int kbytes, int cus) {
+  if (m % 256 != 0 || n % 256 != 0 || kbytes < 16384) return 1;
+  const long t2 = (long)(m / 256) * (n / 256), t128 = (long)(m / 128) * (n / 128);
+  if (t128 > cus) return 1;
+  for (int s = 4; s >= 2; --s)
+    if (t2 * s <= cus && kbytes % (256 * s) == 0) return s;  // whole pairs of 128-byte stages per split
+  return 1;
+}
+
+// Sets up args.ksplit / args.part for a 16-bit GEMM (growing the context's
+// partial-tile area when a split is planned).
+int prepare_split(wafer_hip_context *ctx, GemmArgs &args) {
+  const int s = plan_split(args.m, args.n, args.kbytes, ctx->cu_count > 0 ? ctx->cu_count : 256);
+  if (s < 2) return WAFER_HIP_OK;
+  WAFER_TRY(ensure_workspace(ctx, &ctx->partials, &ctx->partials_bytes, (size_t)s * args.m * args.n * sizeof(float)));
+  args.ksplit = s;
+  args.part = (float *)ctx->partials;
+  return WAFER_HIP_OK;
 }
 
 template <int KIND, int OUT>
@@ -885,6 +990,7 @@ extern "C" int wafer_hip_gemm_mfma(wafer_hip_context *ctx, const void *lhs, cons
   const uint8_t *bt = (const uint8_t *)rhs;
   if (rhs_orientation == WAFER_GEMM_NORMAL) WAFER_TRY(relayout_rhs(ctx, rhs, k, n, 2, &bt));
   GemmArgs args{(const uint8_t *)lhs, bt, dst, nullptr, nullptr, (int)m, (int)n, (int)(k * 2), 0, 0};
+  WAFER_TRY(prepare_split(ctx, args));
   const bool f32 = out_format == WAFER_FMT_F32;
   if (in_format == WAFER_FMT_BF16)
     return f32 ? launch_gemm<KIND_BF16, OUT_F32>(ctx->stream, args)
@@ -907,6 +1013,7 @@ extern "C" int wafer_hip_gemm_mfma_residual(wafer_hip_context *ctx, const void *
   if (rhs_orientation == WAFER_GEMM_NORMAL) WAFER_TRY(relayout_rhs(ctx, rhs, k, n, 2, &bt));
   GemmArgs args{(const uint8_t *)lhs, bt, dst, nullptr, nullptr, (int)m, (int)n, (int)(k * 2), 0, 0,
                 (const uint16_t *)residual};
+  WAFER_TRY(prepare_split(ctx, args));
   return in_format == WAFER_FMT_BF16 ? launch_gemm<KIND_BF16, OUT_NARROW_RES>(ctx->stream, args)
                                      : launch_gemm<KIND_F16, OUT_NARROW_RES>(ctx->stream, args);
 }
