@@ -22,7 +22,11 @@
 // or walk that XCD's own column strip in 4-row groups (other grids whose tile
 // rows divide by 4 and tile columns by 8), bounding the XCD's L2 working set.
 // Tiles are 256x256 when they fill the chip, 128x192 where that saves a round
-// of workgroups, else 128x128.
+// of workgroups, else 128x128.  For 16-bit operands the 256x256 and 128x192
+// tiles run on a 4-wave kernel instead (one wave per SIMD, K slices staged
+// through VGPRs into padded LDS rows), and long-K grids of at most one round
+// of 128x128 tiles split K over 4 workgroups of 256x256 tiles with a fold
+// launch.
 //
 // int8 semantics (no reference implementation exists; the closed form on the
 // reference's conversion routes): acc = sum_k int32(a)*int32(b) exactly
