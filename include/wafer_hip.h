@@ -143,11 +143,11 @@ int wafer_hip_gemm_mfma_residual(wafer_hip_context *ctx, const void *lhs,
                                  uint32_t in_format, uint32_t rhs_orientation);
 
 /* MFMA GEMM with SwiGLU fused into the epilogue: rhs_gu is [2*features, k]
- * (Transposed orientation) with rows in 64-row groups, rows 64j + [0,32) the
- * gate rows 32j + [0,32) and rows 64j + 32 + [0,32) the up rows of the same
+ * (Transposed orientation) with rows in 32-row groups, rows 32j + [0,16) the
+ * gate rows 16j + [0,16) and rows 32j + 16 + [0,16) the up rows of the same
  * features; dst [m, features] = bf16(silu_mul(bf16(gate), bf16(up))) -- the
  * two narrowed products followed by the silu_mul region (same bits).  BF16
- * only; features a multiple of 32.  The region is the SwiGLU composition of
+ * only; features a multiple of 16.  The region is the SwiGLU composition of
  * lib/Wafer/Conversion/TileToInstr/ComputeLowering.cpp:2555-2606 after two GEMMs. */
 int wafer_hip_gemm_mfma_swiglu(wafer_hip_context *ctx, const void *lhs,
                                const void *rhs_gu, void *dst, uint32_t m,

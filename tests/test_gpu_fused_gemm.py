@@ -10,8 +10,10 @@ Both sides accumulate the same products in the same MFMA order, so the
 narrowed products are identical and the region arithmetic is the same
 function; any difference is a bug in the epilogue (a wrong column pairing, a
 dropped rounding point, a tail store).  The unfused GEMM itself is held to
-the formal lane in test_gpu_parity.py.  Shapes cover the 256x256 tiles with
-and without ragged m / feature tails and the decoder layer's own shape.
+the formal lane in test_gpu_parity.py.  Shapes cover the 4-wave kernel's
+256x224 and 256x256 tiles (the decoder layer's shape takes 256x224), the
+8-wave kernel's full and ragged (m / feature tail) tiles, and one 16-feature
+group.
 """
 import pytest
 
@@ -46,7 +48,10 @@ def _same_bits(torch, a, b):
     (1024, 4096, 14336),  # decoder layer gate/up (256x256 tiles)
     (256, 512, 512),
     (200, 256, 96),       # ragged m and a feature count that leaves a partial 256-column tile
-    (64, 128, 32),        # one 32-feature group
+    (64, 128, 32),        # two 16-feature groups
+    (64, 128, 16),        # one 16-feature group
+    (512, 1024, 1792),    # 256x224 tiles on the 4-wave kernel (n 3584)
+    (256, 192, 128),      # 8-wave kernel, full tiles (K not a whole pair of 128-byte stages)
 ])
 def test_gemm_swiglu_bit_exact(hip, torch, m, k, f):
     from vibe_compiler_amd import backend as B
@@ -65,8 +70,8 @@ def test_gemm_swiglu_bit_exact(hip, torch, m, k, f):
     buf = torch.full((m * f + 64,), 1.5, dtype=torch.bfloat16, device="cuda")
     hip.gemm_mfma_swiglu(h, wgu, buf[: m * f].view(m, f), m, k, f)
     torch.cuda.synchronize()
-    # the packing itself: 64-row groups of 32 gate rows then 32 up rows
-    g4 = wgu.view(f // 32, 2, 32, k)
+    # the packing itself: 32-row groups of 16 gate rows then 16 up rows
+    g4 = wgu.view(f // 16, 2, 16, k)
     assert torch.equal(g4[:, 0].reshape(f, k), wg) and torch.equal(g4[:, 1].reshape(f, k), wu)
     assert _same_bits(torch, buf[: m * f].view(m, f), ref)
     assert torch.all(buf[m * f:] == 1.5)
@@ -77,7 +82,7 @@ def test_fused_entries_reject_unsupported(hip, torch):
 
     t = torch.zeros(64 * 64, dtype=torch.bfloat16, device="cuda")
     with pytest.raises(B.WaferHipError):
-        hip.gemm_mfma_swiglu(t, t, t, 8, 64, 16)  # features not a multiple of 32
+        hip.gemm_mfma_swiglu(t, t, t, 8, 64, 24)  # features not a multiple of 16
     r = t.view(torch.int16)  # raw 16-bit storage, so the library (not the wrapper) sees F16
     with pytest.raises(B.WaferHipError):
         hip.gemm_mfma_swiglu(r, r, r, 8, 64, 32, in_fmt=B.F16)  # bf16 only

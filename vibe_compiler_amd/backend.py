@@ -360,7 +360,7 @@ class Context:
 
     def gemm_mfma_swiglu(self, lhs, rhs_gu, dst, m, k, features, in_fmt=BF16):
         """dst [m, features] = silu_mul(gate, up) of the gate/up products, with
-        rhs_gu [2*features, k] in 64-row groups (32 gate rows, then the 32 up
+        rhs_gu [2*features, k] in 32-row groups (16 gate rows, then the 16 up
         rows of the same features); see interleave_gate_up."""
         _arg("gemm_mfma_swiglu", "lhs", lhs, in_fmt, m * k)
         _arg("gemm_mfma_swiglu", "rhs_gu", rhs_gu, in_fmt, 2 * features * k)
@@ -372,12 +372,12 @@ class Context:
         """Packs the [features, k] gate and up weights (16-bit) into the
         [2*features, k] operand of gemm_mfma_swiglu with two strided copies."""
         features, k = w_gate.shape
-        if features % 32 or tuple(w_up.shape) != (features, k) or w_gu.numel() != 2 * features * k:
+        if features % 16 or tuple(w_up.shape) != (features, k) or w_gu.numel() != 2 * features * k:
             raise ValueError("interleave_gate_up: shapes")
-        blk = 32 * k * w_gate.element_size()
+        blk = 16 * k * w_gate.element_size()
         for part, w in enumerate((w_gate, w_up)):
-            self.strided_copy(w, w_gu, blk, (blk, 0, 0), (features // 32, 1, 1), (2 * blk, 0, 0),
-                              (features // 32, 1, 1), dst_offset=part * blk)
+            self.strided_copy(w, w_gu, blk, (blk, 0, 0), (features // 16, 1, 1), (2 * blk, 0, 0),
+                              (features // 16, 1, 1), dst_offset=part * blk)
 
     def gemm_i8(self, a, b, scale, y, m, k, n, acc_out=None, rhs_t=False):
         _arg("gemm_i8", "a", a, I8, m * k)

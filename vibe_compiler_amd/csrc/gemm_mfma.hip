@@ -68,10 +68,13 @@ __device__ inline i32x16 mfma<KIND_I8>(u32x4 a, u32x4 b, i32x16 c) {
 }
 
 // Epilogue selectors.
-// OUT_SWIGLU (bf16 only): the rhs rows come in 64-row groups, 32 gate rows
-// then the 32 up rows of the same features, and y[m, f] =
+// OUT_SWIGLU (bf16 only): the rhs rows come in 32-row groups, 16 gate rows
+// then the 16 up rows of the same features, and y[m, f] =
 // bf16(silu_mul(bf16(gate), bf16(up))) over N/2 features (the narrowed
-// products, then the silu_mul region).
+// products, then the silu_mul region).  In a 32x32 MFMA tile the gate
+// values of 16 features sit in lanes l32 < 16 and their up values in lanes
+// l32 + 16; one v_permlane16_swap per register pair brings both to one
+// lane (swiglu_pair).
 // OUT_NARROW_RES: the narrowed product plus a residual tensor of the same
 // format and shape, y = Add(narrow(acc), res) -- the GEMM's narrow output
 // followed by the CT Add command, bit for bit (y may be res itself: every
@@ -88,6 +91,19 @@ __device__ inline float widen_f16(uint16_t h) { return (float)__builtin_bit_cast
 // 0x7e00 as f32_to_f16 does.
 __device__ inline uint16_t narrow_f16(float x) {
   return x != x ? (uint16_t)0x7e00u : __builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
+// SwiGLU from accumulator registers r and r + 1 (r even: rows q and q + 1)
+// of a 32x32 tile whose columns 0..15 are gate and 16..31 up features:
+// v_permlane16_swap exchanges lanes 16..31 of `a` with lanes 0..15 of `b`
+// (and 48..63 with 32..47), after which lane l holds gate and up of feature
+// l % 16 for row q (l % 32 < 16) or q + 1 (l % 32 >= 16).  Returns the bf16
+// silu_mul of the narrowed pair.
+__device__ inline uint16_t swiglu_pair(float a, float b) {
+  const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  const float gv = bf16_to_f32(f32_to_bf16(__uint_as_float(t[0])));
+  const float uv = bf16_to_f32(f32_to_bf16(__uint_as_float(t[1])));
+  return f32_to_bf16(silu_mul_1(gv, uv));
 }
 
 struct GemmArgs {
@@ -193,16 +209,15 @@ __device__ __attribute__((always_inline)) inline void gemm_store(
       };
       if constexpr (OUT == OUT_SWIGLU) {
         static_assert(KIND == KIND_BF16, "the fused epilogue serves bf16");
+        const int hi = (l32 >> 4) & 1;  // lanes 16..31 of each half take the odd row
 #pragma unroll
         for (int i = 0; i < WTM; ++i)
 #pragma unroll
-          for (int jp = 0; jp < WTN / 2; ++jp)
+          for (int j = 0; j < WTN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const float gv = bf16_to_f32(f32_to_bf16((float)acc[i][2 * jp][r]));
-              const float uv = bf16_to_f32(f32_to_bf16((float)acc[i][2 * jp + 1][r]));
-              put(i * 32 + 8 * (r >> 2) + 4 * g + (r & 3), jp * 32 + l32, f32_to_bf16(silu_mul_1(gv, uv)));
-            }
+            for (int r = 0; r < 16; r += 2)
+              put(i * 32 + 8 * (r >> 2) + 4 * g + (r & 3) + hi, j * 16 + (l32 & 15),
+                  swiglu_pair((float)acc[i][j][r], (float)acc[i][j][r + 1]));
       } else {
 #pragma unroll
         for (int j = 0; j < WTN; ++j) {
@@ -256,24 +271,23 @@ __device__ __attribute__((always_inline)) inline void gemm_store(
   }
   // epilogue: lane holds column l32 and rows 8*(r/4) + 4*g + r%4 of each tile
   if constexpr (OUT == OUT_SWIGLU) {
-    // a wave's 32-column tiles 2 jp and 2 jp + 1 are the gate and up columns
-    // of the same 32 features
-    static_assert(WTN % 2 == 0, "SwiGLU pairs need two 32-column tiles per wave");
+    // each 32-column tile holds 16 features (gate columns 0..15, up 16..31)
     static_assert(KIND == KIND_BF16, "the fused epilogues serve bf16");
     const int nf = args.n / 2;
+    const int hi = (l32 >> 4) & 1;
 #pragma unroll
     for (int i = 0; i < WTM; ++i)
 #pragma unroll
-      for (int jp = 0; jp < WTN / 2; ++jp) {
-        const int feat = (n0 + wn * (BN / WN) + jp * 64) / 2 + l32;
+      for (int j = 0; j < WTN; ++j) {
+        const int feat = (n0 + wn * (BN / WN) + j * 32) / 2 + (l32 & 15);
         const bool col_ok = !TAIL || feat < nf;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        for (int r = 0; r < 16; r += 2) {
+          // every lane takes part in the swap before the tail test
+          const uint16_t v = swiglu_pair((float)acc[i][j][r], (float)acc[i][j][r + 1]);
+          const int row = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3) + hi;
           if (TAIL && !(col_ok && row < args.m)) continue;
-          const float gv = bf16_to_f32(f32_to_bf16((float)acc[i][2 * jp][r]));
-          const float uv = bf16_to_f32(f32_to_bf16((float)acc[i][2 * jp + 1][r]));
-          ((uint16_t *)args.y)[(size_t)row * nf + feat] = f32_to_bf16(silu_mul_1(gv, uv));
+          ((uint16_t *)args.y)[(size_t)row * nf + feat] = v;
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -488,17 +502,19 @@ gemm_nt_kernel(GemmArgs args) {
 }
 
 // Scheduling pins for one k-step of the 4-wave kernel: slot t holds one
-// MFMA, then (t+1) NR / NM - t NR / NM fragment reads and the same share of X
-// other memory operations of mask XM.
-template <int T, int NM, int NR, int X, int XM>
+// MFMA, then (t+1) NR / NM - t NR / NM fragment reads and the same shares of
+// XL buffer loads and XW LDS writes.
+template <int T, int NM, int NR, int XL, int XW>
 __device__ __attribute__((always_inline)) inline void pin_slots() {
   if constexpr (T < NM) {
     constexpr int nr = ((T + 1) * NR) / NM - (T * NR) / NM;
-    constexpr int nx = ((T + 1) * X) / NM - (T * X) / NM;
+    constexpr int nl = ((T + 1) * XL) / NM - (T * XL) / NM;
+    constexpr int nw = ((T + 1) * XW) / NM - (T * XW) / NM;
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     if constexpr (nr > 0) __builtin_amdgcn_sched_group_barrier(0x100, nr, 0);
-    if constexpr (nx > 0) __builtin_amdgcn_sched_group_barrier(XM, nx, 0);
-    pin_slots<T + 1, NM, NR, X, XM>();
+    if constexpr (nl > 0) __builtin_amdgcn_sched_group_barrier(0x020, nl, 0);
+    if constexpr (nw > 0) __builtin_amdgcn_sched_group_barrier(0x200, nw, 0);
+    pin_slots<T + 1, NM, NR, XL, XW>();
   }
 }
 
@@ -516,13 +532,16 @@ __device__ __attribute__((always_inline)) inline void pin_slots() {
 // keeps the 8-wave kernel: this one measured slower for it, its dequant
 // epilogue spilling the accumulators).  STAGE selects the LDS-staged
 // epilogue (else per-element stores).
-template <int KIND, int OUT, int BM, int BN, int SB, bool STAGE>
+template <int KIND, int OUT, int BM, int BN, int SB, bool STAGE, int WM = 2, int WN = 2>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_nt_rs_kernel(GemmArgs args) {
-  constexpr int WM = 2, WN = 2, PITCH = SB + 16, KS = SB / 32, CH = SB / 16, RPI = 64 / CH;
+  static_assert(WM * WN == 4, "four waves");
+  constexpr int PITCH = SB + 16, KS = SB / 32, CH = SB / 16, RPI = 64 / CH;
   constexpr int WTM = BM / WM / 32, WTN = BN / WN / 32;
   constexpr int A_INSTR = BM / RPI, B_INSTR = BN / RPI;  // RPI rows of SB bytes per wave instruction
   constexpr int PER_WAVE = (A_INSTR + B_INSTR) / 4, NR = WTM + WTN, NM = WTM * WTN;
-  constexpr int LK = KS / 2, LPK = PER_WAVE / LK;        // k-steps carrying loads, loads per such k-step
+  // k-steps carrying loads (the first half, else the first KS - 1, else the first) and loads per such k-step
+  constexpr int LK = PER_WAVE % (KS / 2) == 0 ? KS / 2 : PER_WAVE % (KS - 1) == 0 ? KS - 1 : 1;
+  constexpr int LPK = PER_WAVE / LK;
   constexpr int WK = KS - 2;                             // the k-step that writes the older set to LDS
   static_assert((A_INSTR + B_INSTR) % 4 == 0 && PER_WAVE % LK == 0, "loads split evenly");
   constexpr int OC = OUT == OUT_SWIGLU ? BN / WN / 2 : BN / WN;
@@ -601,9 +620,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       for (int j = 0; j < WTN; ++j) acc[i][j] = mfma<KIND>(fa[f][i], fb[f][j], acc[i][j]);
   };
   // pins one k-step's order: NM slots of one MFMA followed by their share of
-  // the NR fragment reads and of X other memory operations (mask XM)
-  auto pin = [&](auto X, auto XM) __attribute__((always_inline)) {
-    pin_slots<0, NM, NR, decltype(X)::value, decltype(XM)::value>();
+  // the NR fragment reads, XL loads and XW LDS writes
+  auto pin = [&](auto XL, auto XW) __attribute__((always_inline)) {
+    pin_slots<0, NM, NR, decltype(XL)::value, decltype(XW)::value>();
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -633,10 +652,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
           asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER_WAVE) : "memory");
           lwrite(p ^ 1, p ^ 1);
         }
-        if (ks < LK) {
-          pin(std::integral_constant<int, LPK>{}, std::integral_constant<int, 0x020>{});
+        constexpr int zero = 0;
+        (void)zero;
+        if (ks < LK && ks == WK) {
+          pin(std::integral_constant<int, LPK>{}, std::integral_constant<int, PER_WAVE>{});
+        } else if (ks < LK) {
+          pin(std::integral_constant<int, LPK>{}, std::integral_constant<int, 0>{});
         } else if (ks == WK) {
-          pin(std::integral_constant<int, PER_WAVE>{}, std::integral_constant<int, 0x200>{});
+          pin(std::integral_constant<int, 0>{}, std::integral_constant<int, PER_WAVE>{});
         } else {
           pin(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
         }
@@ -807,7 +830,22 @@ int launch_gemm_sb(hipStream_t st, GemmArgs args) {
   if constexpr (OUT != OUT_SWIGLU) {
     return launch_gemm_tiles<KIND, OUT, SB>(st, args);
   } else {
-    // gate/up column pairs need 64 columns per wave: 256x256 tiles always
+    // 256x224 tiles (4 x 1 waves of 64 x 224) where their rounds of 256
+    // workgroups take less time than those of 256x256 tiles (gate/up at
+    // n 28672: 512 tiles in two rounds of 7/8 the work, against 448 tiles
+    // whose second round is three quarters full)
+    if constexpr (SB == 128) {
+      if (args.m % 256 == 0 && args.n % 224 == 0 && args.kbytes % 256 == 0) {
+        const long t224 = (long)(args.m / 256) * (args.n / 224), t256 = (long)(args.m / 256) * ((args.n + 255) / 256);
+        if (7 * ((t224 + 255) / 256) < 8 * ((t256 + 255) / 256)) {
+          args.tiles_m = args.m / 256;
+          args.tiles_n = args.n / 224;
+          hipLaunchKernelGGL((gemm_nt_rs_kernel<KIND, OUT, 256, 224, 128, false, 4, 1>),
+                             dim3(args.tiles_m * args.tiles_n), dim3(256), 0, st, args);
+          return launch_status("gemm_nt_rs_kernel");
+        }
+      }
+    }
     args.tiles_m = (args.m + 255) / 256;
     args.tiles_n = (args.n + 255) / 256;
     const dim3 grid(args.tiles_m * args.tiles_n);
@@ -1029,8 +1067,8 @@ extern "C" int wafer_hip_gemm_mfma_swiglu(wafer_hip_context *ctx, const void *lh
   if (in_format != WAFER_FMT_BF16)
     return fail(WAFER_HIP_E_UNSUPPORTED, "gemm_mfma_swiglu: input format must be BF16");
   if (!lhs || !rhs_gu || !dst) return fail(WAFER_HIP_E_INVALID_FIELD, "gemm_mfma_swiglu: null tensor");
-  if (features == 0 || features % 32)
-    return fail(WAFER_HIP_E_UNSUPPORTED, "gemm_mfma_swiglu: features must be a positive multiple of 32");
+  if (features == 0 || features % 16)
+    return fail(WAFER_HIP_E_UNSUPPORTED, "gemm_mfma_swiglu: features must be a positive multiple of 16");
   if (features > 0x3fffffffu) return fail(WAFER_HIP_E_INVALID_FIELD, "gemm_mfma_swiglu: output too large");
   WAFER_TRY(check_shape(m, k, 2 * features, 2, "gemm_mfma_swiglu"));
   WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));

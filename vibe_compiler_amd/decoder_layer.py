@@ -31,7 +31,7 @@ evaluation of the same layer within the attention tolerance, not bit for bit.
 Weights are kept in the nn.Linear orientation [out, in] (rhs Transpose for
 the GEMM), so no re-layout pass runs per call; the gate and up weights are
 packed once, in the constructor, into the [2*ffn, hidden] operand of the
-fused SwiGLU GEMM (64-row groups of 32 gate and 32 up rows).  All buffers are
+fused SwiGLU GEMM (32-row groups of 16 gate and 16 up rows).  All buffers are
 allocated once in the constructor; ``forward`` launches only.
 """
 from __future__ import annotations
