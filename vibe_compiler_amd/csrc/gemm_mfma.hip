@@ -532,7 +532,7 @@ __device__ __attribute__((always_inline)) inline void pin_slots() {
 // keeps the 8-wave kernel: this one measured slower for it, its dequant
 // epilogue spilling the accumulators).  STAGE selects the LDS-staged
 // epilogue (else per-element stores).
-template <int KIND, int OUT, int BM, int BN, int SB, bool STAGE, int WM = 2, int WN = 2>
+template <int KIND, int OUT, int BM, int BN, int SB, bool STAGE, int WM = 2, int WN = 2, bool SPLIT = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_nt_rs_kernel(GemmArgs args) {
   static_assert(WM * WN == 4, "four waves");
   constexpr int PITCH = SB + 16, KS = SB / 32, CH = SB / 16, RPI = 64 / CH;
@@ -549,7 +549,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   __shared__ __align__(16) uint8_t lds[2 * (BM + BN) * PITCH];
   // split-K: workgroup ids [s tiles, (s + 1) tiles) take split s
   const int tiles = args.tiles_m * args.tiles_n;
-  const int split = args.ksplit > 1 ? (int)blockIdx.x / tiles : 0;
+  const int split = SPLIT ? (int)blockIdx.x / tiles : 0;
   int tm, tn;
   tile_coords(args, (int)blockIdx.x - split * tiles, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
@@ -568,7 +568,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
   // row stride kb; this workgroup's K slice starts at byte k0 and spans nkt stages
   const int kb = args.kbytes;
-  const int kchunk = args.ksplit > 1 ? kb / args.ksplit : kb;
+  const int kchunk = SPLIT ? kb / args.ksplit : kb;
   const int k0 = split * kchunk, nkt = kchunk / SB;
   const __amdgpu_buffer_rsrc_t ra =
       __builtin_amdgcn_make_buffer_rsrc((void *)(args.a + (size_t)m0 * kb + k0), 0, BM * kb - k0, 0x00020000);
@@ -677,7 +677,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     stage(kt + 1, std::integral_constant<int, 1>{});
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if (args.ksplit > 1) {
+  if constexpr (SPLIT) {
     GemmArgs pa = args;
     pa.y = args.part + (size_t)split * args.m * args.n;
     gemm_store<KIND, BM, BN, OUT_F32, false, WM, WN, false>(pa, acc, m0, n0, nullptr);
@@ -866,7 +866,7 @@ int launch_gemm_tiles(hipStream_t st, GemmArgs args) {
     if (args.ksplit > 1) {
       args.tiles_m = args.m / 256;
       args.tiles_n = args.n / 256;
-      hipLaunchKernelGGL((gemm_nt_rs_kernel<KIND, OUT, 256, 256, 128, false>),
+      hipLaunchKernelGGL((gemm_nt_rs_kernel<KIND, OUT_F32, 256, 256, 128, false, 2, 2, true>),
                          dim3(args.tiles_m * args.tiles_n * args.ksplit), dim3(256), 0, st, args);
       WAFER_TRY(launch_status("gemm_nt_rs_kernel"));
       const int64_t count = (int64_t)args.m * args.n;
