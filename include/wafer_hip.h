@@ -125,7 +125,12 @@ int wafer_hip_gemm(wafer_hip_context *ctx, const void *lhs, const void *rhs,
  * wafer_hip_gemm with lhs Normal; the MFMA accumulation order differs from
  * the formal k-order, so results match the formal lane within tolerance.
  * out_format F32 or the input format.  Any m, n; k a multiple of 32 (64-byte
- * K stages); other k return WAFER_HIP_E_UNSUPPORTED. */
+ * K stages); other k return WAFER_HIP_E_UNSUPPORTED.  Long-K shapes whose
+ * 128x128 grid is at most one round of workgroups (k * 2 >= 16384 bytes, m
+ * and n multiples of 256) split K over 4 workgroups with f32 partials in a
+ * context-owned area (4 * m * n * 4 bytes, grown on first use; growing is
+ * refused on a capturing stream, so a caller that captures runs the shape
+ * once eagerly first).  Results repeat bit for bit for a given shape. */
 int wafer_hip_gemm_mfma(wafer_hip_context *ctx, const void *lhs,
                         const void *rhs, void *dst, uint32_t m, uint32_t k,
                         uint32_t n, uint32_t in_format, uint32_t out_format,
