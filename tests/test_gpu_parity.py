@@ -382,6 +382,37 @@ def test_i8_gemm_baseline_size_y_only(hip, B, oracle, rt):
     assert np.array_equal(host(acc).astype(np.int64).sum(0), colsum)
 
 
+@pytest.mark.parametrize("m,k,n", [(3072, 128, 4096), (4096, 384, 3072), (4096, 1152, 4096)])
+def test_i8_gemm_kn_rhs_in_place(hip, B, oracle, m, k, n):
+    """A [K, N] rhs on >= 192 whole 256x256 tiles is read in place (the
+    transposing LDS reads, no re-layout pass): y and the accumulator over
+    the whole output equal the run on the same rhs stored [N, K], and the
+    int64 closed form on sampled rows; one, three and nine 128-byte K
+    stages."""
+    say("i8 gemm [K,N] in place", m, k, n)
+    rng = np.random.default_rng(m * 7 + k + n)
+    a = rng.integers(-128, 128, size=(m, k), dtype=np.int64).astype(np.int8)
+    b = rng.integers(-128, 128, size=(k, n), dtype=np.int64).astype(np.int8)
+    scale = rng.uniform(0.001, 0.01, size=n).astype(np.float32)
+    ad, sd = dev(a), dev(scale)
+    outs = []
+    for rt, bb in ((0, b), (1, np.ascontiguousarray(b.T))):
+        acc = torch.full((m, n), 0x5a5a5a5a, dtype=torch.int32, device="cuda")
+        y = torch.full((m, n), 0x1234, dtype=torch.int16, device="cuda")
+        hip.gemm_i8(ad, dev(bb), sd, y, m, k, n, acc_out=acc, rhs_t=bool(rt))
+        y_only = torch.full((m, n), 0x1234, dtype=torch.int16, device="cuda")
+        hip.gemm_i8(ad, dev(bb), sd, y_only, m, k, n, rhs_t=bool(rt))
+        outs.append((host(acc), host(y).view(np.uint16), host(y_only).view(np.uint16)))
+    (acc0, y0, yo0), (acc1, y1, yo1) = outs
+    assert np.array_equal(acc0, acc1)
+    assert np.array_equal(y0, y1) and np.array_equal(yo0, yo1) and np.array_equal(y0, yo0)
+    rows = np.concatenate([[0, 1, 255, 256, m - 1], rng.choice(m, 11, replace=False)])
+    exact = a[rows].astype(np.int64) @ b.astype(np.int64)
+    assert np.array_equal(acc0[rows], exact.astype(np.int32))
+    yr = oracle.f32_to_bf16((exact.astype(np.float32) * scale).astype(np.float32)).reshape(exact.shape)
+    assert np.array_equal(y0[rows], yr)
+
+
 @pytest.mark.parametrize("m,k,n,rt", [(100, 192, 130, 0), (1, 64, 1, 1), (300, 128, 257, 0), (129, 256, 200, 1),
                                       (257, 64, 128, 0), (130, 320, 384, 1), (64, 128, 1000, 0)])
 def test_i8_gemm_ragged_bit_exact(hip, B, oracle, m, k, n, rt):

@@ -42,6 +42,8 @@ namespace wafer {
 namespace {
 
 enum { KIND_BF16 = 0, KIND_F16 = 1, KIND_I8 = 2 };
+typedef int v2i32 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i32 lds_v2i32;
 constexpr int BKB = 64;  // K bytes must be a multiple of the smaller LDS stage
 
 template <int KIND> struct Acc;
@@ -108,7 +110,7 @@ __device__ inline uint16_t swiglu_pair(float a, float b) {
 
 struct GemmArgs {
   const uint8_t *a;    // [M, K] elements, K-contiguous
-  const uint8_t *bt;   // [N, K]
+  const uint8_t *bt;   // [N, K] ([K, N] for the BKN int8 kernel)
   void *y;             // [M, N]
   int32_t *acc_out;    // int8 only, optional [M, N]
   const float *scale;  // int8 only, [N]
@@ -338,9 +340,21 @@ __device__ __attribute__((always_inline)) inline void gemm_store(
 // two per SIMD) by default; 4 x 2 serves tiles whose width is not a multiple
 // of 128 (128 x 192, 128 x 384); 2 x 2 (4 waves, one per SIMD with all 512
 // registers) halves the LDS fragment traffic per MFMA.
-template <int KIND, int BM, int BN, int OUT, bool TAIL, int SB, int WM = 2, int WN = 4>
+//
+// BKN (int8, 256-column tiles): the rhs is read as stored, [K, N] row-major
+// (`bt` points at it), with no re-layout pass.  A B stage then holds SB rows
+// of K, BN bytes each; 16-byte chunk c of k-row r sits at position
+// c ^ 2 (r & 7).  The MFMA's B fragment (16 consecutive k of one column) is
+// gathered by two ds_read_b64_tr_b8: in each 16-lane group lane i addresses
+// k-row i / 2, bytes 8 (i % 2) .. +7 of one chunk, and receives byte i of
+// each of the 8 rows, so the 16 lanes get 8 k of the chunk's 16 columns.
+// The 8 rows of a group sit at 8 distinct chunk positions of one parity, and
+// the neighbouring group (the next chunk) at the other parity: no bank
+// conflicts.
+template <int KIND, int BM, int BN, int OUT, bool TAIL, int SB, int WM = 2, int WN = 4, bool BKN = false>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(1, WM * WN == 4 ? 1 : 2))) void
 gemm_nt_kernel(GemmArgs args) {
+  static_assert(!BKN || (KIND == KIND_I8 && BN == 256 && !TAIL && (BN / WN) % 32 == 0), "[K,N] rhs: int8, 256 columns");
   constexpr int NT = 64 * WM * WN, NW = WM * WN;
   static_assert(BM % (32 * WM) == 0 && BN % (32 * WN) == 0, "whole 32x32 MFMA tiles per wave");
   constexpr int WTM = BM / WM / 32, WTN = BN / WN / 32;  // 32x32 MFMA tiles per wave
@@ -386,7 +400,8 @@ gemm_nt_kernel(GemmArgs args) {
   const int nkt = args.kbytes / SB;
   const size_t kb = (size_t)args.kbytes;
   const uint8_t *abase = args.a + (size_t)m0 * kb;
-  const uint8_t *bbase = args.bt + (size_t)n0 * kb;
+  const uint8_t *bbase = BKN ? args.bt + n0 : args.bt + (size_t)n0 * kb;
+  const uint32_t npitch = (uint32_t)args.n;  // [K, N] rhs row pitch
   const int dma_row = lane / CH, dma_pos = lane % CH;
   // last row of the tile that exists in A / Bt (BM - 1 / BN - 1 unless TAIL)
   const int last_a = TAIL ? min(BM, args.m - m0) - 1 : BM - 1;
@@ -402,7 +417,15 @@ gemm_nt_kernel(GemmArgs args) {
       const int row = (is_a ? ins : ins - A_INSTR) * RPI + dma_row;
       const int chunk = swz(row, dma_pos);
       const int src_row = TAIL ? min(row, is_a ? last_a : last_b) : row;
-      const uint8_t *src = (is_a ? abase : bbase) + (src_row * kb32 + koff + chunk * 16);
+      const uint8_t *src;
+      if constexpr (BKN) {
+        // B: k-row koff + kr, 16-byte chunks of a 256-byte row
+        const int kr = (ins - A_INSTR) * (1024 / BN) + lane / 16;
+        const uint32_t loff = is_a ? src_row * kb32 + chunk * 16 : kr * npitch + (((lane & 15) ^ (2 * (kr & 7))) * 16);
+        src = (is_a ? abase + koff : bbase + (size_t)koff * npitch) + loff;
+      } else {
+        src = (is_a ? abase : bbase) + (src_row * kb32 + koff + chunk * 16);
+      }
       u32x4 *dst = is_a ? &sA[st][(ins * RPI) * CH] : &sB[st][((ins - A_INSTR) * RPI) * CH];
       __builtin_amdgcn_global_load_lds((const void *)src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
     }
@@ -416,10 +439,26 @@ gemm_nt_kernel(GemmArgs args) {
       const int row = wm * (BM / WM) + i * 32 + l32;
       fa[f][i] = sA[buf][row * CH + swz(row, chunk)];
     }
+    if constexpr (BKN) {
+      // k-rows 32 ks + 16 g + 8 h + lane % 16 / 2 (h = 0, 1), chunk of
+      // columns wn * BN / WN + 32 j + 16 (lane / 16 % 2); the row's swizzle
+      // is 2 (row & 7) = 2 (lane % 16 / 2)
+      const char *sb = (const char *)&sB[buf][0];
+      const int l16 = lane & 15;
 #pragma unroll
-    for (int j = 0; j < WTN; ++j) {
-      const int row = wn * (BN / WN) + j * 32 + l32;
-      fb[f][j] = sB[buf][row * CH + swz(row, chunk)];
+      for (int j = 0; j < WTN; ++j) {
+        const int c = (wn * (BN / WN) + j * 32) / 16 + ((lane >> 4) & 1);
+        const int off = (ks * 32 + 16 * g + (l16 >> 1)) * BN + ((c ^ (2 * (l16 >> 1))) * 16) + 8 * (l16 & 1);
+        const v2i32 lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i32 *)(sb + off));
+        const v2i32 hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i32 *)(sb + off + 8 * BN));
+        fb[f][j] = __builtin_bit_cast(u32x4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < WTN; ++j) {
+        const int row = wn * (BN / WN) + j * 32 + l32;
+        fb[f][j] = sB[buf][row * CH + swz(row, chunk)];
+      }
     }
   };
   auto mfmas = [&](int f) __attribute__((always_inline)) {
@@ -436,7 +475,7 @@ gemm_nt_kernel(GemmArgs args) {
   // keep the compiler from moving MFMAs across the barrier; sched_group_barrier
   // pins the interleave (masks: 0x008 MFMA, 0x100 LDS read, 0x010 VMEM,
   // which covers the DMA issues).
-  constexpr int NR = WTM + WTN;                  // fragment reads per k-step
+  constexpr int NR = WTM + (BKN ? 2 : 1) * WTN;  // fragment reads per k-step
   constexpr int DKS = KS > 2 ? KS - 2 : 1;       // k-steps that carry DMA issues
   constexpr int NV = (PER_WAVE + DKS - 1) / DKS;  // DMA issues per such k-step
 #pragma unroll
@@ -1087,6 +1126,16 @@ extern "C" int wafer_hip_gemm_i8(wafer_hip_context *ctx, const int8_t *a, const 
   WAFER_TRY(check_shape(m, k, n, 1, "gemm_i8"));
   WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
   const uint8_t *bt = (const uint8_t *)b;
+  // a [K, N] rhs on whole 256x256 tiles that fill the chip: read in place
+  if (rhs_orientation == WAFER_GEMM_NORMAL && m % 256 == 0 && n % 256 == 0 && k % 128 == 0 &&
+      (m / 256) * (n / 256) >= 192) {
+    GemmArgs args{(const uint8_t *)a, bt, y, acc_out, scale, (int)m, (int)n, (int)k, 0, 0};
+    args.tiles_m = (int)(m / 256);
+    args.tiles_n = (int)(n / 256);
+    hipLaunchKernelGGL((gemm_nt_kernel<KIND_I8, 256, 256, OUT_I8_DEQUANT, false, 128, 2, 4, true>),
+                       dim3(args.tiles_m * args.tiles_n), dim3(512), 0, ctx->stream, args);
+    return launch_status("gemm_nt_kernel");
+  }
   if (rhs_orientation == WAFER_GEMM_NORMAL) WAFER_TRY(relayout_rhs(ctx, b, k, n, 1, &bt));
   GemmArgs args{(const uint8_t *)a, bt, y, acc_out, scale, (int)m, (int)n, (int)k, 0, 0};
   return launch_gemm<KIND_I8, OUT_I8_DEQUANT>(ctx->stream, args);
