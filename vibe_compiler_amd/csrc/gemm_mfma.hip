@@ -568,8 +568,9 @@ __device__ __attribute__((always_inline)) inline void pin_slots() {
 // consecutive rows read at one 16-byte chunk hit all 64 banks once and every
 // fragment address is a per-lane base plus an immediate.  K bytes a multiple
 // of 2 SB (an even number of stages); full tiles only.  16-bit operands (int8
-// keeps the 8-wave kernel: this one measured slower for it, its dequant
-// epilogue spilling the accumulators).  STAGE selects the LDS-staged
+// keeps the 8-wave kernel: with the per-element dequant epilogue compiled in
+// this one spills the accumulators, and with the staged epilogue alone it is
+// bit-identical but no faster at 4096^3).  STAGE selects the LDS-staged
 // epilogue (else per-element stores).
 template <int KIND, int OUT, int BM, int BN, int SB, bool STAGE, int WM = 2, int WN = 2, bool SPLIT = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_nt_rs_kernel(GemmArgs args) {
