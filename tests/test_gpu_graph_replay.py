@@ -6,7 +6,6 @@ and every replay's output must be bit-identical to the eager run's."""
 
 import math
 
-import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu
@@ -119,3 +118,18 @@ def test_mfma_gemm_split_k_graph_replay(hip, B):
     y, y2 = (torch.empty((m, n), dtype=torch.float32, device="cuda") for _ in range(2))
     replay_matches_eager(lambda: hip.gemm_mfma(a, bt, y, m, k, n, in_fmt=B.BF16, out_fmt=B.F32, rhs_t=True), y,
                          lambda: hip.gemm_mfma(a2, bt, y2, m, k, n, in_fmt=B.BF16, out_fmt=B.F32, rhs_t=True))
+
+
+def test_decoder_layer_graph_replay(hip):
+    """The decoder layer forward (config 4: 8 backend calls, 9 kernels,
+    split-K partials and the layer's intermediates reused across calls)."""
+    say("graph replay: decoder layer")
+    from vibe_compiler_amd import decoder_layer as DL
+
+    gen = torch.Generator(device="cuda").manual_seed(15)
+    W = DL.random_weights(torch, gen)
+    x = torch.randn((1024, 4096), device="cuda", generator=gen).to(torch.bfloat16)
+    x2 = torch.randn((1024, 4096), device="cuda", generator=gen).to(torch.bfloat16)
+    y, y2 = torch.empty_like(x), torch.empty_like(x)
+    layer = DL.DecoderLayer(hip, W, 1024)
+    replay_matches_eager(lambda: layer.forward(x, y), y, lambda: layer.forward(x2, y2))
