@@ -172,6 +172,32 @@ def test_strided_copy_tiled_transpose(hip, oracle, inner):
         assert np.array_equal(host(d), want)
 
 
+@pytest.mark.parametrize("n0,n1,n2,pad,flip", [(64, 64, 1, 0, 0), (128, 192, 3, 16, 0), (192, 64, 2, 32, 1),
+                                               (64, 512, 2, 16, 0), (256, 128, 1, 48, 1), (64, 128, 2, 2, 0)])
+def test_strided_copy_transpose_b16_tiles(hip, oracle, n0, n1, n2, pad, flip):
+    # 2-byte transposes on whole 64x64 tiles: 16-byte aligned pitches take
+    # the vector kernel (padded rows, a batch axis, both orientations); a
+    # 2-byte pad breaks the alignment and takes the element kernel
+    rng = np.random.default_rng(n0 * 3 + n1 + n2 + pad)
+    ss = [2, 2 * n0 + pad, 0]
+    ss[2] = ss[1] * n1 + pad
+    ds = [2 * n1 + pad, 2, 0]
+    ds[2] = ds[0] * n0 + pad
+    it = [n0, n1, n2]
+    if flip:
+        ss, ds = ds, ss
+    say("b16 tile transpose", ss, ds, it)
+    src_bytes = 2 + sum((i - 1) * s for s, i in zip(ss, it))
+    dst_bytes = 2 + sum((i - 1) * s for s, i in zip(ds, it))
+    src = rng.integers(0, 256, src_bytes, dtype=np.uint8)
+    dst = rng.integers(0, 256, dst_bytes, dtype=np.uint8)
+    st, want = oracle.strided_copy(src, dst, 2, ss, it, ds, it)
+    assert st == 0
+    d = dev(dst)
+    hip.strided_copy(dev(src), d, 2, ss, it, ds, it)
+    assert np.array_equal(host(d), want)
+
+
 def test_strided_copy_snapshot_in_one_buffer(hip, oracle):
     rng = np.random.default_rng(11)
     for inner, so, do in [(16, 0, 32), (16, 64, 0), (4, 0, 4), (2, 6, 0), (3, 0, 5)]:

@@ -140,6 +140,59 @@ __global__ __launch_bounds__(256) void transpose_tile_kernel(const uint8_t *__re
   }
 }
 
+// 2-byte segments on whole 64x64 tiles with 16-byte aligned rows: both
+// sides move 16-byte vectors.  The LDS holds a tile as 64 rows (b) of 128
+// bytes (a), 16-byte chunk c of row r at position c ^ (r / 8 % 8): a row
+// pair of one ds_write_b128 group fills the 64 banks once, and the 8 rows
+// 8 i + q (i = 0..7) that one read instruction gathers a column from sit at
+// 8 distinct chunk positions.  Thread t stores 8 b-consecutive elements of
+// destination row a0 + j, 8 threads per 128-byte row segment.  A workgroup
+// walks TB tiles along b through two LDS buffers (one barrier per tile), the
+// next tile's loads issued before the current tile's stores.
+template <int TB>
+__global__ __launch_bounds__(256) void transpose_b16x64_kernel(const uint8_t *__restrict__ src,
+                                                               uint8_t *__restrict__ dst, uint32_t tiles_a,
+                                                               uint64_t src_b, uint64_t dst_a, uint64_t src_2,
+                                                               uint64_t dst_2) {
+  __shared__ __align__(16) uint8_t tile[2][64 * 128];
+  const uint32_t a0 = (blockIdx.x % tiles_a) * 64, bt0 = (blockIdx.x / tiles_a) * (64 * TB);
+  const uint8_t *s = src + (uint64_t)blockIdx.y * src_2;
+  uint8_t *d = dst + (uint64_t)blockIdx.y * dst_2;
+  const int t = threadIdx.x;
+  u32x4 v[2];
+  auto load = [&](int u) __attribute__((always_inline)) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int r = p * 32 + t / 8, c = t % 8;
+      v[p] = *(const u32x4 *)(s + (uint64_t)(bt0 + 64 * u + r) * src_b + (uint64_t)(a0 + 8 * c) * 2);
+    }
+  };
+  load(0);
+#pragma unroll
+  for (int u = 0; u < TB; ++u) {
+    uint8_t *buf = tile[u & 1];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int r = p * 32 + t / 8, c = t % 8;
+      *(u32x4 *)(buf + r * 128 + ((c ^ ((r >> 3) & 7)) << 4)) = v[p];
+    }
+    __syncthreads();
+    if (u + 1 < TB) load(u + 1);
+    const uint32_t b0 = bt0 + 64 * u;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int j = p * 32 + t / 8, i = t % 8;
+      const uint8_t *col = buf + (((j >> 3) ^ i) << 4) + 2 * (j & 7);
+      uint32_t w[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        w[q] = (uint32_t)*(const uint16_t *)(col + (8 * i + 2 * q) * 128) |
+               ((uint32_t)*(const uint16_t *)(col + (8 * i + 2 * q + 1) * 128) << 16);
+      *(u32x4 *)(d + (uint64_t)(a0 + j) * dst_a + (uint64_t)(b0 + 8 * i) * 2) = u32x4{w[0], w[1], w[2], w[3]};
+    }
+  }
+}
+
 // bits of 1.0 in a float format (APFloat::getOne bit pattern)
 uint32_t one_bits(uint32_t format) {
   return format == WAFER_FMT_F16 ? 0x3c00u : format == WAFER_FMT_BF16 ? 0x3f80u : 0x3f800000u;
@@ -275,6 +328,20 @@ void launch_transpose(hipStream_t stream, const uint8_t *src, uint8_t *dst, int 
   const int b = 1 - a;
   const uint32_t n_a = (uint32_t)s.it[a], n_b = (uint32_t)s.it[b];
   const uint32_t tiles_a = (n_a + TILE - 1) / TILE, tiles_b = (n_b + TILE - 1) / TILE;
+  if constexpr (E == 2) {
+    const bool batch = s.it[2] > 1;
+    if (n_a % 64 == 0 && n_b % 64 == 0 && s.stride[b] % 16 == 0 && d.stride[a] % 16 == 0 &&
+        (!batch || (s.stride[2] % 16 == 0 && d.stride[2] % 16 == 0)) && ((uintptr_t)src & 15) == 0 &&
+        ((uintptr_t)dst & 15) == 0) {
+      if (tiles_b % 4 == 0)
+        hipLaunchKernelGGL(transpose_b16x64_kernel<4>, dim3(tiles_a * (tiles_b / 4), (uint32_t)s.it[2]), dim3(256), 0,
+                           stream, src, dst, tiles_a, s.stride[b], d.stride[a], s.stride[2], d.stride[2]);
+      else
+        hipLaunchKernelGGL(transpose_b16x64_kernel<1>, dim3(tiles_a * tiles_b, (uint32_t)s.it[2]), dim3(256), 0,
+                           stream, src, dst, tiles_a, s.stride[b], d.stride[a], s.stride[2], d.stride[2]);
+      return;
+    }
+  }
   hipLaunchKernelGGL((transpose_tile_kernel<E, TILE>), dim3(tiles_a * tiles_b, (uint32_t)s.it[2]), dim3(256), 0,
                      stream, src, dst, n_a, n_b, tiles_a, s.stride[a], s.stride[b], d.stride[a], d.stride[b],
                      s.stride[2], d.stride[2]);
