@@ -432,6 +432,33 @@ int wafer_hip_attention_decode_noalloc(wafer_hip_context *ctx, uint32_t format,
                                        uint32_t kv_capacity, uint32_t head_dim,
                                        float scale, uint32_t chunks);
 
+/* Decode step with the functional KV-cache append the compiler requires of a
+ * flash-decoding function (classifyAlgorithm,
+ * lib/Wafer/Transforms/Linalg/AttentionMatching.cpp:1385-1437: each of K and
+ * V is returned as insert_slice(new, insert_slice(past, ...)) along the
+ * sequence axis, as in the board cases attention-causal-decode-two-tokens and
+ * attention-decode-kv-cache, test/Board/PyTorch/wafer_pytorch_board_cases.py:
+ * 1098-1135, 1138-1360).  The caches are updated in place: rows
+ * [past_len, past_len + tokens) of each (batch, kv head) of k_cache / v_cache
+ * take k_new / v_new [batch, kv_heads, tokens, head_dim] byte for byte; the
+ * first past_len rows are not written (the reference's validate demands the
+ * prefix bit for bit).  Then attention of q [batch, q_heads, tokens,
+ * head_dim] over the first past_len + tokens cache rows with query i seeing
+ * keys j <= past_len + i (SDPA causal_lower_right; one token sees them all):
+ * one token with head_dim 128 runs FD decode with `chunks` chunks
+ * (wafer_hip_attention_decode), anything else the masked FA prefill
+ * (wafer_hip_attention_prefill_masked, causal diagonal past_len, kv_capacity
+ * the cache capacity).  o [batch, q_heads, tokens, head_dim].  format BF16 or
+ * F16; head_dim 1..64 or 128; past_len + tokens <= kv_capacity. */
+int wafer_hip_attention_decode_append(wafer_hip_context *ctx, uint32_t format,
+                                      const void *q, const void *k_new,
+                                      const void *v_new, void *k_cache,
+                                      void *v_cache, void *o, uint32_t batch,
+                                      uint32_t q_heads, uint32_t kv_heads,
+                                      uint32_t tokens, uint32_t past_len,
+                                      uint32_t kv_capacity, uint32_t head_dim,
+                                      float scale, uint32_t chunks);
+
 /* ---- region entries: fused TileRegions ----------------------------------------
  * Compositions of the managed elementwise / reduce commands with the op
  * mapping of getInstrElementwiseKindAttr

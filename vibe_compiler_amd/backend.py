@@ -49,7 +49,7 @@ EXPORTS = (
     "wafer_hip_compare_expected", "wafer_hip_compare_statistics", "wafer_hip_environment",
     "wafer_hip_first_nan", "wafer_hip_attention_decode_noalloc", "wafer_hip_attention_prefill_masked",
     "wafer_hip_elementwise_formal", "wafer_hip_pool", "wafer_hip_add_rmsnorm", "wafer_hip_attention_prefill_strided",
-    "wafer_hip_gemm_mfma_residual", "wafer_hip_gemm_f32_mfma",
+    "wafer_hip_gemm_mfma_residual", "wafer_hip_gemm_f32_mfma", "wafer_hip_attention_decode_append",
 )
 
 # wafer_hip_gemm_f32_mfma epilogues
@@ -171,6 +171,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.wafer_hip_attention_prefill_strided.argtypes = [vp, u32, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32, u32,
                                                       ctypes.POINTER(AttentionStrides)]
     L.wafer_hip_attention_decode_noalloc.argtypes = [vp, u32, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32, u32]
+    L.wafer_hip_attention_decode_append.argtypes = [vp, u32, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32,
+                                                    u32, f32, u32]
     L.wafer_hip_rmsnorm.argtypes = [vp, u32, vp, vp, vp, u64, u64, f32]
     L.wafer_hip_softmax.argtypes = [vp, u32, vp, vp, u64, u64]
     L.wafer_hip_add_rmsnorm.argtypes = [vp, u32, vp, vp, vp, vp, vp, u64, u64, f32]
@@ -544,6 +546,27 @@ class Context:
             _arg("attention_decode", name, t, fmt, n)
         _check(self._L.wafer_hip_attention_decode(self._bind(), fmt, _p(q), _p(k_cache), _p(v_cache),
                                                   _p(o), B, Hq, Hkv, kv_len, cap, D, float(scale), chunks))
+
+    def attention_decode_append(self, q, k_new, v_new, k_cache, v_cache, o, scale, past_len, chunks=16, fmt=BF16):
+        """One decode step with the functional KV append: k_new / v_new [batch, kv_heads, tokens, head_dim] are
+        written into rows [past_len, past_len + tokens) of the caches [batch, kv_heads, cap, head_dim] (earlier
+        rows untouched), then q [batch, q_heads, tokens, head_dim] attends to the first past_len + tokens rows
+        with query i seeing keys j <= past_len + i."""
+        B, Hq, T, D = q.shape
+        _, Hkv, cap, _ = k_cache.shape
+        if tuple(k_new.shape) != (B, Hkv, T, D) or tuple(v_new.shape) != (B, Hkv, T, D) or \
+                tuple(v_cache.shape) != tuple(k_cache.shape) or k_cache.shape[0] != B or k_cache.shape[3] != D or \
+                tuple(o.shape) != tuple(q.shape) or not 0 <= past_len <= cap - T:
+            raise ValueError("attention_decode_append: q/o [batch, q_heads, tokens, head_dim], new K/V [batch, "
+                             "kv_heads, tokens, head_dim], caches [batch, kv_heads, cap, head_dim], past_len + tokens "
+                             "<= cap")
+        for name, t, n in (("q", q, B * Hq * T * D), ("k_new", k_new, B * Hkv * T * D),
+                           ("v_new", v_new, B * Hkv * T * D), ("k_cache", k_cache, B * Hkv * cap * D),
+                           ("v_cache", v_cache, B * Hkv * cap * D), ("o", o, B * Hq * T * D)):
+            _arg("attention_decode_append", name, t, fmt, n)
+        _check(self._L.wafer_hip_attention_decode_append(self._bind(), fmt, _p(q), _p(k_new), _p(v_new), _p(k_cache),
+                                                         _p(v_cache), _p(o), B, Hq, Hkv, T, past_len, cap, D,
+                                                         float(scale), chunks))
 
     def attention_decode_noalloc(self, q, k_cache, v_cache, o, scale, chunks=16, kv_len=None, fmt=BF16):
         """attention_decode with the library's static scratch for chunk

@@ -464,6 +464,34 @@ int decode(wafer_hip_context *ctx, uint32_t format, const void *q, const void *k
   return launch_status("fd_fold_d128");
 }
 
+// The functional KV-cache append of a decode step: rows
+// [past_len, past_len + tokens) of every (batch, kv head) of both caches take
+// the new tokens' K / V rows, byte for byte; the rows before past_len are not
+// touched.  One thread per 16-byte piece when rows are whole 16-byte vectors
+// (VEC), else per element.
+template <bool VEC>
+__global__ __launch_bounds__(256) void kv_append_kernel(const uint16_t *__restrict__ k_new,
+                                                        const uint16_t *__restrict__ v_new, uint16_t *k_cache,
+                                                        uint16_t *v_cache, int64_t pieces, int piece_elems,
+                                                        int row_pieces, int tokens, int past_len, int capacity) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= pieces) return;
+  // piece i of the new tensors [bh][token][row_pieces]
+  const int64_t row = i / row_pieces;          // bh * tokens + token
+  const int64_t bh = row / tokens;
+  const int64_t tok = row - bh * tokens;
+  const int64_t within = i - row * row_pieces;  // piece within the row
+  const int64_t dst = ((bh * capacity + past_len + tok) * row_pieces + within) * piece_elems;
+  const int64_t src = i * piece_elems;
+  if constexpr (VEC) {
+    *(u32x4 *)(k_cache + dst) = *(const u32x4 *)(k_new + src);
+    *(u32x4 *)(v_cache + dst) = *(const u32x4 *)(v_new + src);
+  } else {
+    k_cache[dst] = k_new[src];
+    v_cache[dst] = v_new[src];
+  }
+}
+
 }  // namespace
 }  // namespace wafer
 
@@ -487,4 +515,62 @@ extern "C" int wafer_hip_attention_decode_noalloc(wafer_hip_context *ctx, uint32
                                                   uint32_t head_dim, float scale, uint32_t chunks) {
   return decode(ctx, format, q, k_cache, v_cache, o, batch, q_heads, kv_heads, kv_len, kv_capacity, head_dim, scale,
                 chunks, true);
+}
+
+extern "C" int wafer_hip_attention_decode_append(wafer_hip_context *ctx, uint32_t format, const void *q,
+                                                 const void *k_new, const void *v_new, void *k_cache,
+                                                 void *v_cache, void *o, uint32_t batch, uint32_t q_heads,
+                                                 uint32_t kv_heads, uint32_t tokens, uint32_t past_len,
+                                                 uint32_t kv_capacity, uint32_t head_dim, float scale,
+                                                 uint32_t chunks) {
+  WAFER_CHECK_CTX(ctx);
+  if (format != WAFER_FMT_BF16 && format != WAFER_FMT_F16)
+    return fail(WAFER_HIP_E_UNSUPPORTED, "attention_decode_append: storage must be BF16 or F16");
+  if (!q || !k_new || !v_new || !k_cache || !v_cache || !o)
+    return fail(WAFER_HIP_E_INVALID_FIELD, "attention_decode_append: null tensor");
+  if (batch == 0 || q_heads == 0 || kv_heads == 0 || tokens == 0 || head_dim == 0 || chunks == 0)
+    return fail(WAFER_HIP_E_INVALID_FIELD, "attention_decode_append: empty dimension");
+  if (q_heads % kv_heads != 0)
+    return fail(WAFER_HIP_E_INVALID_FIELD, "attention_decode_append: q_heads % kv_heads != 0");
+  if ((uint64_t)past_len + tokens > kv_capacity)
+    return fail(WAFER_HIP_E_INVALID_FIELD, "attention_decode_append: past_len + tokens exceeds kv_capacity");
+  if (head_dim > 128 || (head_dim > 64 && head_dim < 128))
+    return fail(WAFER_HIP_E_UNSUPPORTED, "attention_decode_append: head_dim must be 1..64 or 128");
+  if (!(scale > 0.0f)) return fail(WAFER_HIP_E_INVALID_FIELD, "attention_decode_append: scale must be positive");
+  const bool fd = tokens == 1 && head_dim == D;
+  if (fd) {
+    const uint32_t G = q_heads / kv_heads;
+    if (G != 1 && G != 2 && G != 4 && G != 8)
+      return fail(WAFER_HIP_E_UNSUPPORTED, "attention_decode_append: q_heads/kv_heads must be 1, 2, 4 or 8");
+    if (chunks > 65535 || kv_heads > 65535 || batch > 65535)
+      return fail(WAFER_HIP_E_INVALID_FIELD, "attention_decode_append: grid dimension above 65535");
+  }
+  WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
+  // the append: whole 16-byte pieces when every row is, else per element
+  const bool vec = head_dim % 8 == 0 &&
+                   (((uintptr_t)k_new | (uintptr_t)v_new | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15) == 0;
+  const int piece_elems = vec ? 8 : 1;
+  const int row_pieces = (int)head_dim / piece_elems;
+  const int64_t pieces = (int64_t)batch * kv_heads * tokens * row_pieces;
+  const dim3 grid((unsigned)((pieces + 255) / 256));
+  if (vec)
+    hipLaunchKernelGGL(kv_append_kernel<true>, grid, dim3(256), 0, ctx->stream, (const uint16_t *)k_new,
+                       (const uint16_t *)v_new, (uint16_t *)k_cache, (uint16_t *)v_cache, pieces, piece_elems,
+                       row_pieces, (int)tokens, (int)past_len, (int)kv_capacity);
+  else
+    hipLaunchKernelGGL(kv_append_kernel<false>, grid, dim3(256), 0, ctx->stream, (const uint16_t *)k_new,
+                       (const uint16_t *)v_new, (uint16_t *)k_cache, (uint16_t *)v_cache, pieces, piece_elems,
+                       row_pieces, (int)tokens, (int)past_len, (int)kv_capacity);
+  WAFER_TRY(launch_status("kv_append_kernel"));
+  // attention over the updated caches: query i sees keys j <= past_len + i
+  // (lower-right causal), so one token sees the whole cache
+  if (fd)
+    return decode(ctx, format, q, k_cache, v_cache, o, batch, q_heads, kv_heads, past_len + 1, kv_capacity, head_dim,
+                  scale, chunks, false);
+  wafer_hip_attention_mask mask{};
+  mask.flags = WAFER_HIP_ATT_CAUSAL;
+  mask.kv_capacity = kv_capacity;
+  mask.causal_diagonal = past_len;
+  return attention_prefill_masked(ctx, format, q, k_cache, v_cache, o, batch, q_heads, kv_heads, tokens,
+                                  past_len + tokens, head_dim, scale, &mask);
 }
