@@ -150,9 +150,9 @@ int wafer_hip_gemm_mfma_residual(wafer_hip_context *ctx, const void *lhs,
 /* MFMA GEMM with SwiGLU fused into the epilogue: rhs_gu is [2*features, k]
  * (Transposed orientation) with rows in 32-row groups, rows 32j + [0,16) the
  * gate rows 16j + [0,16) and rows 32j + 16 + [0,16) the up rows of the same
- * features; dst [m, features] = bf16(silu_mul(bf16(gate), bf16(up))) -- the
- * two narrowed products followed by the silu_mul region (same bits).  BF16
- * only; features a multiple of 16.  The region is the SwiGLU composition of
+ * features; dst [m, features] = T(silu_mul(T(gate), T(up))), T = in_format
+ * (BF16 or F16) -- the two narrowed products followed by the silu_mul region
+ * (same bits); features a multiple of 16.  The region is the SwiGLU composition of
  * lib/Wafer/Conversion/TileToInstr/ComputeLowering.cpp:2555-2606 after two GEMMs. */
 int wafer_hip_gemm_mfma_swiglu(wafer_hip_context *ctx, const void *lhs,
                                const void *rhs_gu, void *dst, uint32_t m,
@@ -326,8 +326,8 @@ int wafer_hip_unpack(wafer_hip_context *ctx, uint32_t format, uint32_t layout,
  * h / (q_heads/kv_heads)).  Causal: query i sees key j iff j <= i (and
  * j < kv_len).  format BF16 or F16 (the compiler's F16/BF16 attention
  * formation, include/Wafer/IR/LinalgExt/AttentionOps.td:42-46); head_dim 128
- * or 1..64; any q_len, kv_len >= 1 (kv_len up to 8388607).  BF16 with
- * head_dim 128 runs the dedicated kernel, every other case the kernels of
+ * or 1..64; any q_len, kv_len >= 1 (kv_len up to 8388607).  head_dim 128
+ * (BF16 or F16) runs the dedicated kernel, every other case the kernels of
  * wafer_hip_attention_prefill_masked with the causal flag alone. */
 int wafer_hip_attention_prefill(wafer_hip_context *ctx, uint32_t format,
                                 const void *q, const void *k, const void *v,
@@ -339,8 +339,8 @@ int wafer_hip_attention_prefill(wafer_hip_context *ctx, uint32_t format,
  * row) for each of Q, K, V and O, so a caller can pass head slices of a
  * token-major projection ([T, heads * 128] rows) and receive a token-major
  * output without re-layout steps.  Same kernel walk, so the bits equal
- * wafer_hip_attention_prefill on the densely re-laid-out tensors.  BF16,
- * head_dim 128; strides non-negative multiples of 8, row strides >= 128,
+ * wafer_hip_attention_prefill on the densely re-laid-out tensors.  BF16 or
+ * F16, head_dim 128; strides non-negative multiples of 8, row strides >= 128,
  * 16-byte aligned tensors.  Additive (the reference's attention op has no
  * layout operands); a decoder block's V and O re-layouts are what it removes. */
 typedef struct wafer_hip_attention_strides {

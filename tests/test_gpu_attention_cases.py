@@ -153,8 +153,8 @@ def test_reference_attention_case(hip, oracle, case, fmt):
     got = run_masked(hip, fmt, q, k, v, scale, **kw)
     attention_gate(tof(oracle, fmt, got), tof(oracle, fmt, ref), what=f"{name} masked")
     if mode in ("causal", "none") and valid is None:
-        # the plain entry: BF16 head_dim 128 takes its own kernel, the rest
-        # the masked kernels with the causal flag alone
+        # the plain entry: head_dim 128 takes its own kernel, the rest the
+        # masked kernels with the causal flag alone
         o = torch.full(q.shape, 0x7E00, dtype=torch.int16, device="cuda")
         hip.attention_prefill(u16(q), u16(k), u16(v), o, scale, causal=mode == "causal", fmt=fmt)
         attention_gate(tof(oracle, fmt, back(o)), tof(oracle, fmt, ref), what=f"{name} plain")
@@ -231,7 +231,8 @@ def test_valid_prefix_never_reads_the_tail(hip, oracle, fmt, D):
 @pytest.mark.parametrize("fmt", [F16, BF16], ids=["f16", "bf16"])
 def test_config1_shape_f16_and_masked_bf16(hip, oracle, fmt):
     """The headline shape [1, 16, 2048, 128] causal through the masked entry
-    (and, for F16, the plain entry, which routes there), against the oracle."""
+    and through the plain entry (the dedicated head_dim-128 kernel, F16 and
+    BF16), each against the oracle."""
     say("config-1 shape masked", fmt)
     rng = np.random.default_rng(51)
     q, k, v = inputs(oracle, rng, fmt, 16, 16, 2048, 2048, 128)
@@ -239,10 +240,9 @@ def test_config1_shape_f16_and_masked_bf16(hip, oracle, fmt):
     ref = oracle.attention_prefill_ex(q, k, v, scale, causal=True, fmt=fmt)
     got = run_masked(hip, fmt, q, k, v, scale, causal=True)
     attention_gate(tof(oracle, fmt, got), tof(oracle, fmt, ref), what="config-1 masked")
-    if fmt == F16:
-        o = torch.full(q.shape, 0x7E00, dtype=torch.int16, device="cuda")
-        hip.attention_prefill(u16(q), u16(k), u16(v), o, scale, causal=True, fmt=fmt)
-        assert np.array_equal(back(o), got)
+    o = torch.full(q.shape, 0x7E00, dtype=torch.int16, device="cuda")
+    hip.attention_prefill(u16(q), u16(k), u16(v), o, scale, causal=True, fmt=fmt)
+    attention_gate(tof(oracle, fmt, back(o)), tof(oracle, fmt, ref), what="config-1 plain")
 
 
 def test_diagonal_past_the_keys_is_noncausal(hip, oracle):
@@ -326,37 +326,48 @@ def test_fd_decode_storage_formats(hip, oracle, fmt, Bn, Hq, Hkv, L, cap, chunks
 
 
 # ---------------------------------------------------------------- strided FA
-@pytest.mark.parametrize("Bn,Hq,Hkv,S,causal", [(1, 32, 8, 1024, True), (2, 4, 2, 300, True), (1, 2, 1, 130, False)])
-def test_strided_prefill_equals_dense(hip, B, Bn, Hq, Hkv, S, causal):
+@pytest.mark.parametrize("fmt", [F16, BF16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("Bn,Hq,Hkv,S,causal", [(1, 32, 8, 1024, True), (2, 4, 2, 300, True), (1, 2, 1, 130, False),
+                                                 (1, 32, 32, 16, True)])
+def test_strided_prefill_equals_dense(hip, B, oracle, fmt, Bn, Hq, Hkv, S, causal):
     """wafer_hip_attention_prefill_strided on head slices of token-major
     projection rows (Q, K, V inside one [B, S, (Hq + 2 Hkv) 128] buffer, O
     written into token-major [B, S, Hq 128] rows) gives the bits of the dense
-    entry on the re-laid-out tensors (same kernel walk)."""
-    say("strided prefill", Bn, Hq, Hkv, S, causal)
+    entry on the re-laid-out tensors (same kernel walk); the first head
+    against the oracle."""
+    say("strided prefill", fmt, Bn, Hq, Hkv, S, causal)
     D = 128
+    dt = torch.bfloat16 if fmt == BF16 else torch.float16
     gen = torch.Generator(device="cuda").manual_seed(Bn * 1000 + Hq * 10 + S)
     n = (Hq + 2 * Hkv) * D
-    qkv = torch.randn(Bn, S, n, generator=gen, device="cuda").to(torch.bfloat16)
+    qkv = torch.randn(Bn, S, n, generator=gen, device="cuda").to(dt)
     qv = qkv[:, :, :Hq * D].view(Bn, S, Hq, D).permute(0, 2, 1, 3)
     kv_ = qkv[:, :, Hq * D:(Hq + Hkv) * D].view(Bn, S, Hkv, D).permute(0, 2, 1, 3)
     vv = qkv[:, :, (Hq + Hkv) * D:].view(Bn, S, Hkv, D).permute(0, 2, 1, 3)
-    out = torch.full((Bn, S, Hq * D + 8), 5.0, dtype=torch.bfloat16, device="cuda")  # padded rows
+    out = torch.full((Bn, S, Hq * D + 8), 5.0, dtype=dt, device="cuda")  # padded rows
     ov = out[:, :, :Hq * D].view(Bn, S, Hq, D).permute(0, 2, 1, 3)
     scale = 1 / math.sqrt(D)
-    hip.attention_prefill_strided(qv, kv_, vv, ov, scale, causal=causal)
-    od = torch.empty(Bn, Hq, S, D, dtype=torch.bfloat16, device="cuda")
-    hip.attention_prefill(qv.contiguous(), kv_.contiguous(), vv.contiguous(), od, scale, causal=causal)
+    hip.attention_prefill_strided(qv, kv_, vv, ov, scale, causal=causal, fmt=fmt)
+    od = torch.empty(Bn, Hq, S, D, dtype=dt, device="cuda")
+    hip.attention_prefill(qv.contiguous(), kv_.contiguous(), vv.contiguous(), od, scale, causal=causal, fmt=fmt)
     torch.cuda.synchronize()
     assert torch.equal(ov.contiguous().view(torch.int16), od.view(torch.int16))
     assert torch.all(out[:, :, Hq * D:] == 5.0)  # the row padding is untouched
+    bits = lambda t: back(t[:1, :1].contiguous().view(torch.int16))
+    ref = oracle.attention_prefill(bits(qv), bits(kv_), bits(vv), scale, causal=causal, block_k=64, fmt=fmt)
+    attention_gate(tof(oracle, fmt, bits(ov)), tof(oracle, fmt, ref), what="strided head 0")
 
 
 def test_strided_prefill_rejections(hip, B):
     say("strided prefill rejections")
     D = 128
     q = torch.zeros(1, 2, 64, D, dtype=torch.bfloat16, device="cuda")
-    with pytest.raises(B.WaferHipError) as e:  # F16 storage: not served by this entry
-        hip.attention_prefill_strided(q, q, q, q.clone(), 0.1, fmt=B.F16)
+    q64 = torch.zeros(1, 2, 64, 64, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(B.WaferHipError) as e:  # head_dim 64: not served by this entry
+        hip.attention_prefill_strided(q64, q64, q64, q64.clone(), 0.1)
+    assert e.value.status == -3
+    with pytest.raises(B.WaferHipError) as e:  # F32 storage
+        hip.attention_prefill_strided(q, q, q, q.clone(), 0.1, fmt=B.F32)
     assert e.value.status == -3
     big = torch.zeros(64, 2 * D + 4, dtype=torch.bfloat16, device="cuda")  # row stride 260: not a multiple of 8
     v = big[:, :2 * D].view(64, 2, D).permute(1, 0, 2)[None]

@@ -101,12 +101,12 @@ __device__ inline f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
 template <typename T>
 __device__ inline uint32_t pack2(float lo, float hi) {
   typedef T t2 __attribute__((ext_vector_type(2)));
-  const t2 v = {(T)lo, (T)hi};
+  const t2 v = {(T)f32_rounded(lo), (T)f32_rounded(hi)};
   return __builtin_bit_cast(uint32_t, v);
 }
 template <typename T>
 __device__ inline float round_to(float x) {
-  return (float)(T)x;
+  return (float)(T)f32_rounded(x);
 }
 template <typename T>
 __device__ inline float load_elem(const uint16_t *p) {
@@ -688,7 +688,7 @@ __global__ __launch_bounds__(SMALL_ROWS) void fa_small(const FaArgs a, int D, in
   uint16_t *orow = a.o + ((size_t)bh * a.q_len + i) * D;
 #pragma unroll
   for (int d = 0; d < SMALL_D; ++d)
-    if (d < D) orow[d] = __builtin_bit_cast(uint16_t, (T)(acc[d] * coef));
+    if (d < D) orow[d] = __builtin_bit_cast(uint16_t, (T)f32_rounded(acc[d] * coef));
 }
 
 }  // namespace

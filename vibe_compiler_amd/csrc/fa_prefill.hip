@@ -6,8 +6,9 @@
 // lib/Wafer/Transforms/Linalg/OnlineAttentionMaterialization.cpp:197-262):
 //   per KV block: S = q.k (f32 accumulate), S = S*scale (+0/-inf causal bias),
 //   m' = max(m, rowmax S), alpha = ExpLp(m - m'), P = ExpLp(S - m'),
-//   l = l*alpha + rowsum(P) (unrounded P), acc = acc*alpha + bf16(P).V,
-//   out = bf16(acc * (1/l)), 0 for a row with l == 0.
+//   l = l*alpha + rowsum(P) (unrounded P), acc = acc*alpha + T(P).V,
+//   out = T(acc * (1/l)), 0 for a row with l == 0; T the storage format
+//   (bf16 or f16, both RNE).
 // The two partial states of interleaved key sets combine with the state
 // merge of OnlineAttentionMaterialization.cpp:264-373: m = max(mL, mR),
 // sL = ExpLp(mL - m), sR = ExpLp(mR - m), l = lL sL + lR sR,
@@ -28,12 +29,12 @@
 //    MFMA and VALU work interleave; at the end of a phase the two key halves
 //    of a query tile merge through LDS;
 //  * scores are computed transposed, S^T = K . Q^T, on
-//    v_mfma_f32_16x16x32_bf16 (A = 16 keys x 32 d from LDS, B = Q^T kept in
+//    v_mfma_f32_16x16x32_{bf16,f16} (A = 16 keys x 32 d from LDS, B = Q^T kept in
 //    VGPRs): each lane holds 16 scores of one query, the 4 lanes of a query
 //    combine with permlane16/permlane32 swaps;
 //  * the output is accumulated transposed as well, O^T = V^T . P^T: P^T feeds
 //    the MFMA B operand straight from the score registers after RNE narrowing
-//    (v_cvt_pk_bf16_f32), and the V^T operand comes from row-major V in LDS
+//    (v_cvt_pk_{bf16,f16}_f32), and the V^T operand comes from row-major V in LDS
 //    through the transposing read ds_read_b64_tr_b16 (within each 16-lane
 //    group, lane i receives element i%4 of the 4-element vectors at the
 //    addresses of lanes 4e + i/4, e = 0..3);
@@ -55,8 +56,8 @@
 // exp2(fma(s_raw, scale*log2e, -m_ref*scale*log2e)) (one rounding fewer than
 // the reference's mul, sub, mul chain); the difference is below 1 ulp of the
 // f32 argument and far inside the attention tolerance.  With the lazy
-// reference P <= 2^8 and its bf16 rounding point differs from the
-// reference's, with the same relative bound.
+// reference P <= 2^8 and its rounding point in T differs from the
+// reference's, with the same relative bound (2^8 is far inside f16's range).
 #include "common.h"
 
 #include <type_traits>
@@ -101,14 +102,40 @@ __device__ inline float xor16_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// 16x16x32 MFMA on 8-element fragments of the storage type T
+template <typename T>
+__device__ inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (std::is_same_v<T, __bf16>)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+}
+// output narrowing: bf16 by the reference's codec (canonical NaN 0x7fc0);
+// f16 by v_cvt_f16_f32 (RNE, gradual underflow, overflow to inf), a NaN to
+// the canonical 0x7e00
+template <typename T>
+__device__ inline uint32_t narrow_pair(float lo, float hi) {
+  if constexpr (std::is_same_v<T, __bf16>) {
+    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+  } else {
+    lo = f32_rounded(lo);
+    hi = f32_rounded(hi);
+    const uint32_t l = lo != lo ? 0x7e00u : __builtin_bit_cast(uint16_t, (_Float16)lo);
+    const uint32_t h = hi != hi ? 0x7e00u : __builtin_bit_cast(uint16_t, (_Float16)hi);
+    return l | (h << 16);
+  }
+}
+
 // Element strides (batch, head, row) of Q, K, V and O for the STRIDED
 // instantiation; the other reads the dense [B, H, S, 128] layout.
 struct FaStrides {
   int64_t q[3], k[3], v[3], o[3];
 };
 
-template <bool CAUSAL, bool STRIDED = false>
-__global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
+template <typename T, bool CAUSAL, bool STRIDED = false>
+__global__ __launch_bounds__(THREADS) void fa_prefill_d128(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, uint16_t *__restrict__ O, int q_heads, int kv_heads,
     int q_len, int kv_len, float c, int bh_count, int n_qblocks, const FaStrides st = FaStrides{}) {
@@ -146,13 +173,13 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
 
   // Q^T as the MFMA B operand: lane holds query l16, d = 32 s + 8 g + [0,8)
   // (rows past q_len load the last row and are never stored)
-  bf16x8 qreg[4];
+  u32x4 qreg[4];
   int q0 = qb_a * QB + qt * 16;
   auto load_q = [&]() __attribute__((always_inline)) {
     const int row = min(q0 + l16, q_len - 1);
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      qreg[s] = *(const bf16x8 *)(Qp + (size_t)row * q_rs + s * 32 + g * 8);
+      qreg[s] = *(const u32x4 *)(Qp + (size_t)row * q_rs + s * 32 + g * 8);
   };
   load_q();
 
@@ -244,16 +271,16 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
       for (int j = 0; j < 4; ++j) sacc[kt][j] = 0.0f;
-    bf16x8 kf[4][4], vf[2][8];
+    u32x4 kf[4][4], vf[2][8];
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) kf[s][kt] = *(const bf16x8 *)(sk + k_off[s] + kt * 4096);
+      for (int kt = 0; kt < 4; ++kt) kf[s][kt] = *(const u32x4 *)(sk + k_off[s] + kt * 4096);
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
-        sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[s][kt], qreg[s], sacc[kt], 0, 0, 0);
+        sacc[kt] = mfma16<T>(kf[s][kt], qreg[s], sacc[kt]);
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
@@ -262,7 +289,7 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
             (lds_v4i16 *)(sv + v_off[dt] + (32 * s) * 256));
         const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (lds_v4i16 *)(sv + v_off[dt] + (32 * s + 16) * 256));
-        vf[s][dt] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        vf[s][dt] = __builtin_bit_cast(u32x4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
     kdma();
     __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 16, 0);
@@ -315,19 +342,23 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     l_part += rsum;
     // P^T operand of k-step s: slots 8 g + [0,4) are keys 32 s + 4 g + [0,4)
     // (tile 2 s), slots 8 g + [4,8) keys 32 s + 16 + 4 g + [0,4) (tile 2 s + 1)
-    bf16x8 pb[2];
+    typedef T t8 __attribute__((ext_vector_type(8)));
+    u32x4 pb[2];
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+    for (int s = 0; s < 2; ++s) {
+      t8 x;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        pb[s][j] = (__bf16)p[2 * s][j];
-        pb[s][4 + j] = (__bf16)p[2 * s + 1][j];
+        x[j] = (T)p[2 * s][j];
+        x[4 + j] = (T)p[2 * s + 1][j];
       }
+      pb[s] = __builtin_bit_cast(u32x4, x);
+    }
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt)
-        acc_o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[s][dt], pb[s], acc_o[dt], 0, 0, 0);
+        acc_o[dt] = mfma16<T>(vf[s][dt], pb[s], acc_o[dt]);
     vdma();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -362,7 +393,7 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
     const float s0 = __builtin_amdgcn_exp2f(mc_ref - e);
     const float s1 = __builtin_amdgcn_exp2f(m1 - e);
     const float l = xor16_sum(xor32_sum(l_part * s0 + l1 * s1));
-    // finalize: coefficient = Recip(l) (0 for an empty row), out = bf16(acc * coef)
+    // finalize: coefficient = Recip(l) (0 for an empty row), out = T(acc * coef)
     const float coef = (l == 0.0f) ? 0.0f : 1.0f / l;
     uint16_t *orow = (STRIDED ? O + b * st.o[0] + h * st.o[1] + (int64_t)(q0 + l16) * st.o[2]
                               : O + ((size_t)bh * q_len + q0 + l16) * D) + 4 * g;
@@ -374,8 +405,8 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
 #pragma unroll
       for (int j = 0; j < 4; ++j) r[j] = (acc_o[dt][j] * s0 + o[j] * s1) * coef;
       u32x2 packed;
-      packed[0] = (uint32_t)f32_to_bf16(r[0]) | ((uint32_t)f32_to_bf16(r[1]) << 16);
-      packed[1] = (uint32_t)f32_to_bf16(r[2]) | ((uint32_t)f32_to_bf16(r[3]) << 16);
+      packed[0] = narrow_pair<T>(r[0], r[1]);
+      packed[1] = narrow_pair<T>(r[2], r[3]);
       if (q0 + l16 < q_len) *(u32x2 *)(orow + dt * 16) = packed;
     }
     if (!last) lds_barrier();  // exchange reads done before the buffers are reused
@@ -437,6 +468,27 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_bf16_d128(
   finish((float *)&sbuf[0][0][0], true);
 }
 
+// one launch of the kernel for the storage format (BF16 or F16)
+template <bool STRIDED>
+int launch_fa(wafer_hip_context *ctx, uint32_t format, bool causal, const void *q, const void *k, const void *v,
+              void *o, uint32_t q_heads, uint32_t kv_heads, uint32_t q_len, uint32_t kv_len, float c, int bh_count,
+              int n_qblocks, const FaStrides &st) {
+  dim3 grid((unsigned)(bh_count * ((n_qblocks + 1) / 2)));  // one workgroup per pair of query blocks
+#define FA_GO(T, CZ)                                                                                           \
+  hipLaunchKernelGGL((fa_prefill_d128<T, CZ, STRIDED>), grid, dim3(THREADS), 0, ctx->stream, (const uint16_t *)q, \
+                     (const uint16_t *)k, (const uint16_t *)v, (uint16_t *)o, (int)q_heads, (int)kv_heads,      \
+                     (int)q_len, (int)kv_len, c, bh_count, n_qblocks, st)
+  if (format == WAFER_FMT_BF16) {
+    if (causal) FA_GO(__bf16, true);
+    else FA_GO(__bf16, false);
+  } else {
+    if (causal) FA_GO(_Float16, true);
+    else FA_GO(_Float16, false);
+  }
+#undef FA_GO
+  return launch_status("fa_prefill_d128");
+}
+
 }  // namespace
 }  // namespace wafer
 
@@ -449,7 +501,7 @@ extern "C" int wafer_hip_attention_prefill(wafer_hip_context *ctx, uint32_t form
                                            uint32_t kv_len, uint32_t head_dim,
                                            float scale, uint32_t causal) {
   WAFER_CHECK_CTX(ctx);
-  if (format != WAFER_FMT_BF16 || head_dim != D) {
+  if ((format != WAFER_FMT_BF16 && format != WAFER_FMT_F16) || head_dim != D) {
     wafer_hip_attention_mask mask{};
     mask.flags = causal ? WAFER_HIP_ATT_CAUSAL : 0u;
     return attention_prefill_masked(ctx, format, q, k, v, o, batch, q_heads, kv_heads, q_len, kv_len, head_dim,
@@ -470,16 +522,8 @@ extern "C" int wafer_hip_attention_prefill(wafer_hip_context *ctx, uint32_t form
   const int n_qblocks = (int)n_qblocks64;
   const int bh_count = (int)(batch * q_heads);
   const float c = scale * 0x1.715476p+0f;
-  dim3 grid((unsigned)(bh_count * ((n_qblocks + 1) / 2)));  // one workgroup per pair of query blocks
-  if (causal)
-    hipLaunchKernelGGL(fa_prefill_bf16_d128<true>, grid, dim3(THREADS), 0, ctx->stream,
-                       (const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)v, (uint16_t *)o,
-                       (int)q_heads, (int)kv_heads, (int)q_len, (int)kv_len, c, bh_count, n_qblocks);
-  else
-    hipLaunchKernelGGL(fa_prefill_bf16_d128<false>, grid, dim3(THREADS), 0, ctx->stream,
-                       (const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)v, (uint16_t *)o,
-                       (int)q_heads, (int)kv_heads, (int)q_len, (int)kv_len, c, bh_count, n_qblocks);
-  return launch_status("fa_prefill_bf16_d128");
+  return launch_fa<false>(ctx, format, causal != 0, q, k, v, o, q_heads, kv_heads, q_len, kv_len, c, bh_count,
+                          n_qblocks, FaStrides{});
 }
 
 extern "C" int wafer_hip_attention_prefill_strided(wafer_hip_context *ctx, uint32_t format, const void *q,
@@ -488,8 +532,8 @@ extern "C" int wafer_hip_attention_prefill_strided(wafer_hip_context *ctx, uint3
                                                    uint32_t kv_len, uint32_t head_dim, float scale,
                                                    uint32_t causal, const wafer_hip_attention_strides *strides) {
   WAFER_CHECK_CTX(ctx);
-  if (format != WAFER_FMT_BF16 || head_dim != D)
-    return fail(WAFER_HIP_E_UNSUPPORTED, "attention_prefill_strided: BF16 with head_dim 128 only");
+  if ((format != WAFER_FMT_BF16 && format != WAFER_FMT_F16) || head_dim != D)
+    return fail(WAFER_HIP_E_UNSUPPORTED, "attention_prefill_strided: BF16 or F16 with head_dim 128 only");
   if (!q || !k || !v || !o || !strides) return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill_strided: null tensor");
   if (batch == 0 || q_heads == 0 || kv_heads == 0 || q_len == 0 || kv_len == 0)
     return fail(WAFER_HIP_E_INVALID_FIELD, "attention_prefill_strided: empty dimension");
@@ -522,14 +566,6 @@ extern "C" int wafer_hip_attention_prefill_strided(wafer_hip_context *ctx, uint3
   const int n_qblocks = (int)n_qblocks64;
   const int bh_count = (int)(batch * q_heads);
   const float c = scale * 0x1.715476p+0f;
-  dim3 grid((unsigned)(bh_count * ((n_qblocks + 1) / 2)));
-  if (causal)
-    hipLaunchKernelGGL((fa_prefill_bf16_d128<true, true>), grid, dim3(THREADS), 0, ctx->stream, (const uint16_t *)q,
-                       (const uint16_t *)k, (const uint16_t *)v, (uint16_t *)o, (int)q_heads, (int)kv_heads,
-                       (int)q_len, (int)kv_len, c, bh_count, n_qblocks, st);
-  else
-    hipLaunchKernelGGL((fa_prefill_bf16_d128<false, true>), grid, dim3(THREADS), 0, ctx->stream, (const uint16_t *)q,
-                       (const uint16_t *)k, (const uint16_t *)v, (uint16_t *)o, (int)q_heads, (int)kv_heads,
-                       (int)q_len, (int)kv_len, c, bh_count, n_qblocks, st);
-  return launch_status("fa_prefill_bf16_d128");
+  return launch_fa<true>(ctx, format, causal != 0, q, k, v, o, q_heads, kv_heads, q_len, kv_len, c, bh_count,
+                         n_qblocks, st);
 }

@@ -55,7 +55,7 @@ __device__ inline f32x4 mfma16(v8<T> a, v8<T> b, f32x4 c) {
 }
 template <typename T>
 __device__ inline uint16_t narrow(float x) {
-  return __builtin_bit_cast(uint16_t, (T)x);
+  return __builtin_bit_cast(uint16_t, (T)f32_rounded(x));
 }
 // element e of 8 packed storage values, widened (exact); for F16 the
 // conversion folds into v_fma_mix_f32 at its use.  (The F16 half is taken
@@ -159,7 +159,7 @@ struct WaveSweep {
         for (int r = 0; r < 4; ++r) {
           const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[gi][r], c, -e2));
           rs += p;
-          if (hl < G) sP[gi * 16 + 4 * grp + r][hl] = (float)(T)p;
+          if (hl < G) sP[gi * 16 + 4 * grp + r][hl] = (float)(T)f32_rounded(p);
         }
       rs += __shfl_xor(rs, 16);
       rs += __shfl_xor(rs, 32);

@@ -70,9 +70,9 @@ __device__ inline i32x16 mfma<KIND_I8>(u32x4 a, u32x4 b, i32x16 c) {
 }
 
 // Epilogue selectors.
-// OUT_SWIGLU (bf16 only): the rhs rows come in 32-row groups, 16 gate rows
+// OUT_SWIGLU (bf16 or f16): the rhs rows come in 32-row groups, 16 gate rows
 // then the 16 up rows of the same features, and y[m, f] =
-// bf16(silu_mul(bf16(gate), bf16(up))) over N/2 features (the narrowed
+// T(silu_mul(T(gate), T(up))) over N/2 features, T the storage format (the narrowed
 // products, then the silu_mul region).  In a 32x32 MFMA tile the gate
 // values of 16 features sit in lanes l32 < 16 and their up values in lanes
 // l32 + 16; one v_permlane16_swap per register pair brings both to one
@@ -92,6 +92,7 @@ __device__ inline float widen_f16(uint16_t h) { return (float)__builtin_bit_cast
 // gradual underflow and overflow to +-inf; a NaN narrows to the canonical
 // 0x7e00 as f32_to_f16 does.
 __device__ inline uint16_t narrow_f16(float x) {
+  x = f32_rounded(x);
   return x != x ? (uint16_t)0x7e00u : __builtin_bit_cast(uint16_t, (_Float16)x);
 }
 
@@ -100,12 +101,19 @@ __device__ inline uint16_t narrow_f16(float x) {
 // v_permlane16_swap exchanges lanes 16..31 of `a` with lanes 0..15 of `b`
 // (and 48..63 with 32..47), after which lane l holds gate and up of feature
 // l % 16 for row q (l % 32 < 16) or q + 1 (l % 32 >= 16).  Returns the bf16
-// silu_mul of the narrowed pair.
+// silu_mul of the narrowed pair in the storage format (bf16 or f16).
+template <int KIND>
 __device__ inline uint16_t swiglu_pair(float a, float b) {
   const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
-  const float gv = bf16_to_f32(f32_to_bf16(__uint_as_float(t[0])));
-  const float uv = bf16_to_f32(f32_to_bf16(__uint_as_float(t[1])));
-  return f32_to_bf16(silu_mul_1(gv, uv));
+  if constexpr (KIND == KIND_F16) {
+    const float gv = widen_f16(narrow_f16(__uint_as_float(t[0])));
+    const float uv = widen_f16(narrow_f16(__uint_as_float(t[1])));
+    return narrow_f16(silu_mul_1(gv, uv));
+  } else {
+    const float gv = bf16_to_f32(f32_to_bf16(__uint_as_float(t[0])));
+    const float uv = bf16_to_f32(f32_to_bf16(__uint_as_float(t[1])));
+    return f32_to_bf16(silu_mul_1(gv, uv));
+  }
 }
 
 struct GemmArgs {
@@ -210,7 +218,7 @@ __device__ __attribute__((always_inline)) inline void gemm_store(
         *(uint16_t *)(stage + row * (CPR * 16) + (spos(row, col >> 3) << 4) + (col & 7) * 2) = v;
       };
       if constexpr (OUT == OUT_SWIGLU) {
-        static_assert(KIND == KIND_BF16, "the fused epilogue serves bf16");
+        static_assert(KIND == KIND_BF16 || KIND == KIND_F16, "the fused epilogue serves bf16 and f16");
         const int hi = (l32 >> 4) & 1;  // lanes 16..31 of each half take the odd row
 #pragma unroll
         for (int i = 0; i < WTM; ++i)
@@ -219,7 +227,7 @@ __device__ __attribute__((always_inline)) inline void gemm_store(
 #pragma unroll
             for (int r = 0; r < 16; r += 2)
               put(i * 32 + 8 * (r >> 2) + 4 * g + (r & 3) + hi, j * 16 + (l32 & 15),
-                  swiglu_pair((float)acc[i][j][r], (float)acc[i][j][r + 1]));
+                  swiglu_pair<KIND>((float)acc[i][j][r], (float)acc[i][j][r + 1]));
       } else {
 #pragma unroll
         for (int j = 0; j < WTN; ++j) {
@@ -274,7 +282,7 @@ __device__ __attribute__((always_inline)) inline void gemm_store(
   // epilogue: lane holds column l32 and rows 8*(r/4) + 4*g + r%4 of each tile
   if constexpr (OUT == OUT_SWIGLU) {
     // each 32-column tile holds 16 features (gate columns 0..15, up 16..31)
-    static_assert(KIND == KIND_BF16, "the fused epilogues serve bf16");
+    static_assert(KIND == KIND_BF16 || KIND == KIND_F16, "the fused epilogues serve bf16 and f16");
     const int nf = args.n / 2;
     const int hi = (l32 >> 4) & 1;
 #pragma unroll
@@ -286,7 +294,7 @@ __device__ __attribute__((always_inline)) inline void gemm_store(
 #pragma unroll
         for (int r = 0; r < 16; r += 2) {
           // every lane takes part in the swap before the tail test
-          const uint16_t v = swiglu_pair((float)acc[i][j][r], (float)acc[i][j][r + 1]);
+          const uint16_t v = swiglu_pair<KIND>((float)acc[i][j][r], (float)acc[i][j][r + 1]);
           const int row = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3) + hi;
           if (TAIL && !(col_ok && row < args.m)) continue;
           ((uint16_t *)args.y)[(size_t)row * nf + feat] = v;
@@ -1104,8 +1112,8 @@ extern "C" int wafer_hip_gemm_mfma_swiglu(wafer_hip_context *ctx, const void *lh
                                           void *dst, uint32_t m, uint32_t k, uint32_t features,
                                           uint32_t in_format) {
   WAFER_CHECK_CTX(ctx);
-  if (in_format != WAFER_FMT_BF16)
-    return fail(WAFER_HIP_E_UNSUPPORTED, "gemm_mfma_swiglu: input format must be BF16");
+  if (in_format != WAFER_FMT_BF16 && in_format != WAFER_FMT_F16)
+    return fail(WAFER_HIP_E_UNSUPPORTED, "gemm_mfma_swiglu: input format must be BF16 or F16");
   if (!lhs || !rhs_gu || !dst) return fail(WAFER_HIP_E_INVALID_FIELD, "gemm_mfma_swiglu: null tensor");
   if (features == 0 || features % 16)
     return fail(WAFER_HIP_E_UNSUPPORTED, "gemm_mfma_swiglu: features must be a positive multiple of 16");
@@ -1114,7 +1122,8 @@ extern "C" int wafer_hip_gemm_mfma_swiglu(wafer_hip_context *ctx, const void *lh
   WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
   GemmArgs args{(const uint8_t *)lhs, (const uint8_t *)rhs_gu, dst, nullptr, nullptr, (int)m,
                 (int)(2 * features), (int)(k * 2), 0, 0};
-  return launch_gemm<KIND_BF16, OUT_SWIGLU>(ctx->stream, args);
+  return in_format == WAFER_FMT_BF16 ? launch_gemm<KIND_BF16, OUT_SWIGLU>(ctx->stream, args)
+                                     : launch_gemm<KIND_F16, OUT_SWIGLU>(ctx->stream, args);
 }
 
 extern "C" int wafer_hip_gemm_i8(wafer_hip_context *ctx, const int8_t *a, const int8_t *b,
