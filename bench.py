@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the gfx950 numeric backend on BASELINE.json's headline metric.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fa,fd,i8,mlp,llama,mv,cmp,regions]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fa,fa_cases,fd,i8,mlp,llama,mv,cmp,regions]
                   (also: copy = counter calibration, vendor = ROCm library kernels for context)
 
 One step = one launch of the hot path over one batch of synthetic, seeded
@@ -59,9 +59,15 @@ def cores() -> int:
         return os.cpu_count() or 1
 
 
+TRAFFIC_SOURCE = ("read from profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this kernel, "
+                  "calibrated on a copy kernel, measured offline (not in this run)")
+
+
 def traffic_for(kernel: str):
     """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE +
-    WRITE_SIZE, calibrated against a copy kernel), if committed."""
+    WRITE_SIZE, calibrated against a copy kernel), if committed.  The bench
+    itself does not run the counters (they need their own profiler pass);
+    the roofline carries TRAFFIC_SOURCE next to the figure."""
     f = ROOT / "profiles" / "traffic.json"
     if not f.exists():
         return None
@@ -127,7 +133,7 @@ def bench_fa(torch, hip, steps, warmup, with_cpu=True):
     res = {
         "ms": ms, "value": achieved,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK["bf16"], "unit": "TFLOP/s",
-                     "frac": achieved / PEAK["bf16"], "traffic": traffic_for("fa_prefill")},
+                     "frac": achieved / PEAK["bf16"], "traffic": traffic_for("fa_prefill"), "traffic_source": TRAFFIC_SOURCE},
     }
     if with_cpu:
         from oracle import oracle as orc
@@ -143,6 +149,59 @@ def bench_fa(torch, hip, steps, warmup, with_cpu=True):
     return res
 
 
+def causal_flops(heads, s, d):
+    """Algorithmic FLOPs of causal attention: 4*d per visible (q, k) pair."""
+    return 4 * heads * d * (s * (s + 1) // 2)
+
+
+TX81_28x2048_MS = 3.649  # docs/attention-optimization-retrospective.md:9 (TX81, 16 tiles)
+
+
+def bench_fa_cases(torch, hip, steps, warmup):
+    """FA on the shapes and formats the reference's own attention cases use:
+    config 1 in F16 through the plain entry (the dedicated head_dim-128
+    kernel), config 1 through the masked entry in F16 and BF16 (the fa_fwd
+    kernels, which serve every masked / windowed / valid-prefix case),
+    attention-prefill at the cases' default head_dim 64 (q = kv = 1024, one
+    head, causal; wafer_pytorch_board_cases.py:34, 1058-1070), and the
+    TX81 retrospective's [1,28,2048,128] bf16 causal shape, next to its
+    published 3.649 ms."""
+    from vibe_compiler_amd.backend import BF16, F16
+
+    gen = torch.Generator(device="cuda").manual_seed(SEED)
+    legs = []
+
+    def leg(name, kernel, shape, fmt, masked, ref_ms=None):
+        dt = torch.bfloat16 if fmt == BF16 else torch.float16
+        q, k, v = (torch.randn(shape, device="cuda", generator=gen).to(dt) for _ in range(3))
+        o = torch.empty(shape, dtype=dt, device="cuda")
+        scale = 1.0 / math.sqrt(shape[3])
+        if masked:
+            fn = lambda: hip.attention_prefill_masked(q, k, v, o, scale, causal=True, fmt=fmt)  # noqa: E731
+        else:
+            fn = lambda: hip.attention_prefill(q, k, v, o, scale, causal=True, fmt=fmt)  # noqa: E731
+        ms = timed(torch, fn, steps, warmup)
+        fl = causal_flops(shape[0] * shape[1], shape[2], shape[3])
+        tf = fl / (ms * 1e-3) / 1e12
+        e = {"name": name, "kernel": kernel, "workload": f"{'F16' if fmt == F16 else 'BF16'} Q,K,V {list(shape)} causal",
+             "ms": ms, "value": tf, "unit": "TFLOP/s", "algorithmic_flops": fl,
+             "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK["bf16"], "unit": "TFLOP/s",
+                          "frac": tf / PEAK["bf16"], "traffic": None}}
+        if ref_ms is not None:
+            e["reference_published_ms"] = ref_ms
+            e["speedup_vs_reference_published"] = ref_ms / ms
+        legs.append(e)
+
+    leg("fa_prefill_f16_config1", "fa_prefill_d128<_Float16, true, false>", FA_SHAPE, F16, False)
+    leg("fa_fwd_bf16_config1", "fa_fwd<__bf16, 128, MASK_CAUSAL>", FA_SHAPE, BF16, True)
+    leg("fa_fwd_f16_config1", "fa_fwd<_Float16, 128, MASK_CAUSAL>", FA_SHAPE, F16, True)
+    leg("attention_prefill_d64_1024_f16", "fa_fwd<_Float16, 64, MASK_CAUSAL>", (1, 1, 1024, 64), F16, False)
+    leg("attention_prefill_d64_1024_bf16", "fa_fwd<__bf16, 64, MASK_CAUSAL>", (1, 1, 1024, 64), BF16, False)
+    leg("tx81_28x2048_bf16", "fa_prefill_d128<__bf16, true, false>", (1, 28, 2048, 128), BF16, False,
+        ref_ms=TX81_28x2048_MS)
+    return {"workload": "FA prefill on the reference's attention-case shapes and formats", "legs": legs}
+
+
 def bench_fd(torch, hip, steps, warmup, with_cpu=True):
     gen = torch.Generator(device="cuda").manual_seed(SEED)
     q = rnd_bf16(torch, gen, (FD_B, FD_HQ, 1, FD_D))
@@ -156,7 +215,7 @@ def bench_fd(torch, hip, steps, warmup, with_cpu=True):
         "workload": "FD decode bf16 Q[32,32,1,128] KV[32,8,8192,128] GQA 32/8, 16 chunks, LSE fold",
         "metric": "HBM GB/s", "ms": ms, "value": gbs, "unit": "GB/s", "tflops": FD_FLOPS / (ms * 1e-3) / 1e12,
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK["hbm"], "unit": "GB/s",
-                     "frac": gbs / PEAK["hbm"], "traffic": traffic_for("fd_decode")},
+                     "frac": gbs / PEAK["hbm"], "traffic": traffic_for("fd_decode"), "traffic_source": TRAFFIC_SOURCE},
     }
     if with_cpu:
         from oracle import oracle as orc
@@ -184,7 +243,7 @@ def bench_i8(torch, hip, steps, warmup, with_cpu=True):
         "workload": "int8 GEMM 4096^3 (rhs [K,N]), exact int32 accumulate, per-column f32 dequant, bf16 out",
         "metric": "TOP/s", "ms": ms, "value": tops, "unit": "TOP/s",
         "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK["i8"], "unit": "TOP/s",
-                     "frac": tops / PEAK["i8"], "traffic": traffic_for("gemm_i8")},
+                     "frac": tops / PEAK["i8"], "traffic": traffic_for("gemm_i8"), "traffic_source": TRAFFIC_SOURCE},
     }
     if with_cpu:
         from oracle import oracle as orc
@@ -424,7 +483,7 @@ def bench_regions(torch, hip, steps, warmup):
         out.append({"name": name, "kernel": kernel, "workload": workload, "ms": ms, "value": gbs, "unit": "GB/s",
                     "algorithmic_bytes": nbytes,
                     "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK["hbm"], "unit": "GB/s",
-                                 "frac": gbs / PEAK["hbm"], "traffic": traffic_for(name)}})
+                                 "frac": gbs / PEAK["hbm"], "traffic": traffic_for(name), "traffic_source": TRAFFIC_SOURCE}})
 
     B = 2  # bytes per bf16 element
     x = rnd_bf16(torch, gen, (R, C))
@@ -471,8 +530,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="fa,fd,i8,mlp,llama,mv,cmp,regions",
-                    help="comma list of fa, fd, i8, mlp, llama, mv, cmp, regions, copy, vendor")
+    ap.add_argument("--only", default="fa,fa_cases,fd,i8,mlp,llama,mv,cmp,regions",
+                    help="comma list of fa, fa_cases, fd, i8, mlp, llama, mv, cmp, regions, copy, vendor")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -493,6 +552,8 @@ def main() -> int:
     fa = None
     if "fa" in only:
         fa = bench_fa(torch, hip, args.steps, args.warmup, with_cpu)
+    if "fa_cases" in only:
+        secondary.append(dict(name="fa_cases", **bench_fa_cases(torch, hip, args.steps, args.warmup)))
     if "fd" in only:
         secondary.append(dict(name="fd_decode", **bench_fd(torch, hip, args.steps, args.warmup, with_cpu)))
     if "i8" in only:
