@@ -70,7 +70,17 @@ typedef struct wafer_hip_context wafer_hip_context;
  * (tools/wafer-compile/wafer-compile.cpp:477-506).  A context binds one HIP
  * device and one stream (the null stream until set).  Calls on one context
  * are serialised by the caller, as SystemCTargetModel::issue serialises
- * backend calls (lib/Wafer/Simulator/SystemC/SystemCTargetModel.cpp:156-185). */
+ * backend calls (lib/Wafer/Simulator/SystemC/SystemCTargetModel.cpp:156-185).
+ * Workspace: the context owns three device areas, each grown on first need
+ * and never shrunk -- the split-K partial tiles of the MFMA GEMMs (up to
+ * 4 * m * n * 4 bytes for the 16-bit GEMMs, 64 MiB at the decoder layer's
+ * down projection), the re-laid-out [n,k] rhs of a Normal-orientation GEMM
+ * (k * n * element bytes) and FD's chunk states for small batches.  Growing
+ * is refused on a capturing stream, so a caller that captures runs each
+ * shape once eagerly first.  A grown area's old buffer is kept until
+ * wafer_hip_context_destroy, so graphs captured before a later, larger eager
+ * call still replay on valid memory (the area at least doubles per growth,
+ * bounding the retired buffers by its current size). */
 int wafer_hip_context_create(int device, wafer_hip_context **out);
 int wafer_hip_context_destroy(wafer_hip_context *ctx);
 int wafer_hip_set_stream(wafer_hip_context *ctx, void *hip_stream);
@@ -423,7 +433,9 @@ int wafer_hip_attention_decode(wafer_hip_context *ctx, uint32_t format,
  * WAFER_HIP_E_UNSUPPORTED before any launch.  It calls no hipMalloc / hipFree.
  * All calls on one GPU share that scratch (it keeps the last call's
  * contents; every state is written before it is read), so calls that overlap
- * on one GPU -- on different streams or from different threads -- race. */
+ * on one GPU -- on different streams or from different threads -- race.
+ * The scratch's device address is resolved by wafer_hip_context_create, so
+ * even the first call on a context may run under a graph capture. */
 int wafer_hip_attention_decode_noalloc(wafer_hip_context *ctx, uint32_t format,
                                        const void *q, const void *k_cache,
                                        const void *v_cache, void *o,

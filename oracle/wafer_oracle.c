@@ -671,9 +671,14 @@ static inline float maximumf(float a, float b) {
 /* Score masking of one query row: the score region and the position bias of
  * applyScoreRegion (lib/Wafer/Transforms/Linalg/OnlineAttentionDecomposition.cpp:279-426).
  * Key j is visible iff lo <= j <= hi and keep[j] != 0 (when a boolean mask is
- * given); an invisible key's score gets + (-inf), as the 0/-inf position
- * bias template of :316-330 does (its `visible` = min(diagonal + q + 1,
- * valid) is hi + 1 here, valid = kv_len). */
+ * given).  An invisible key's score becomes -inf: for a finite score that is
+ * the 0/-inf position bias template of :316-330 added to it (its `visible` =
+ * min(diagonal + q + 1, valid) is hi + 1 here, valid = kv_len).  A
+ * non-finite score (or NaN mask value) at an invisible key is excluded too,
+ * where the reference's sum would carry the NaN: keys past kv_len are never
+ * read and key blocks past the row's last visible key are never walked, so
+ * an invisible key must not reach the output (the GPU kernels follow the
+ * same rule). */
 typedef struct {
   int format;
   uint32_t flags;
@@ -734,7 +739,7 @@ static void att_block(att_state *st, int format, const uint16_t *qrow,
     float sc = oracle_attention_score(format, row->flags, dot, scale,
                                       row->bias ? row->bias + j : NULL);
     if (j < row->lo || j > row->hi || (row->keep && !row->keep[j]))
-      sc = sc + (-INFINITY);
+      sc = -INFINITY;  /* excluded */
     s[j - j0] = sc;
     rowmax = maximumf(rowmax, sc);
   }

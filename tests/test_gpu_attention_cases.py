@@ -376,3 +376,62 @@ def test_strided_prefill_rejections(hip, B):
     assert e.value.status == -1
     with pytest.raises(ValueError):  # head_dim must have unit stride
         hip.attention_prefill_strided(q, q, q.transpose(2, 3), q.clone(), 0.1)
+
+
+# --------------------------------------------- invisible keys are excluded
+@pytest.mark.parametrize("fmt", [F16, BF16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("D", [16, 128])
+def test_invisible_nan_key_is_excluded(hip, oracle, fmt, D):
+    """A NaN K row at key j: queries that cannot see j (causal, window,
+    boolean mask) give the bits of the same call with that row zeroed, and
+    queries that can see it give NaN -- the oracle's rule, through the
+    masked entry (fa_small at head_dim 16, fa_fwd at 128) and, at 128, the
+    plain causal entry's dedicated kernel."""
+    say("invisible NaN key", fmt, D)
+    rng = np.random.default_rng(170 + D + fmt)
+    Sq = Skv = 100
+    j = 50
+    nan = 0x7E00 if fmt == F16 else 0x7FC0
+    q, k, v = inputs(oracle, rng, fmt, 2, 1, Sq, Skv, D)
+    kn, kz = k.copy(), k.copy()
+    kn[:, :, j] = nan
+    kz[:, :, j] = 0
+    s = 1.0 / math.sqrt(D)
+    isnan = lambda a: np.isnan(tof(oracle, fmt, a).astype(np.float64))  # noqa: E731
+    a = run_masked(hip, fmt, q, kn, v, s, causal=True)
+    b = run_masked(hip, fmt, q, kz, v, s, causal=True)
+    assert np.array_equal(a[:, :, :j], b[:, :, :j]) and isnan(a[:, :, j:]).all()
+    ref = oracle.attention_prefill_ex(q, kn, v, s, causal=True, fmt=fmt)
+    attention_gate(tof(oracle, fmt, a[:, :, :j]), tof(oracle, fmt, ref[:, :, :j]), what="causal, rows before the NaN key")
+    if D == 128:  # the plain entry's dedicated kernel
+        o1 = torch.full(q.shape, 0x7E00, dtype=torch.int16, device="cuda")
+        o2 = torch.full(q.shape, 0x7E00, dtype=torch.int16, device="cuda")
+        hip.attention_prefill(u16(q), u16(kn), u16(v), o1, s, causal=True, fmt=fmt)
+        hip.attention_prefill(u16(q), u16(kz), u16(v), o2, s, causal=True, fmt=fmt)
+        p1, p2 = back(o1), back(o2)
+        assert np.array_equal(p1[:, :, :j], p2[:, :, :j]) and isnan(p1[:, :, j:]).all()
+    keep = np.ones((1, 1, 1, Skv), np.uint8)
+    keep[..., j] = 0
+    assert np.array_equal(run_masked(hip, fmt, q, kn, v, s, keep=keep), run_masked(hip, fmt, q, kz, v, s, keep=keep))
+    a = run_masked(hip, fmt, q, kn, v, s, causal=True, window=8)
+    b = run_masked(hip, fmt, q, kz, v, s, causal=True, window=8)
+    rows = np.r_[0:j, j + 8:Sq]
+    assert np.array_equal(a[:, :, rows], b[:, :, rows]) and isnan(a[:, :, j:j + 8]).all()
+
+
+@pytest.mark.parametrize("fmt", [F16, BF16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("D", [16, 64, 128])
+def test_hugely_negative_visible_scores_keep_their_maximum(hip, oracle, fmt, D):
+    """Every visible score far below -1e29 (an additive mask of -1e30 -
+    1e28 * j): softmax keeps only the maximum, so every output row is the V
+    row of its largest visible score, bit for bit, as in the oracle."""
+    say("hugely negative scores", fmt, D)
+    rng = np.random.default_rng(181 + D + fmt)
+    Sq, Skv = 40, 200
+    q, k, v = inputs(oracle, rng, fmt, 1, 1, Sq, Skv, D)
+    bias = np.ascontiguousarray(np.broadcast_to(
+        (-1e30 - 1e28 * rng.permutation(Skv)).astype(np.float32)[None, None, None, :], (1, 1, Sq, Skv)))
+    got = run_masked(hip, fmt, q, k, v, 0.125, bias=bias)
+    best = int(np.argmax(bias[0, 0, 0]))
+    assert np.array_equal(got[0, 0], np.broadcast_to(v[0, 0, best], (Sq, D)))
+    assert np.array_equal(got, oracle.attention_prefill_ex(q, k, v, 0.125, bias=bias, fmt=fmt))

@@ -133,3 +133,51 @@ def test_decoder_layer_graph_replay(hip):
     y, y2 = torch.empty_like(x), torch.empty_like(x)
     layer = DL.DecoderLayer(hip, W, 1024)
     replay_matches_eager(lambda: layer.forward(x, y), y, lambda: layer.forward(x2, y2))
+
+
+def test_graph_survives_workspace_growth(B):
+    """A graph captured while the context's split-K partial area was small
+    still replays correctly after a larger eager call on the same context
+    grows the area: the outgrown buffer is kept until the context is
+    destroyed, so the graph's partial tiles never land in memory handed out
+    since (a torch tensor allocated after the growth keeps its contents)."""
+    say("graph replay across workspace growth")
+    hip = B.Context(0)
+    gen = torch.Generator(device="cuda").manual_seed(16)
+    k, n = 8192, 1024
+    small_m, big_m = 256, 1024   # 4 and 16 MiB of f32 partials (4 splits)
+    a = rnd((small_m, k), gen)
+    bt = rnd((n, k), gen)
+    y = torch.empty((small_m, n), dtype=torch.float32, device="cuda")
+    call = lambda: hip.gemm_mfma(a, bt, y, small_m, k, n, in_fmt=B.BF16, out_fmt=B.F32, rhs_t=True)  # noqa: E731
+    call()
+    torch.cuda.synchronize()
+    ref = y.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            call()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    # the larger eager call grows the partial area
+    a_big = rnd((big_m, k), gen)
+    y_big = torch.empty((big_m, n), dtype=torch.float32, device="cuda")
+    hip.gemm_mfma(a_big, bt, y_big, big_m, k, n, in_fmt=B.BF16, out_fmt=B.F32, rhs_t=True)
+    torch.cuda.synchronize()
+    canary = torch.full((8 << 20,), 3.0, dtype=torch.float32, device="cuda")  # 32 MiB allocated after the growth
+    for r in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref), f"replay {r} differs from the eager run"
+        assert bool(torch.all(canary == 3.0)), f"replay {r} wrote into memory allocated after the growth"
+    # the grown area serves the large shape as before
+    y_big2 = torch.empty_like(y_big)
+    hip.gemm_mfma(a_big, bt, y_big2, big_m, k, n, in_fmt=B.BF16, out_fmt=B.F32, rhs_t=True)
+    torch.cuda.synchronize()
+    assert torch.equal(y_big, y_big2)
+    del graph
+    hip.close()

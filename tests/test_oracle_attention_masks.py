@@ -246,3 +246,60 @@ def test_score_rounding_flags_reach_the_scores(oracle):
     attention_gate(o_u, ref_u, what="unrounded")
     # each misses the other closed form by more than the policy allows
     assert stats(o_r, ref_u)[1] > 0.01 and stats(o_u, ref_r)[1] > 0.01
+
+
+def _nan_bits(fmt):
+    return 0x7E00 if fmt == F16 else 0x7FC0
+
+
+@pytest.mark.parametrize("fmt", [F16, BF16])
+@pytest.mark.parametrize("D", [16, 128])
+def test_invisible_keys_are_excluded(oracle, fmt, D):
+    """One rule for every invisible key (past the causal diagonal, outside a
+    window, or masked by a boolean mask): it is excluded, whatever its score.
+    A NaN K row therefore changes nothing for the queries that cannot see it
+    (bit for bit against the same call with that row zeroed), and makes the
+    output NaN exactly for the queries that can."""
+    rng = np.random.default_rng(70 + D + fmt)
+    Sq = Skv = 100
+    j = 50
+    q, k, v = _inputs(oracle, rng, fmt, 2, 1, Sq, Skv, D)
+    kn, kz = k.copy(), k.copy()
+    kn[:, :, j] = _nan_bits(fmt)
+    kz[:, :, j] = 0
+    s = 1.0 / math.sqrt(D)
+    # causal: queries i < j cannot see key j
+    a = oracle.attention_prefill_ex(q, kn, v, s, causal=True, fmt=fmt)
+    b = oracle.attention_prefill_ex(q, kz, v, s, causal=True, fmt=fmt)
+    assert np.array_equal(a[:, :, :j], b[:, :, :j])
+    assert np.isnan(oracle.to_float(fmt, a[:, :, j:]).astype(np.float64)).all()
+    # the legacy causal entry (the dedicated kernel's oracle) follows the same rule
+    c = oracle.attention_prefill(q, kn, v, s, causal=True, block_k=64, fmt=fmt)
+    assert np.array_equal(c[:, :, :j], oracle.attention_prefill(q, kz, v, s, causal=True, block_k=64, fmt=fmt)[:, :, :j])
+    # a boolean mask hiding key j from every query: nothing changes anywhere
+    keep = np.ones((1, 1, 1, Skv), np.uint8)
+    keep[..., j] = 0
+    assert np.array_equal(oracle.attention_prefill_ex(q, kn, v, s, keep=keep, fmt=fmt),
+                          oracle.attention_prefill_ex(q, kz, v, s, keep=keep, fmt=fmt))
+    # a window of 8 keys ending at the diagonal: only queries j..j+7 see key j
+    a = oracle.attention_prefill_ex(q, kn, v, s, causal=True, window=8, fmt=fmt)
+    b = oracle.attention_prefill_ex(q, kz, v, s, causal=True, window=8, fmt=fmt)
+    rows = np.r_[0:j, j + 8:Sq]
+    assert np.array_equal(a[:, :, rows], b[:, :, rows])
+    assert np.isnan(oracle.to_float(fmt, a[:, :, j:j + 8]).astype(np.float64)).all()
+
+
+@pytest.mark.parametrize("fmt", [F16, BF16])
+def test_hugely_negative_visible_scores_keep_their_maximum(oracle, fmt):
+    """A row whose every visible score is far below any float a reference
+    floor could hold (an additive mask of -1e30 - 1e28 * j) normalises over
+    those scores: softmax keeps only the maximum, so each output row is the
+    V row of its largest visible score (narrowed), as the closed form says."""
+    rng = np.random.default_rng(81 + fmt)
+    Sq, Skv, D = 40, 70, 64
+    q, k, v = _inputs(oracle, rng, fmt, 1, 1, Sq, Skv, D)
+    bias = (-1e30 - 1e28 * rng.permutation(Skv)).astype(np.float32)[None, None, None, :]
+    out = oracle.attention_prefill_ex(q, k, v, 0.125, bias=np.ascontiguousarray(np.broadcast_to(bias, (1, 1, Sq, Skv))),
+                                      fmt=fmt)
+    best = int(np.argmax(bias[0, 0, 0]))
+    assert np.array_equal(out[0, 0], np.broadcast_to(v[0, 0, best], (Sq, D)))

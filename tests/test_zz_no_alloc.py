@@ -37,6 +37,46 @@ def _case(B, Hq, Hkv, cap, kv_len, seed):
     return q, k, v
 
 
+def test_noalloc_decode_captured_as_first_call():
+    """On a fresh context, the chunk-grid no-allocation call is captured into
+    a HIP graph as the context's first call; the graph is replayed three
+    times (output cleared between replays) and each replay is bit-identical
+    to the allocating entry run eagerly on another context."""
+    from vibe_compiler_amd import backend
+
+    L = backend.load()
+    B, Hq, Hkv, cap, kv_len, chunks = 2, 8, 2, 4096, 3000, 16
+    print(f"[gpu-case] noalloc decode captured first: B={B} Hq={Hq} Hkv={Hkv} kv_len={kv_len}", flush=True)
+    q, k, v = _case(B, Hq, Hkv, cap, kv_len, 31)
+    scale = 1.0 / math.sqrt(128)
+    o = torch.full((B, Hq, 1, 128), 7.0, dtype=torch.bfloat16, device="cuda")
+    hip = backend.Context(0)
+    f = _noalloc(L)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    status = []
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            status.append(f(hip._bind(), backend.BF16, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), B,
+                            Hq, Hkv, kv_len, cap, 128, scale, chunks))
+    torch.cuda.current_stream().wait_stream(side)
+    assert status == [0], L.wafer_hip_last_error()
+    ref_ctx = backend.Context(0)
+    o_ref = torch.zeros_like(o)
+    ref_ctx.attention_decode(q, k, v, o_ref, scale, chunks=chunks, kv_len=kv_len)
+    torch.cuda.synchronize()
+    for r in range(3):
+        o.fill_(7.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o.view(torch.int16), o_ref.view(torch.int16)), f"replay {r}"
+    del graph
+    ref_ctx.close()
+    hip.close()
+
+
 @pytest.mark.parametrize("first,second", [
     ((2, 8, 2, 4096, 4000, 16), (1, 4, 1, 1024, 777, 8)),     # chunk grid, then a smaller one
     ((3, 32, 4, 2048, 2048, 16), (2, 16, 2, 512, 300, 4)),    # GQA 8 (chunk grid), then smaller

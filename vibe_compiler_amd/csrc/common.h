@@ -8,6 +8,7 @@
 #include <cstdint>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "wafer_hip.h"
 
@@ -23,10 +24,14 @@ struct wafer_hip_context {
   // Scratch for operand re-layout (transposed rhs), grown on demand.
   void *relayout = nullptr;
   size_t relayout_bytes = 0;
-  // Split-K partial tiles of the f32 GEMM, grown on demand.
+  // Split-K partial tiles of the 16-bit and f32 MFMA GEMMs, grown on demand.
   void *partials = nullptr;
   size_t partials_bytes = 0;
   int cu_count = 0;
+  // Buffers a workspace slot outgrew.  They stay allocated until the
+  // context is destroyed, so a graph captured while a smaller buffer was
+  // current keeps valid memory after a later eager call grows the slot.
+  std::vector<void *> retired;
 };
 
 namespace wafer {
@@ -50,6 +55,9 @@ int status_words(wafer_hip_context *ctx, const char *what, uint8_t **words);
 // stream (a memset node recorded into a graph has given wrong results on
 // later replays, so device words are never cleared with hipMemsetAsync).
 int fill_words(wafer_hip_context *ctx, void *p, uint32_t n, uint32_t value);
+// Resolves the device address of the no-allocation decode scratch on
+// `device` (fd_decode.hip); wafer_hip_context_create calls it.
+int noalloc_scratch_lookup(int device);
 // FA prefill through the masked-attention kernels (fa_masked.hip): the
 // body of wafer_hip_attention_prefill_masked, also taken by
 // wafer_hip_attention_prefill for the cases its own kernel does not serve.

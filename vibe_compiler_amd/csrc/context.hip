@@ -53,23 +53,24 @@ int status_words(wafer_hip_context *ctx, const char *what, uint8_t **words) {
   return WAFER_HIP_OK;
 }
 
-// Grows *slot to at least `need` bytes.  The old contents are discarded; the
-// growth is stream-ordered by synchronising the context's stream first, so
-// in-flight kernels never see the buffer freed under them.  Growing is
-// refused on a capturing stream (a captured graph would keep the old
-// address); a slot that is already large enough is used as it is.
+// Grows *slot to at least `need` bytes (whole MiB, and at least twice the
+// old size, so the buffers a slot retires sum to less than its current
+// size).  The old buffer is not freed: it moves to ctx->retired and lives
+// until the context is destroyed, so kernels still in flight on it and
+// graphs captured while it was current keep valid memory.  The new buffer's
+// contents are undefined.  Growing is refused on a capturing stream (the
+// allocation cannot be recorded); a slot that is large enough is used as it
+// is.
 int ensure_workspace(wafer_hip_context *ctx, void **slot, size_t *slot_bytes,
                      size_t need) {
   if (*slot_bytes >= need) return WAFER_HIP_OK;
   WAFER_TRY(refuse_capture(ctx, "growing the context workspace"));
-  WAFER_TRY(check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize"));
-  if (*slot) {
-    WAFER_TRY(check_hip(hipFree(*slot), "hipFree(workspace)"));
-    *slot = nullptr;
-    *slot_bytes = 0;
-  }
   size_t rounded = (need + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
-  WAFER_TRY(check_hip(hipMalloc(slot, rounded), "hipMalloc(workspace)"));
+  if (*slot && rounded < 2 * *slot_bytes) rounded = 2 * *slot_bytes;
+  void *grown = nullptr;
+  WAFER_TRY(check_hip(hipMalloc(&grown, rounded), "hipMalloc(workspace)"));
+  if (*slot) ctx->retired.push_back(*slot);
+  *slot = grown;
   *slot_bytes = rounded;
   return WAFER_HIP_OK;
 }
@@ -90,6 +91,10 @@ extern "C" int wafer_hip_context_create(int device, wafer_hip_context **out) {
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     return fail(WAFER_HIP_E_UNAVAILABLE,
                 std::string("device is ") + prop.gcnArchName + ", kernels are built for gfx950");
+  // the no-allocation decode entry's scratch address, resolved here (once
+  // per device) rather than at that entry's first call, which may run
+  // under a graph capture
+  WAFER_TRY(noalloc_scratch_lookup(device));
   auto *ctx = new wafer_hip_context();
   ctx->device = device;
   ctx->cu_count = prop.multiProcessorCount;
@@ -100,13 +105,14 @@ extern "C" int wafer_hip_context_create(int device, wafer_hip_context **out) {
 extern "C" int wafer_hip_context_destroy(wafer_hip_context *ctx) {
   if (!ctx) return WAFER_HIP_OK;
   int st = WAFER_HIP_OK;
-  if (ctx->workspace || ctx->relayout || ctx->status || ctx->partials) {
+  if (ctx->workspace || ctx->relayout || ctx->status || ctx->partials || !ctx->retired.empty()) {
     st = check_hip(hipSetDevice(ctx->device), "hipSetDevice");
     if (st == WAFER_HIP_OK) st = check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     if (ctx->workspace) st = check_hip(hipFree(ctx->workspace), "hipFree(workspace)");
     if (ctx->relayout) st = check_hip(hipFree(ctx->relayout), "hipFree(relayout)");
     if (ctx->status) st = check_hip(hipFree(ctx->status), "hipFree(status)");
     if (ctx->partials) st = check_hip(hipFree(ctx->partials), "hipFree(partials)");
+    for (void *p : ctx->retired) st = check_hip(hipFree(p), "hipFree(retired workspace)");
   }
   delete ctx;
   return st;

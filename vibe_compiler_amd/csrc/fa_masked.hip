@@ -55,13 +55,12 @@ constexpr int BK = 64;        // keys per KV block
 constexpr int THREADS = 256;  // 4 waves: (tile, key half)
 constexpr float RESCALE_LOG2 = 8.0f;
 constexpr float RESCALE_BOUND = 256.0f;
-// "no reference yet": finite, so exp2(u - NOREF) is +inf for a visible score
-// and 0 for a masked one (never NaN), and exp2(NOREF - x) == 0
-constexpr float NOREF = -0x1p100f;
-// MASK_GENERAL clamps finite log2-domain scores at this floor (above NOREF),
-// so a row whose every visible score is hugely negative still normalises
-// over those scores instead of reading as fully masked
-constexpr float UFLOOR = -0x1p99f;
+// "no reference yet": the lowest finite float, so exp2(u - NOREF) is +inf
+// (or at least 1) for a visible score and 0 for a masked one (never NaN),
+// exp2(NOREF - x) == 0 for any score x above NOREF + 150, and every finite
+// visible score is a valid reference (P relative to NOREF stays below 2^8
+// until a score exceeds NOREF + 8, which sends the wave to the exact update).
+constexpr float NOREF = -0x1.fffffep127f;
 constexpr float LOG2E = 0x1.715476p+0f;
 
 enum { MASK_CAUSAL = 1, MASK_GENERAL = 2 };
@@ -126,7 +125,8 @@ __device__ inline float xor32_sum(float x) {
 }
 
 // One score through the score region and the masks: visible -> u = t*log2(e)
-// (finite values clamped at UFLOOR), invisible -> -inf.
+// (a finite t whose u overflows is clamped to the lowest finite float),
+// invisible -> -inf, whatever t is (an invisible key is excluded).
 template <typename T>
 __device__ inline float general_score(float s, float scale, uint32_t flags, const float *brow,
                                       const uint8_t *krow, int key, bool vis) {
@@ -139,7 +139,7 @@ __device__ inline float general_score(float s, float scale, uint32_t flags, cons
   if (vis && krow) vis = krow[key] != 0;
   if (!vis || t == -__builtin_inff()) return -__builtin_inff();
   const float u = t * LOG2E;
-  return u == u ? fmaxf(u, UFLOOR) : u;  // NaN passes through
+  return u == u ? fmaxf(u, NOREF) : u;  // NaN passes through
 }
 
 // LDS swizzles (16-byte chunk index XOR): K rows are read 32 rows x one
@@ -658,7 +658,7 @@ __global__ __launch_bounds__(SMALL_ROWS) void fa_small(const FaArgs a, int D, in
           t = t + brow[key];
           if (a.flags & F_ROUND_BIASED) t = round_to<T>(t);
         }
-        if (key < lo || key > hi || (krow && krow[key] == 0)) t = t + -__builtin_inff();
+        if (key < lo || key > hi || (krow && krow[key] == 0)) t = -__builtin_inff();  // excluded
       }
       ss[j][threadIdx.x] = t;
       rowmax = (t != t || rowmax != rowmax) ? __builtin_nanf("") : fmaxf(rowmax, t);

@@ -78,9 +78,11 @@ constexpr float RESCALE_BOUND = 256.0f;  // 2^RESCALE_LOG2
 constexpr int SG_MFMA = 0x008, SG_VMEM = 0x010, SG_DS_READ = 0x100;
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-// "no reference yet": finite, so exp2(fma(s, c, -NOREF)) is +inf for a
-// visible score and 0 for a masked one (never NaN), and exp2(NOREF - x) == 0
-constexpr float NOREF = -0x1p100f;
+// "no reference yet": the lowest finite float, so exp2(fma(s, c, -NOREF)) is
+// +inf (or at least 1) for a visible score and 0 for a masked one (never
+// NaN), exp2(NOREF - x) == 0 for x above NOREF + 150, and any visible score,
+// however negative, becomes a valid reference
+constexpr float NOREF = -0x1.fffffep127f;
 
 // x combined with the value of lane ^ 32 (v_permlane32_swap exchanges the
 // upper half of one register with the lower half of the other)

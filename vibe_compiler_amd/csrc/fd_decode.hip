@@ -493,6 +493,21 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const uint16_t *__restri
 }
 
 }  // namespace
+
+// Looks up the no-allocation scratch's address on `device` (made current
+// here; the caller's current device is restored).  Called once per context
+// at creation, so the entry's first call -- possibly inside a graph
+// capture -- finds the address already known.
+int noalloc_scratch_lookup(int device) {
+  int prev = 0;
+  WAFER_TRY(check_hip(hipGetDevice(&prev), "hipGetDevice"));
+  WAFER_TRY(check_hip(hipSetDevice(device), "hipSetDevice"));
+  ChunkState *unused = nullptr;
+  const int st = scratch_for(device, &unused);
+  WAFER_TRY(check_hip(hipSetDevice(prev), "hipSetDevice"));
+  return st;
+}
+
 }  // namespace wafer
 
 using namespace wafer;
