@@ -77,6 +77,20 @@ def traffic_for(kernel: str):
         return None
 
 
+def cpu_time(fn):
+    """Wall seconds of one call of fn (the CPU oracle over a bounded sample)."""
+    t0 = time.perf_counter()
+    fn()
+    return time.perf_counter() - t0
+
+
+def cpu_gbs(nbytes, dt, sample, cores_used=1):
+    """cpu_baseline record for an HBM-class leg: algorithmic bytes of the
+    sample / wall time."""
+    return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": cores_used, "kind": "port",
+            "sample": f"{sample}, {dt:.3f} s wall"}
+
+
 SETTLE_S = 0.3  # untimed replays before the timed one: the GPU's clocks
                 # take tens of milliseconds of sustained load to settle
 
@@ -347,7 +361,7 @@ def bench_llama(torch, hip, steps, warmup, with_cpu=True):
     return res
 
 
-def bench_mv(torch, hip, steps, warmup):
+def bench_mv(torch, hip, steps, warmup, with_cpu=True):
     """Movement commands: a strided tile gather (RDMA shape: 131072 rows of
     4 KiB out of an 8 KiB-pitch matrix into a dense tile, 512 MiB payload,
     working set above the 256 MB last-level cache) and
@@ -365,17 +379,33 @@ def bench_mv(torch, hip, steps, warmup):
     ms_t = timed(torch, lambda: hip.strided_copy(x, t, 2, [2, 2 * n, 0], [n, n, 1], [2 * n, 2, 0], [n, n, 1]),
                  steps, warmup)
     gbs_t = 2 * n * n * 2 / (ms_t * 1e-3) / 1e9
+    cpu = None
+    if with_cpu:
+        from oracle import oracle as orc
+        rs = 16384  # 16384 rows of the gather (64 MiB payload)
+        src_s = src[: rs * pitch].cpu().numpy()
+        dst_s = np.zeros(rs * inner, np.uint8)
+        dt = cpu_time(lambda: orc.strided_copy(src_s, dst_s, inner, [pitch, 0, 0], [rs, 1, 1], [inner, 0, 0],
+                                               [rs, 1, 1]))
+        cpu = cpu_gbs(2 * rs * inner, dt, f"{rs} of {rows} rows of the same gather (scalar C oracle)")
+        nt = 4096  # a 4096 x 4096 corner of the transpose
+        xs = x[:nt, :nt].contiguous().cpu().numpy().view(np.uint8).reshape(-1)
+        dt_t = cpu_time(lambda: orc.strided_copy(xs, np.zeros_like(xs), 2, [2, 2 * nt, 0], [nt, nt, 1],
+                                                 [2 * nt, 2, 0], [nt, nt, 1]))
+        cpu_t = cpu_gbs(2 * nt * nt * 2, dt_t, f"a {nt} x {nt} bf16 transpose (scalar C oracle)")
     return {
         "workload": "strided tile gather 131072 x 4 KiB segments at 8 KiB pitch -> dense (512 MiB payload)",
         "metric": "GB/s", "ms": ms, "value": gbs, "unit": "GB/s",
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK["hbm"], "unit": "GB/s",
                      "frac": gbs / PEAK["hbm"], "traffic": None},
+        "cpu_baseline": cpu,
         "transpose": {"workload": "bf16 16384 x 16384 transpose, 2-byte segments (512 MiB payload)", "ms": ms_t,
-                      "value": gbs_t, "unit": "GB/s", "frac": gbs_t / PEAK["hbm"]},
+                      "value": gbs_t, "unit": "GB/s", "frac": gbs_t / PEAK["hbm"],
+                      "cpu_baseline": cpu_t if with_cpu else None},
     }
 
 
-def bench_cmp(torch, hip, steps, warmup):
+def bench_cmp(torch, hip, steps, warmup, with_cpu=True):
     """Program-boundary comparator on a 256M-element bf16 pair (512 MiB each,
     above the 256 MB last-level cache): the output gate (one statistics pass)
     and the full error statistics (that pass plus the radix-selection passes
@@ -403,14 +433,27 @@ def bench_cmp(torch, hip, steps, warmup):
     ms_elem = per_call(lambda: hip.compare_expected(a, e, 0.008, 0.006))
     ms_stats = per_call(lambda: hip.compare_statistics(a, e, 0.008, 0.006))
     gbs = 2 * n * 2 / (ms_gate * 1e-3) / 1e9
+    cpu = cpu_s = None
+    if with_cpu:
+        from oracle import oracle as orc
+        ns = 16 << 20  # 16M-element sample of the same pair
+        ya, xe = y[:ns].cpu().view(torch.uint8).numpy(), x[:ns].cpu().view(torch.uint8).numpy()
+        dt = cpu_time(lambda: orc.compare_expected((10, (ns,), ya), (10, (ns,), xe), 0.008, 0.006, (0.9999, 0.01)))
+        cpu = cpu_gbs(2 * ns * 2, dt, f"{ns} of {n} elements of the same bf16 pair (scalar C oracle)")
+        nq = 4 << 20  # the statistics' quantile selection is the slow part: a 4M-element sample
+        dt_s = cpu_time(lambda: orc.compare_statistics((10, (nq,), ya[:2 * nq]), (10, (nq,), xe[:2 * nq]), 0.008,
+                                                       0.006))
+        cpu_s = {"elements_per_s": nq / dt_s, "cores": 1, "kind": "port",
+                 "sample": f"{nq} elements of the same pair, {dt_s:.3f} s wall"}
     return {
         "workload": "comparator gate (similarity policy) on a bf16 pair of 268,435,456 elements",
         "metric": "GB/s", "ms": ms_gate, "value": gbs, "unit": "GB/s",
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK["hbm"], "unit": "GB/s",
                      "frac": gbs / PEAK["hbm"], "traffic": None},
+        "cpu_baseline": cpu,
         "elementwise_gate": {"ms": ms_elem, "value": 2 * n * 2 / (ms_elem * 1e-3) / 1e9, "unit": "GB/s"},
         "statistics": {"workload": "full statistics incl. nearest-rank p99/p999 of |error| and ULP",
-                       "ms": ms_stats, "elements_per_s": n / (ms_stats * 1e-3)},
+                       "ms": ms_stats, "elements_per_s": n / (ms_stats * 1e-3), "cpu_baseline": cpu_s},
     }
 
 
@@ -464,7 +507,7 @@ def bench_vendor(torch, hip, steps, warmup):
 REGION_ROWS, REGION_COLS = 65536, 4096  # 256M elements: 512 MiB per bf16 tensor, twice the 256 MB last-level cache
 
 
-def bench_regions(torch, hip, steps, warmup):
+def bench_regions(torch, hip, steps, warmup, with_cpu=True):
     """The managed elementwise command and the fused regions at HBM scale:
     every tensor is 256M elements (512 MiB in bf16, 1 GiB in f32), twice the
     256 MB last-level cache, so each launch streams from HBM.  Algorithmic
@@ -477,39 +520,54 @@ def bench_regions(torch, hip, steps, warmup):
     n = R * C
     out = []
 
-    def leg(name, kernel, workload, fn, nbytes):
+    SR = 4096  # CPU sample: 4096 of the rows (16M elements)
+
+    def leg(name, kernel, workload, fn, nbytes, cpu_fn=None):
         ms = timed(torch, fn, steps, warmup)
         gbs = nbytes / (ms * 1e-3) / 1e9
-        out.append({"name": name, "kernel": kernel, "workload": workload, "ms": ms, "value": gbs, "unit": "GB/s",
-                    "algorithmic_bytes": nbytes,
-                    "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK["hbm"], "unit": "GB/s",
-                                 "frac": gbs / PEAK["hbm"], "traffic": traffic_for(name), "traffic_source": TRAFFIC_SOURCE}})
+        e = {"name": name, "kernel": kernel, "workload": workload, "ms": ms, "value": gbs, "unit": "GB/s",
+             "algorithmic_bytes": nbytes,
+             "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK["hbm"], "unit": "GB/s",
+                          "frac": gbs / PEAK["hbm"], "traffic": traffic_for(name), "traffic_source": TRAFFIC_SOURCE}}
+        if with_cpu and cpu_fn is not None:
+            dt = cpu_time(cpu_fn)
+            e["cpu_baseline"] = cpu_gbs(nbytes * SR // R, dt, f"{SR} of {R} rows of the same tensors (scalar C oracle)")
+        out.append(e)
+
+    from oracle import oracle as orc
+    h16 = lambda t: t[:SR].contiguous().cpu().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
 
     B = 2  # bytes per bf16 element
     x = rnd_bf16(torch, gen, (R, C))
     y = torch.empty_like(x)
     z = rnd_bf16(torch, gen, (R, C))
     from vibe_compiler_amd.backend import BF16, F32
+    xs, zs = h16(x), h16(z)
     leg("ew_add", "ew_kernel (Add)", f"managed elementwise Add, bf16, {n} elements",
-        lambda: hip.elementwise("Add", BF16, x, y, z), 3 * n * B)
-    leg("silu_mul", "silu_mul", f"silu(gate) * up, bf16, {n} elements", lambda: hip.silu_mul(x, z, y), 3 * n * B)
-    leg("gelu_tanh", "gelu_tanh", f"tanh-GELU, bf16, {n} elements", lambda: hip.gelu_tanh(x, y), 2 * n * B)
+        lambda: hip.elementwise("Add", BF16, x, y, z), 3 * n * B, lambda: orc.elementwise(8, orc.BF16, xs, zs))
+    leg("silu_mul", "silu_mul", f"silu(gate) * up, bf16, {n} elements", lambda: hip.silu_mul(x, z, y), 3 * n * B,
+        lambda: orc.silu_mul(xs, zs))
+    leg("gelu_tanh", "gelu_tanh", f"tanh-GELU, bf16, {n} elements", lambda: hip.gelu_tanh(x, y), 2 * n * B,
+        lambda: orc.gelu_tanh(xs))
     w = rnd_bf16(torch, gen, (C,))
+    ws = w.cpu().view(torch.int16).numpy().view(np.uint16)
     leg("rmsnorm", "rmsnorm", f"RMSNorm rows of {C}, bf16, {R} rows", lambda: hip.rmsnorm(x, w, y, 1e-5),
-        2 * n * B + C * B)
+        2 * n * B + C * B, lambda: orc.rmsnorm(xs, ws, 1e-5))
     leg("softmax", "softmax", f"row softmax over {C} columns, bf16, {R} rows", lambda: hip.softmax(x, y),
-        2 * n * B)
+        2 * n * B, lambda: orc.softmax(xs))
     xr, yr = x.view(R, 32, C // 32), y.view(R, 32, C // 32)
     pos = torch.arange(R, dtype=torch.int32, device="cuda")
+    xrs, ps = xs.reshape(SR, 32, C // 32), np.arange(SR, dtype=np.int32)
     leg("rope", "rope", f"RoPE (rotate-half, theta 1e4), bf16 [{R}, 32, {C // 32}]",
-        lambda: hip.rope(xr, yr, pos, 1e4), 2 * n * B + R * 4)
+        lambda: hip.rope(xr, yr, pos, 1e4), 2 * n * B + R * 4, lambda: orc.rope(xrs, ps, 1e4))
     del x, y, z, xr, yr
     torch.cuda.empty_cache()
     xf = torch.randn((R, C), device="cuda", generator=gen)
     yf = torch.empty_like(xf)
     bias = torch.randn((C,), device="cuda", generator=gen)
+    xfs, bs = xf[:SR].cpu().numpy(), bias.cpu().numpy()
     leg("bias_add", "bias_add", f"row bias add, f32 [{R}, {C}]", lambda: hip.bias_add(xf, bias, yf, fmt=F32),
-        2 * n * 4 + C * 4)
+        2 * n * 4 + C * 4, lambda: orc.bias_add(xfs, bs))
     del xf, yf
     torch.cuda.empty_cache()
     return out
@@ -565,11 +623,11 @@ def main() -> int:
     if "llama" in only:
         secondary.append(dict(name="llama_layer", **bench_llama(torch, hip, args.steps, args.warmup, with_cpu)))
     if "mv" in only:
-        secondary.append(dict(name="movement", **bench_mv(torch, hip, args.steps, args.warmup)))
+        secondary.append(dict(name="movement", **bench_mv(torch, hip, args.steps, args.warmup, with_cpu)))
     if "cmp" in only:
-        secondary.append(dict(name="comparator", **bench_cmp(torch, hip, args.steps, args.warmup)))
+        secondary.append(dict(name="comparator", **bench_cmp(torch, hip, args.steps, args.warmup, with_cpu)))
     if "regions" in only:
-        secondary.append({"name": "regions", "legs": bench_regions(torch, hip, args.steps, args.warmup)})
+        secondary.append({"name": "regions", "legs": bench_regions(torch, hip, args.steps, args.warmup, with_cpu)})
     if "copy" in only:
         secondary.append(dict(name="copy", **bench_copy(torch, args.steps, args.warmup)))
     if "vendor" in only:

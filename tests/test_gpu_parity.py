@@ -1111,3 +1111,42 @@ def test_fd_decode_group_path(hip, B, oracle, Bn, Hq, Hkv, L, chunks):
     o = torch.zeros((Bn, Hq, 1, 128), dtype=torch.int16, device="cuda")
     hip.attention_decode(u16(q), u16(k), u16(v), o, 0.088, chunks=chunks)
     attention_gate(oracle.bf16_to_f32(from_u16(o)), oracle.bf16_to_f32(ref), what="FD group path")
+
+
+def test_gelu_tanh_error_bound(hip, B):
+    """gelu_tanh evaluates 0.5*x*(1 + tanh(k0*(x + k1*x^3))) as
+    x / (1 + 2^(c*(x + k1*x^3))), c = -2*log2(e)*k0 (the same function:
+    1 + tanh(z) = 2 / (1 + e^(-2z))).  Bound, against a float64 evaluation
+    of that function over every finite bf16 value and dense f32 samples:
+    relative error <= 2^-24 * (8 + 3*|a|), a = c*(x + k1*x^3) the
+    exponent (v_exp_f32 and v_rcp_f32 add about an ulp each; the rounding of
+    the exponent's argument grows with |a|, and where |a| is large the
+    output is below |x| * 2^-|a|); outputs below 1e-30 within 1e-34
+    absolute.  Measured: 4 ulps for |x| < 1, 17 for |x| < 3, 238 at
+    |x| = 10 (a = 126, output ~1e-37).  Special values map as in the tanh
+    form: +inf -> +inf, -inf -> NaN, NaN -> NaN, signed zeros kept."""
+    bits = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    rng = np.random.default_rng(940)
+    x = np.concatenate([bits[np.isfinite(bits)], rng.uniform(-10, 10, 1 << 21).astype(np.float32),
+                        rng.uniform(-1e-2, 1e-2, 1 << 18).astype(np.float32)])
+    y = torch.empty(len(x), dtype=torch.float32, device="cuda")
+    hip.gelu_tanh(torch.from_numpy(x).cuda(), y, fmt=B.F32)
+    g = y.cpu().numpy().astype(np.float64)
+    xd = x.astype(np.float64)
+    k0, k1 = math.sqrt(2 / math.pi), 0.044715
+    with np.errstate(all="ignore"):
+        a = -2 * math.log2(math.e) * k0 * (xd + k1 * xd ** 3)
+        exact = xd / (1 + np.exp2(a))
+    fin = np.isfinite(exact)
+    assert np.array_equal(np.isfinite(g), fin)
+    big = fin & (np.abs(exact) > 1e-30)
+    err = np.abs(g - exact)
+    bound = 2.0 ** -24 * (8 + 3 * np.abs(a)) * np.abs(exact)
+    assert np.all(err[big] <= bound[big]), float(np.max(err[big] / bound[big]))
+    assert np.all(err[fin & ~big] <= 1e-34)
+    sp = np.array([0.0, -0.0, np.inf, -np.inf, np.nan], np.float32)
+    ys = torch.empty(len(sp), dtype=torch.float32, device="cuda")
+    hip.gelu_tanh(torch.from_numpy(sp).cuda(), ys, fmt=B.F32)
+    r = ys.cpu().numpy()
+    assert r[0] == 0 and not np.signbit(r[0]) and r[1] == 0 and np.signbit(r[1])
+    assert r[2] == np.inf and np.isnan(r[3]) and np.isnan(r[4])
