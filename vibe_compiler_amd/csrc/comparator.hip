@@ -6,10 +6,11 @@
 //
 // Both tensors stay in HBM.  One pass accumulates, per element of an F16 /
 // BF16 / F32 pair decoded exactly to double: the similarity sums (dot,
-// |a|^2, |e|^2, |a-e|^2) and the absolute-error sum (compensated per thread,
-// double-double across threads: an error bound of a few units in the last
-// place of a double, independent of the element count, where the
-// reference's in-order long double sums carry n * 2^-64), exact and
+// |a|^2, |e|^2, |a-e|^2) and the absolute-error sum (plain double within
+// groups of eight elements, compensated per thread, double-double across
+// threads: an error bound of about ten units in the last place of a double,
+// independent of the element count, where the reference's in-order long
+// double sums carry n * 2^-64), exact and
 // mismatch counts, the ULP-distance sum (exact, integer), maxima, the first
 // element that ends the comparison (non-finite actual / expected, non-finite
 // tolerance) and the mismatch samples the reference reports (first mismatch,
@@ -119,7 +120,8 @@ template <uint32_t F> __device__ inline bool decode(uint32_t bits, double &v) {
     v = (double)bf16_to_f32((uint16_t)bits);
     return ((bits >> 7) & 0xffu) != 0xffu;
   } else {
-    v = (double)f16_to_f32((uint16_t)bits);
+    // v_cvt_f32_f16 widens every finite f16 exactly (subnormals included)
+    v = (double)(float)__builtin_bit_cast(_Float16, (uint16_t)bits);
     return ((bits >> 10) & 0x1fu) != 0x1fu;
   }
 }
@@ -184,12 +186,105 @@ __device__ inline void visit(Acc &a, uint64_t i, uint32_t ab, uint32_t eb, doubl
   }
 }
 
+// Eight consecutive elements i0..i0+7, as visit() does them one by one,
+// except that the similarity sums (and the absolute-error sum) of the group
+// are first formed in plain double -- each term added with one rounding
+// (fma of the exact product, which is exact for F16 / BF16 / F32 operands)
+// -- and only the group sums go into the compensated per-thread sums.  The
+// error bound grows from Kahan's ~2u to ~10u of the sum of magnitudes, still
+// a few units in the last place of a double, and the f64 work per element
+// falls about threefold (the pass was bound by f64 issue, not HBM).
+// Elements that end the comparison (non-finite input or tolerance)
+// contribute no terms, as in visit().
+template <uint32_t F, int MODE>
+__device__ inline void visit8(Acc &a, uint64_t i0, const uint32_t (&ab)[8], const uint32_t (&eb)[8], double atol,
+                              double rtol) {
+  double pd = 0.0, pa = 0.0, pb = 0.0, pe = 0.0, pabs = 0.0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint64_t i = i0 + e;
+    double av, ev;
+    const bool fa = decode<F>(ab[e], av), fe = decode<F>(eb[e], ev);
+    if (!fa || !fe) {
+      const uint64_t code = 4 * i + (fa ? 2 : 1);
+      a.bad = a.bad < code ? a.bad : code;
+      continue;
+    }
+    const double ad = fabs(av - ev);
+    const double tol = atol + rtol * fabs(ev);
+    if (!isfinite(tol)) {
+      a.bad = a.bad < 4 * i + 3 ? a.bad : 4 * i + 3;
+      continue;
+    }
+    if constexpr (MODE != GATE_ELEMENTWISE) {
+      pd = __builtin_fma(av, ev, pd);
+      pa = __builtin_fma(av, av, pa);
+      pb = __builtin_fma(ev, ev, pb);
+      const double d = av - ev;
+      pe = __builtin_fma(d, d, pe);
+    }
+    if constexpr (MODE == FULL) {
+      pabs += ad;
+      a.exact += ad == 0.0;
+      const uint64_t u = ulp_distance<F>(ab[e], eb[e], av, ev);
+      a.ulp_sum += u;
+      a.max_ulp = a.max_ulp > u ? a.max_ulp : u;
+      a.max_abs = a.max_abs > ad ? a.max_abs : ad;
+    }
+    if (ad > tol) {
+      ++a.mism;
+      if constexpr (MODE != GATE_SIMILARITY) {
+        if (a.first_mm == NONE) a.first_mm = i;
+        take_max(a.mm_abs, a.mm_abs_idx, ad, i);
+        take_max(a.mm_ratio, a.mm_ratio_idx, tol == 0.0 ? INFINITY : ad / tol, i);
+      }
+    }
+  }
+  if constexpr (MODE != GATE_ELEMENTWISE) {
+    kahan_add(a.dot, pd);
+    kahan_add(a.aa, pa);
+    kahan_add(a.bb, pb);
+    kahan_add(a.ee, pe);
+  }
+  if constexpr (MODE == FULL) kahan_add(a.abs, pabs);
+}
+
 // Raw storage bits of element i.
 template <uint32_t F> __device__ inline uint32_t bits_at(const void *p, uint64_t i) {
   if constexpr (F == WAFER_FMT_F32)
     return ((const uint32_t *)p)[i];
   else
     return ((const uint16_t *)p)[i];
+}
+
+// The raw 16-byte words holding eight consecutive elements (one for 16-bit
+// formats, two for F32; bases 16-byte aligned, i a multiple of 8), and their
+// split into per-element bits.
+struct Raw8 {
+  u32x4 lo, hi;
+};
+template <uint32_t F> __device__ inline Raw8 raw8(const void *p, uint64_t i) {
+  Raw8 r;
+  if constexpr (F == WAFER_FMT_F32) {
+    r.lo = ((const u32x4 *)p)[i / 4];
+    r.hi = ((const u32x4 *)p)[i / 4 + 1];
+  } else {
+    r.lo = ((const u32x4 *)p)[i / 8];
+    r.hi = r.lo;
+  }
+  return r;
+}
+template <uint32_t F> __device__ inline void unpack8(const Raw8 &r, uint32_t (&b)[8]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if constexpr (F == WAFER_FMT_F32) {
+      b[e] = r.lo[e];
+      b[4 + e] = r.hi[e];
+    } else {
+      b[2 * e] = r.lo[e] & 0xffffu;
+      b[2 * e + 1] = r.lo[e] >> 16;
+    }
+  }
 }
 
 // Eight consecutive elements' bits with 16-byte loads (bases 16-byte aligned,
@@ -272,13 +367,34 @@ __device__ inline void block_reduce(Acc &a) {
 }
 
 template <uint32_t F, int MODE>
-__global__ __launch_bounds__(NT) void stats_kernel(const void *__restrict__ act, const void *__restrict__ exp,
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void stats_kernel(const void *__restrict__ act, const void *__restrict__ exp,
                                                    uint64_t n, bool vec, double atol, double rtol,
                                                    Acc *__restrict__ partials) {
   Acc a;
   acc_init(a);
-  for_each_element<F>(act, exp, n, vec,
-                      [&](uint64_t i, uint32_t ab, uint32_t eb) { visit<F, MODE>(a, i, ab, eb, atol, rtol); });
+  const uint64_t groups = vec ? n / 8 : 0;
+  const uint64_t step = (uint64_t)gridDim.x * NT;
+  // the next group's 16-byte loads are issued before the current group is
+  // visited, so their latency hides behind that work
+  uint64_t g = (uint64_t)blockIdx.x * NT + threadIdx.x;
+  Raw8 na{}, ne{};
+  if (g < groups) {
+    na = raw8<F>(act, g * 8);
+    ne = raw8<F>(exp, g * 8);
+  }
+  for (; g < groups; g += step) {
+    const Raw8 ca = na, ce = ne;
+    if (g + step < groups) {
+      na = raw8<F>(act, (g + step) * 8);
+      ne = raw8<F>(exp, (g + step) * 8);
+    }
+    uint32_t ab[8], eb[8];
+    unpack8<F>(ca, ab);
+    unpack8<F>(ce, eb);
+    visit8<F, MODE>(a, g * 8, ab, eb, atol, rtol);
+  }
+  for (uint64_t i = groups * 8 + (uint64_t)blockIdx.x * NT + threadIdx.x; i < n; i += step)
+    visit<F, MODE>(a, i, bits_at<F>(act, i), bits_at<F>(exp, i), atol, rtol);
   a.dot = kahan_to_dd(a.dot);
   a.aa = kahan_to_dd(a.aa);
   a.bb = kahan_to_dd(a.bb);
@@ -667,7 +783,17 @@ int run_stats(wafer_hip_context *ctx, uint32_t fmt, const void *act, const void 
   WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
   const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
   const uint64_t want = (n + (uint64_t)NT * 8 - 1) / ((uint64_t)NT * 8);
-  const int blocks = (int)std::max<uint64_t>(1, std::min<uint64_t>(want, (uint64_t)cus * 4));
+  // one full round of workgroups: as many per CU as the statistics kernel's
+  // registers allow (a second, partial round of a grid-stride pass would
+  // hold the whole pass for another block's share)
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)stats_kernel<WAFER_FMT_BF16, FULL>, NT, 0) !=
+          hipSuccess ||
+      per_cu < 1) {
+    (void)hipGetLastError();  // the query's failure is not the launch's
+    per_cu = 1;
+  }
+  const int blocks = (int)std::max<uint64_t>(1, std::min<uint64_t>(want, (uint64_t)cus * per_cu));
   const size_t acc_bytes = ((size_t)blocks + 1) * sizeof(Acc);
   const size_t sel_off = (acc_bytes + 255) & ~size_t(255);
   const size_t hist_off = sel_off + 256;
