@@ -224,44 +224,50 @@ def test_decoder_layer_vs_oracle_composition(hip, torch, oracle):
     assert mx <= 4 * ulp, (mx, ulp)
 
 
-# ------------------------------------------- llama-2-7b-block, F16 storage
+# ------------------------------------------- llama-2-7b-block, F16 and BF16
 # test/Board/PyTorch/wafer_pytorch_board_cases.py:817-866 with the
 # configuration test/Tools/Inputs/hf/llama-2-7b-block-config.json: hidden
 # 4096, 32 query and 32 KV heads of 128, intermediate 11008, RMSNorm eps 1e-5,
-# RoPE theta 1e4, float16; hidden_states [1, 16, 4096] ~ N(0, 1) * 0.125; the
-# HF comparison policy (:28-30): rtol 0.002, atol 0.004, cosine >= 0.9999,
-# relative L2 <= 0.01 (make_similarity_policy,
-# test/Board/PyTorch/wafer_pytorch_board_common.py:59-71).  Weights ~ N(0,
-# 0.02) (the configuration's initializer_range), norm weights 1.
+# RoPE theta 1e4, float16 (the case also runs bfloat16, :817-829);
+# hidden_states [1, 16, 4096] ~ N(0, 1) * 0.125; the HF comparison policy
+# (:28-30): rtol 0.002, atol 0.004, cosine >= 0.9999, relative L2 <= 0.01
+# (make_similarity_policy, test/Board/PyTorch/wafer_pytorch_board_common.py:
+# 59-71).  Weights ~ N(0, 0.02) (the configuration's initializer_range), norm
+# weights 1.
 L2B = dict(T=16, Hd=4096, Hq=32, Hkv=32, D=128, F=11008, eps=1e-5, theta=1e4)
 HF_RTOL, HF_ATOL = 0.002, 0.004
+# storage format: (torch dtype name, oracle format, mantissa bits, smallest normal exponent)
+L2B_FORMATS = {"f16": ("float16", 2, 10, -14), "bf16": ("bfloat16", 3, 7, -126)}
 
 
-def llama_2_7b_block_inputs(torch):
-    """Weights and input of the F16 block, drawn on the CPU (seeded), so the
-    same tensors can be formed without a GPU."""
+def llama_2_7b_block_inputs(torch, name="f16"):
+    """Weights and input of the block in the named storage format, drawn on
+    the CPU (seeded), so the same tensors can be formed without a GPU."""
     from vibe_compiler_amd import decoder_layer as DL
 
     c = L2B
+    dt = getattr(torch, L2B_FORMATS[name][0])
     gen = torch.Generator().manual_seed(817)
     W = DL.random_weights(torch, gen, hidden=c["Hd"], q_heads=c["Hq"], kv_heads=c["Hkv"], head_dim=c["D"],
-                          ffn=c["F"], dtype=torch.float16)
-    x = (torch.randn((c["T"], c["Hd"]), generator=gen) * 0.125).to(torch.float16)
+                          ffn=c["F"], dtype=dt)
+    x = (torch.randn((c["T"], c["Hd"]), generator=gen) * 0.125).to(dt)
     return W, x
 
 
-@pytest.fixture(scope="module")
-def llama_2_7b_block(hip, torch):
-    """(weights, input, backend output) of the F16 block, run once."""
+@pytest.fixture(scope="module", params=["f16", "bf16"])
+def llama_2_7b_block(hip, torch, request):
+    """(format name, weights, input, backend output, layer) of the block, run
+    once per storage format."""
     from vibe_compiler_amd import decoder_layer as DL
 
     c = L2B
-    print("llama-2-7b-block f16 [1,16,4096]", flush=True)
-    W, x = llama_2_7b_block_inputs(torch)
+    name = request.param
+    print(f"llama-2-7b-block {name} [1,16,4096]", flush=True)
+    W, x = llama_2_7b_block_inputs(torch, name)
     W = {k: v.cuda() for k, v in W.items()}
     x = x.cuda()
     layer = DL.DecoderLayer(hip, W, c["T"], hidden=c["Hd"], q_heads=c["Hq"], kv_heads=c["Hkv"], head_dim=c["D"],
-                            ffn=c["F"], eps=c["eps"], theta=c["theta"], dtype=torch.float16)
+                            ffn=c["F"], eps=c["eps"], theta=c["theta"], dtype=x.dtype)
     y = torch.empty_like(x)
     layer.forward(x, y)
     torch.cuda.synchronize()
@@ -269,7 +275,7 @@ def llama_2_7b_block(hip, torch):
     layer.forward(x, y2)
     torch.cuda.synchronize()
     assert torch.equal(y.view(torch.int16), y2.view(torch.int16)), "second forward differs"
-    return W, x, y, layer
+    return name, W, x, y, layer
 
 
 def hf_policy(actual, expected, what):
@@ -291,16 +297,17 @@ def hf_policy(actual, expected, what):
     return bad
 
 
-def test_llama_2_7b_block_f16_vs_oracle_composition(torch, oracle, llama_2_7b_block):
-    """The F16 block against the CPU oracle's composition of the same regions
-    over all 16 tokens (formal-order f16 GEMMs, RMSNorm, RoPE, online-softmax
+def test_llama_2_7b_block_vs_oracle_composition(torch, oracle, llama_2_7b_block):
+    """The block against the CPU oracle's composition of the same regions
+    over all 16 tokens (formal-order GEMMs, RMSNorm, RoPE, online-softmax
     attention in 64-key blocks, SiLU-mul, managed Add; every intermediate
-    rounded to f16 where the backend rounds it): the HF policy on y and on the
-    update y - x, every element within 4 f16 ulps at the largest |y|, and
-    the down projection with its residual Add (fed the backend's own x1 and
-    SwiGLU output) within one ulp of the product plus one of the sum.  The two sides differ only in
-    accumulation order (MFMA against k-order); one-ulp differences in the
-    early f16 intermediates spread through the later GEMMs, so about 0.3 % of
+    rounded to the storage format where the backend rounds it): the HF policy
+    on y and on the update y - x, every element within 4 ulps of the storage
+    format at the largest |y|, and the down projection with its residual Add
+    (fed the backend's own x1 and SwiGLU output) within one ulp of the
+    product plus one of the sum.  The two sides differ only in accumulation
+    order (MFMA against k-order); one-ulp differences in the early
+    intermediates spread through the later GEMMs, so in F16 about 0.3 % of
     the outputs fall outside rtol 0.002 / atol 0.004 here (the oracle
     composition itself has about 1.5 % outside against Hugging Face's float16
     layer)."""
@@ -308,74 +315,74 @@ def test_llama_2_7b_block_f16_vs_oracle_composition(torch, oracle, llama_2_7b_bl
 
     from tests.similarity import stats as sim_stats
 
-    W, x, y, layer = llama_2_7b_block
+    name, W, x, y, layer = llama_2_7b_block
+    _, FMT, MB, EMIN = L2B_FORMATS[name]
     c = L2B
     T, Hd, Hq, Hkv, D, F = c["T"], c["Hd"], c["Hq"], c["Hkv"], c["D"], c["F"]
-    H16 = oracle.F16
     u16 = lambda t: t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
     xb, yb = u16(x), u16(y)
     Wn = {k: u16(v) for k, v in W.items()}
-    gemm = lambda a, w, n: oracle.gemm_formal(H16, H16, a, w, a.shape[0], a.shape[1], n,  # noqa: E731
+    gemm = lambda a, w, n: oracle.gemm_formal(FMT, FMT, a, w, a.shape[0], a.shape[1], n,  # noqa: E731
                                               rhs_t=True).reshape(a.shape[0], n)
-    h = oracle.rmsnorm(xb, Wn["input_norm"], c["eps"], fmt=H16)
+    h = oracle.rmsnorm(xb, Wn["input_norm"], c["eps"], fmt=FMT)
     qkv = gemm(h, Wn["wqkv"], (Hq + 2 * Hkv) * D)
     pos = np.arange(T, dtype=np.int32)
-    q = oracle.rope(np.ascontiguousarray(qkv[:, :Hq * D]).reshape(T, Hq, D), pos, c["theta"], fmt=H16)
+    q = oracle.rope(np.ascontiguousarray(qkv[:, :Hq * D]).reshape(T, Hq, D), pos, c["theta"], fmt=FMT)
     k = oracle.rope(np.ascontiguousarray(qkv[:, Hq * D:(Hq + Hkv) * D]).reshape(T, Hkv, D), pos, c["theta"],
-                    fmt=H16)
+                    fmt=FMT)
     v = np.ascontiguousarray(qkv[:, (Hq + Hkv) * D:]).reshape(T, Hkv, D)
     hm = lambda t: np.ascontiguousarray(t.reshape(T, -1, D).transpose(1, 0, 2))[None]  # noqa: E731
-    o = oracle.attention_prefill(hm(q), hm(k), hm(v), 1.0 / math.sqrt(D), causal=True, block_k=64, fmt=H16)
+    o = oracle.attention_prefill(hm(q), hm(k), hm(v), 1.0 / math.sqrt(D), causal=True, block_k=64, fmt=FMT)
     o = np.ascontiguousarray(o[0].transpose(1, 0, 2)).reshape(T, Hq * D)
     add = 8  # TargetElementwiseOperation::Add
-    x1 = oracle.elementwise(add, H16, xb, gemm(o, Wn["wo"], Hd))
-    h2 = oracle.rmsnorm(x1, Wn["post_norm"], c["eps"], fmt=H16)
-    act = oracle.silu_mul(gemm(h2, Wn["wgate"], F), gemm(h2, Wn["wup"], F), fmt=H16)
-    yo = oracle.elementwise(add, H16, x1, gemm(act, Wn["wdown"], Hd))
-    f = lambda b: oracle.to_float(H16, b).reshape(b.shape).astype(np.float64)  # noqa: E731
+    x1 = oracle.elementwise(add, FMT, xb, gemm(o, Wn["wo"], Hd))
+    h2 = oracle.rmsnorm(x1, Wn["post_norm"], c["eps"], fmt=FMT)
+    act = oracle.silu_mul(gemm(h2, Wn["wgate"], F), gemm(h2, Wn["wup"], F), fmt=FMT)
+    yo = oracle.elementwise(add, FMT, x1, gemm(act, Wn["wdown"], Hd))
+    f = lambda b: oracle.to_float(FMT, b).reshape(b.shape).astype(np.float64)  # noqa: E731
     got, exp, xf = f(yb), f(yo), f(xb)
-    hf_policy(got, exp, "llama-2-7b-block y vs oracle")
+    hf_policy(got, exp, f"llama-2-7b-block {name} y vs oracle")
     cos_d, rel_d, _ = sim_stats(got - xf, exp - xf)
     print(f"update vs oracle: cos {cos_d:.7f} relL2 {rel_d:.6f}", flush=True)
     assert cos_d >= 0.9999 and rel_d <= 0.01
-    ulp = 2.0 ** (math.floor(math.log2(np.abs(exp).max())) - 10)
-    assert np.abs(got - exp).max() <= 4 * ulp
+    ulp = lambda a: 2.0 ** (np.floor(np.log2(np.maximum(np.abs(a), 2.0 ** EMIN))) - MB)  # noqa: E731
+    assert np.abs(got - exp).max() <= 4 * ulp(np.abs(exp).max())
     # the last GEMM and its residual Add on the backend's own inputs: at most
     # one ulp of the narrowed product (accumulation order) carried through
     # the Add's own rounding
     x1g, actg = u16(layer.x1), u16(layer.act)
     down = gemm(actg, Wn["wdown"], Hd)
-    yl = f(oracle.elementwise(add, H16, x1g, down))
-    ulp16 = lambda a: 2.0 ** (np.floor(np.log2(np.maximum(np.abs(a), 2.0 ** -14))) - 10)  # noqa: E731
-    assert np.all(np.abs(got - yl) <= ulp16(f(down)) + ulp16(yl))
+    yl = f(oracle.elementwise(add, FMT, x1g, down))
+    assert np.all(np.abs(got - yl) <= ulp(f(down)) + ulp(yl))
 
 
-def test_llama_2_7b_block_f16_vs_hugging_face(torch, llama_2_7b_block):
-    """The F16 block against the official Hugging Face LlamaDecoderLayer run
-    as the board case runs it for its expected output (float16, eval, CPU),
-    with the same weights and input: the HF policy on y and the cosine /
-    relative-L2 acceptance on the update y - x.  Elementwise, against the
-    float32 evaluation of the same layer, the backend has no more elements
-    outside rtol 0.002 / atol 0.004 than Hugging Face's own float16 output."""
+def test_llama_2_7b_block_vs_hugging_face(torch, llama_2_7b_block):
+    """The block against the official Hugging Face LlamaDecoderLayer run as
+    the board case runs it for its expected output (the case's dtype, eval,
+    CPU), with the same weights and input: the HF policy on y and the
+    cosine / relative-L2 acceptance on the update y - x.  Elementwise,
+    against the float32 evaluation of the same layer, the backend has no
+    more elements outside rtol 0.002 / atol 0.004 than Hugging Face's own
+    output in the same dtype."""
     pytest.importorskip("transformers")
     import numpy as np
 
     from tests.decoder_reference import hf_layer
     from tests.similarity import stats as sim_stats
 
-    W, x, y, _ = llama_2_7b_block
+    name, W, x, y, _ = llama_2_7b_block
     c = L2B
     Wc = {k: v.cpu() for k, v in W.items()}
-    ref = hf_layer(torch, x.cpu(), Wc, c["eps"], c["theta"], c["Hq"], c["Hkv"], c["D"], c["F"], torch.float16)
-    assert ref.dtype == torch.float16 and torch.isfinite(ref).all()
+    ref = hf_layer(torch, x.cpu(), Wc, c["eps"], c["theta"], c["Hq"], c["Hkv"], c["D"], c["F"], x.dtype)
+    assert ref.dtype == x.dtype and torch.isfinite(ref).all()
     got = y.float().cpu().numpy().astype(np.float64)
     exp = ref.float().numpy().astype(np.float64)
     xf = x.float().cpu().numpy().astype(np.float64)
-    hf_policy(got, exp, "llama-2-7b-block y vs HF float16")
+    hf_policy(got, exp, f"llama-2-7b-block {name} y vs HF")
     cos_d, rel_d, _ = sim_stats(got - xf, exp - xf)
-    print(f"update vs HF float16: cos {cos_d:.7f} relL2 {rel_d:.6f}", flush=True)
+    print(f"update vs HF {name}: cos {cos_d:.7f} relL2 {rel_d:.6f}", flush=True)
     assert cos_d >= 0.9999 and rel_d <= 0.01
     f32 = reference_layer(torch, x.cpu(), Wc, c["eps"], c["theta"], c["Hq"], c["Hkv"], c["D"]).double().numpy()
-    bad_gpu = hf_policy(got, f32, "llama-2-7b-block y vs float32 layer")
-    bad_hf = hf_policy(exp, f32, "HF float16 vs float32 layer")
+    bad_gpu = hf_policy(got, f32, f"llama-2-7b-block {name} y vs float32 layer")
+    bad_hf = hf_policy(exp, f32, f"HF {name} vs float32 layer")
     assert bad_gpu <= bad_hf, (bad_gpu, bad_hf)
