@@ -121,18 +121,21 @@ def test_causal_decode_two_tokens(hip, oracle, fmt, cap):
 
 
 @pytest.mark.parametrize("fmt", [F16, BF16], ids=["f16", "bf16"])
-def test_decode_kv_cache_two_steps(hip, oracle, fmt):
+@pytest.mark.parametrize("past0,cap", [(1023, 1040), (4094, 4096)], ids=["kv-cache", "kv-cache-long-4096"])
+def test_decode_kv_cache_two_steps(hip, oracle, fmt, past0, cap):
     """attention-decode-kv-cache at the Llama-2-7B layer shapes (32 heads MHA,
     head_dim 128, past 1023): step 1 appends one token and runs FD over 1024
     keys; the continuation consumes step 1's updated caches (past 1024 -> 1025
-    keys).  The case's projections and RoPE stay outside the attention
-    command; q and the new K / V are drawn directly."""
-    say("kv cache two steps", fmt)
-    rng = np.random.default_rng(1138 + fmt)
-    Hq, D, cap = 32, 128, 1040
+    keys).  attention-decode-kv-cache-long-4096 (:1528-1530) is the same two
+    steps from past 4094, ending with the cache full at 4096
+    (max_position_embeddings).  The case's projections and RoPE stay outside
+    the attention command; q and the new K / V are drawn directly."""
+    say("kv cache two steps", fmt, past0)
+    rng = np.random.default_rng(1138 + fmt + past0)
+    Hq, D = 32, 128
     kc = u16(store(oracle, fmt, rng.standard_normal((1, Hq, cap, D)) * 0.125))
     vc = u16(store(oracle, fmt, rng.standard_normal((1, Hq, cap, D))))
-    past = 1023
+    past = past0
     step1_k = None
     for step in range(2):
         q = store(oracle, fmt, rng.standard_normal((1, Hq, 1, D)) * 0.125)

@@ -15,23 +15,28 @@
 // acc = accL sL + accR sR.
 //
 // Mapping onto CDNA4:
-//  * a workgroup (8 waves) serves two 64-query blocks of one (batch, head):
-//    block n-1-i (phase A) and then block i (phase B) of the causal
-//    triangle, so every workgroup does the same amount of work (n-i + i+1
-//    key blocks) and one launch of heads*ceil(n/2) workgroups fills the CUs
+//  * a workgroup (8 waves) serves two 64-query blocks of one (batch, head),
+//    block n-1-i (late) and block i (early) of the causal triangle, side by
+//    side: every workgroup does the same amount of work (n-i + i+1 key
+//    blocks) and one launch of heads*ceil(n/2) workgroups fills the CUs
 //    evenly with no cross-workgroup merge (an odd n leaves the middle block
 //    alone in its workgroup).  Partial last blocks: padding queries load a
 //    clamped row and are not stored; keys past kv_len read as zero (each
 //    block's buffer resource is sized to its rows) and are masked;
-//  * wave w: query tile w&3 (16 queries of the current block), key half
-//    w>>2 (the even or the odd 64-key blocks).  All 8 waves work on the same
-//    query block, so each SIMD always carries two equally long chains whose
-//    MFMA and VALU work interleave; at the end of a phase the two key halves
-//    of a query tile merge through LDS;
-//  * scores are computed transposed, S^T = K . Q^T, on
-//    v_mfma_f32_16x16x32_{bf16,f16} (A = 16 keys x 32 d from LDS, B = Q^T kept in
-//    VGPRs): each lane holds 16 scores of one query, the 4 lanes of a query
-//    combine with permlane16/permlane32 swaps;
+//  * both blocks read the same two-block stages (their key ranges start at
+//    0; the early block's is a prefix of the late one's).  Waves 0-3 take
+//    the late block: query tile w & 1 (32 queries) and key half w >> 1 (the
+//    even or the odd 64-key blocks); the two halves of a tile merge through
+//    LDS at the end.  Waves 4-7 take the early block: 16 queries each over
+//    every key block (both blocks of each stage), so they need no merge.
+//    Waves w and w + 4 share a SIMD, so each SIMD carries one wave of each
+//    block and all SIMDs do the same work;
+//  * scores are computed transposed, S^T = K . Q^T (A = keys x d from LDS,
+//    B = Q^T kept in VGPRs): the late waves on v_mfma_f32_32x32x16 (each
+//    lane holds 32 scores of one query, the 2 lanes of a query combine with
+//    a permlane32 swap; every K and V fragment read feeds 32 queries), the
+//    early waves on v_mfma_f32_16x16x32 (16 scores per lane, the 4 lanes of
+//    a query combine with permlane16/permlane32 swaps);
 //  * the output is accumulated transposed as well, O^T = V^T . P^T: P^T feeds
 //    the MFMA B operand straight from the score registers after RNE narrowing
 //    (v_cvt_pk_{bf16,f16}_f32), and the V^T operand comes from row-major V in LDS
@@ -39,8 +44,8 @@
 //    group, lane i receives element i%4 of the 4-element vectors at the
 //    addresses of lanes 4e + i/4, e = 0..3);
 //  * K and V blocks move global -> LDS by buffer_load ... lds (no staging
-//    registers): two stages, the next block's DMA overlapping the current
-//    block's compute.  Rows are 256 bytes with 16-byte chunks XOR-swizzled
+//    registers): two stages, the next blocks' DMA overlapping the current
+//    blocks' compute.  Rows are 256 bytes with 16-byte chunks XOR-swizzled
 //    by 2 (row & 7), which keeps the ds_read_b128 K reads and the
 //    transposed V reads free of bank conflicts (measured: 128 banks per
 //    half-wave for b128 reads, 64 for b64 reads);
@@ -76,8 +81,6 @@ constexpr float RESCALE_LOG2 = 8.0f;
 constexpr float RESCALE_BOUND = 256.0f;  // 2^RESCALE_LOG2
 // __builtin_amdgcn_sched_group_barrier instruction classes
 constexpr int SG_MFMA = 0x008, SG_VMEM = 0x010, SG_DS_READ = 0x100;
-typedef short v4i16 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 // "no reference yet": the lowest finite float, so exp2(fma(s, c, -NOREF)) is
 // +inf (or at least 1) for a visible score and 0 for a masked one (never
 // NaN), exp2(NOREF - x) == 0 for x above NOREF + 150, and any visible score,
@@ -136,14 +139,28 @@ struct FaStrides {
   int64_t q[3], k[3], v[3], o[3];
 };
 
+// 32x32x16 MFMA on 8-element fragments of the storage type T
+template <typename T>
+__device__ inline f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (std::is_same_v<T, __bf16>)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+}
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
 template <typename T, bool CAUSAL, bool STRIDED = false>
 __global__ __launch_bounds__(THREADS) void fa_prefill_d128(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, uint16_t *__restrict__ O, int q_heads, int kv_heads,
     int q_len, int kv_len, float c, int bh_count, int n_qblocks, const FaStrides st = FaStrides{}) {
-  // two stages of [K half 0 | K half 1 | V half 0 | V half 1], 16 KiB each:
-  // rows of 256 bytes (64 keys x 128 d), 16-byte chunk ch of row r stored at
-  // chunk position ch ^ swz(r)
+  // two stages of [K block 2t | K block 2t+1 | V block 2t | V block 2t+1],
+  // 16 KiB each: rows of 256 bytes (64 keys x 128 d), 16-byte chunk ch of
+  // row r stored at chunk position ch ^ 2 (r & 7)
   __shared__ __align__(1024) uint16_t sbuf[2][4][BK * D];
 
   const int bid = blockIdx.x;
@@ -155,46 +172,37 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_d128(
   const uint16_t *Qp = STRIDED ? Q + b * st.q[0] + h * st.q[1] : Q + ((size_t)bh * q_len) * D;
   const uint16_t *Kp = STRIDED ? K + b * st.k[0] + kvh * st.k[1] : K + ((size_t)(b * kv_heads + kvh) * kv_len) * D;
   const uint16_t *Vp = STRIDED ? V + b * st.v[0] + kvh * st.v[1] : V + ((size_t)(b * kv_heads + kvh) * kv_len) * D;
+  uint16_t *Op = STRIDED ? O + b * st.o[0] + h * st.o[1] : O + ((size_t)bh * q_len) * D;
   // row strides in elements (D in the dense layout)
   const int64_t q_rs = STRIDED ? st.q[2] : D, k_rs = STRIDED ? st.k[2] : D, v_rs = STRIDED ? st.v[2] : D;
+  const int64_t o_rs = STRIDED ? st.o[2] : D;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int qt = wave & 3, half = wave >> 2;
-  const int l16 = lane & 15, g = lane >> 4;
-  // phase A serves the late query block n-1-pair, phase B the early one
-  // `pair` (none when they coincide: the middle block of an odd count).  The
-  // last query block and the last key block may be partial.
+  // the late query block n-1-pair (waves 0-3) and the early block `pair`
+  // (waves 4-7; none when they coincide: the middle block of an odd count)
+  // run side by side.  The last query block and the last key block may be
+  // partial.
   const int qb_a = n_qblocks - 1 - pair;
   const int qb_b = pair;
   const int kv_blocks = (kv_len + BK - 1) / BK;
   const int nk_a = CAUSAL ? min(kv_blocks, qb_a + 1) : kv_blocks;
   const int nk_b = qb_b < qb_a ? (CAUSAL ? min(kv_blocks, qb_b + 1) : kv_blocks) : 0;
-  const int ta = (nk_a + 1) / 2, niter = ta + (nk_b + 1) / 2;
+  const int niter = (nk_a + 1) / 2;  // iteration t works on key blocks 2t and 2t + 1
+  const int nite = (nk_b + 1) / 2;   // iterations in which the early block has keys
 
-  // Q^T as the MFMA B operand: lane holds query l16, d = 32 s + 8 g + [0,8)
-  // (rows past q_len load the last row and are never stored)
-  u32x4 qreg[4];
-  int q0 = qb_a * QB + qt * 16;
-  auto load_q = [&]() __attribute__((always_inline)) {
-    const int row = min(q0 + l16, q_len - 1);
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-      qreg[s] = *(const u32x4 *)(Qp + (size_t)row * q_rs + s * 32 + g * 8);
-  };
-  load_q();
-
-  // global -> LDS by buffer_load ... lds: the 4 waves of a key half move that
-  // half's K and V blocks, 4 + 4 instructions of 1 KiB (4 rows) per wave.
-  // Instruction j of wave qt writes rows 16 qt + 4 j + lane/16, chunk
-  // position lane%16, so lane loads global chunk (lane%16) ^ swz(row), with
-  // swz(row) = 2 (row & 7) = 8 (j & 1) + 2 (lane >> 4), which keeps the K
-  // fragment reads (ds_read_b128) and the transposed V reads
-  // (ds_read_b64_tr_b16) free of bank conflicts.
-  // One buffer resource per block, based at the block and sized to its rows
-  // (the hardware range check covers the lane offset, not the scalar one), so
-  // rows of a partial last block past kv_len read as zero.
+  // global -> LDS by buffer_load ... lds: wave w moves rows
+  // 16 (w >> 1) + 4 j + lane / 16 (j = 0..3) of the K and V blocks of key
+  // half w & 1 (block 2t + (w & 1)), 4 + 4 instructions of 1 KiB per wave
+  // and iteration.  Lane l writes chunk position l % 16, so it loads global
+  // chunk (l % 16) ^ swz(row), swz(row) = 2 (row & 7) = 8 (j & 1) + 2 (l >> 4),
+  // which keeps the K fragment reads (ds_read_b128) and the transposed V
+  // reads (ds_read_b64_tr_b16) free of bank conflicts.  One buffer resource
+  // per block, based at the block and sized to its rows (the hardware range
+  // check covers the lane offset, not the scalar one), so rows of a partial
+  // last block past kv_len read as zero.
+  const int dq = wave >> 1, dh = wave & 1;
   auto block_rsrc = [&](const uint16_t *base, int64_t rs, int kb) __attribute__((always_inline)) {
     const int rows = min(BK, kv_len - kb * BK);
     return __builtin_amdgcn_make_buffer_rsrc((void *)(base + (size_t)kb * BK * rs), 0,
@@ -203,271 +211,459 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_d128(
   uint32_t dma_off_k[4], dma_off_v[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int row = 16 * qt + 4 * j + (lane >> 4);
+    const int row = 16 * dq + 4 * j + (lane >> 4);
     const uint32_t chunk = (uint32_t)(((lane & 15) ^ (8 * (j & 1) + 2 * (lane >> 4))) << 4);
     dma_off_k[j] = (uint32_t)(row * k_rs * 2) + chunk;
     dma_off_v[j] = (uint32_t)(row * v_rs * 2) + chunk;
   }
-  // key block of iteration t for this half (t clamped to the last iteration,
-  // the block to the phase's last block: loads past the end are harmless)
-  auto block_of = [&](int t) __attribute__((always_inline)) {
-    t = min(t, niter - 1);
-    return t < ta ? min(2 * t + half, nk_a - 1) : min(2 * (t - ta) + half, nk_b - 1);
-  };
-  auto dma_k = [&](int kb, int buf) __attribute__((always_inline)) {
+  // this wave's share of iteration t's blocks (t clamped to the last
+  // iteration, the block to the late block's last: loads past the end are
+  // harmless)
+  auto dma_k = [&](int t, int buf) __attribute__((always_inline)) {
+    const int kb = min(2 * min(t, niter - 1) + dh, nk_a - 1);
     const __amdgpu_buffer_rsrc_t rsrc = block_rsrc(Kp, k_rs, __builtin_amdgcn_readfirstlane(kb));
-    uint16_t *dk = sbuf[buf][half] + qt * 4 * 512;
+    uint16_t *dk = sbuf[buf][dh] + dq * 4 * 512;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)(dk + j * 512), 16,
                                                dma_off_k[j], 0, 0, 0);
   };
-  auto dma_v = [&](int kb, int buf) __attribute__((always_inline)) {
+  auto dma_v = [&](int t, int buf) __attribute__((always_inline)) {
+    const int kb = min(2 * min(t, niter - 1) + dh, nk_a - 1);
     const __amdgpu_buffer_rsrc_t rsrc = block_rsrc(Vp, v_rs, __builtin_amdgcn_readfirstlane(kb));
-    uint16_t *dv = sbuf[buf][2 + half] + qt * 4 * 512;
+    uint16_t *dv = sbuf[buf][2 + dh] + dq * 4 * 512;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)(dv + j * 512), 16,
                                                dma_off_v[j], 0, 0, 0);
   };
+  auto lds_barrier = [&]() __attribute__((always_inline)) {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // LDS only: stores stay in flight
+  };
 
-  // LDS read offsets (bytes within a 16 KiB block), per lane:
-  //  K (A operand of S^T = K.Q^T, k-step s, key tile kt): row kt*16 + l16,
-  //    chunk 4 s + g, swz = 2 (l16 & 7)  ->  k_off[s] + kt * 4096
-  //  V^T (A operand of O^T = V^T.P^T via ds_read_b64_tr_b16, k-step s, key
-  //    half hh, d tile dt): lane reads row 32 s + 16 hh + 4 g + l16/4,
-  //    d 16 dt + 4 (l16 % 4) (chunk 2 dt + (l16/2) % 2, byte 8 (l16 % 2));
-  //    swz = 8 (g % 2) + 2 (l16 / 4)  ->  v_off[dt] + (32 s + 16 hh) * 256
-  uint32_t k_off[4], v_off[8];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) k_off[s] = (uint32_t)(l16 * 256 + (((4 * s + g) ^ (2 * (l16 & 7))) << 4));
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
-    v_off[dt] = (uint32_t)((4 * g + (l16 >> 2)) * 256 +
-                           (((2 * dt + ((l16 >> 1) & 1)) ^ (8 * (g & 1) + 2 * (l16 >> 2))) << 4) + 8 * (l16 & 1));
-
-  // per lane: the scaled reference max of query l16 (shared by the 4 lanes
-  // of the query; NOREF until the query has seen a visible key) and this
-  // lane's partial sum of P
-  float mc_ref = NOREF;
-  float l_part = 0.0f;
-  f32x4 acc_o[8];  // O^T rows dt*16 + 4 g + [0,4), column query l16
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc_o[dt][j] = 0.0f;
-
-  // one 64-key block: S^T = K.Q^T, online-softmax update, O^T += V^T.P^T.
-  // The exponentials are taken against the current reference first; a lane
-  // sum above 2^RESCALE_LOG2 (implied by any P above it, and by every
-  // visible score while there is no reference) sends the wave to the exact
-  // update: block max, reference moved if some query's max exceeds it by
-  // more than 2^RESCALE_LOG2, state rescaled, exponentials recomputed.
-  // `kdma` / `vdma` issue the next blocks' K / V moves: K's after this
-  // block's QK fragments and MFMAs are queued, V's one instruction per 4 PV
-  // MFMAs (a DMA issue stalls the wave; between queued MFMAs it costs
-  // little).
-  auto compute = [&](int kb, const char *sk, const char *sv, auto &&kdma, auto &&vdma) __attribute__((always_inline)) {
-    f32x4 sacc[4];  // S^T rows kt*16 + 4 g + [0,4)
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sacc[kt][j] = 0.0f;
-    u32x4 kf[4][4], vf[2][8];
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) kf[s][kt] = *(const u32x4 *)(sk + k_off[s] + kt * 4096);
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-        sacc[kt] = mfma16<T>(kf[s][kt], qreg[s], sacc[kt]);
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_v4i16 *)(sv + v_off[dt] + (32 * s) * 256));
-        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_v4i16 *)(sv + v_off[dt] + (32 * s + 16) * 256));
-        vf[s][dt] = __builtin_bit_cast(u32x4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-      }
-    kdma();
-    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 16, 0);
-    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 16, 0);
-    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 32, 0);
-    __builtin_amdgcn_sched_group_barrier(SG_VMEM, 4, 0);
-    // key kb*BK + kt*16 + 4 g + j is visible to query q0 + l16 iff it is
-    // below kv_len and (causal) not past the query
-    if ((CAUSAL && kb * BK + BK - 1 > q0) || kb * BK + BK > kv_len) {
-      const int lim = CAUSAL ? min(q0 + l16, kv_len - 1) : kv_len - 1;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (kb * BK + kt * 16 + 4 * g + j > lim) sacc[kt][j] = -__builtin_inff();
+  // Iteration t computes from stage t % 2 while every wave moves its share
+  // of iteration t+1's blocks into stage (t+1) % 2 (read last in iteration
+  // t-1, before the barrier that ended it), then waits for its own moves and
+  // meets the other waves at one barrier.  Both roles run the same loop and
+  // the same barriers.
+  auto run = [&](auto &&body) __attribute__((always_inline)) {
+    dma_k(0, 0);
+    dma_v(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // Q and the first blocks
+    __syncthreads();
+    auto step = [&](int t, auto slot) __attribute__((always_inline)) {
+      constexpr int P = decltype(slot)::value;  // == t % 2
+      // the next blocks' moves (after the last iteration a clamped, unused
+      // block: unconditional, so they can sit between the MFMAs)
+      auto kdma = [&]() __attribute__((always_inline)) { dma_k(t + 1, P ^ 1); };
+      auto vdma = [&]() __attribute__((always_inline)) { dma_v(t + 1, P ^ 1); };
+      body(t, slot, kdma, vdma);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    };
+    for (int t = 0; t < niter; t += 2) {
+      step(t, std::integral_constant<int, 0>{});
+      if (t + 1 < niter) step(t + 1, std::integral_constant<int, 1>{});
     }
-    f32x4 p[4];
-    float rs[4];
+  };
+
+  if (wave < 4) {
+    // ---- late block: wave w takes queries 32 (w & 1) + [0,32) and the key
+    // blocks of half w >> 1; the halves merge at the end.
+    // S^T = K.Q^T on v_mfma_f32_32x32x16 (A = 32 keys x 16 d from LDS,
+    // B = Q^T in VGPRs): each lane holds 32 scores of query l32 (keys
+    // 32 kt + 8 (r / 4) + 4 g2 + r % 4 of tile kt, register r), the
+    // other 32 sit in lane ^ 32.  O^T = V^T.P^T: P^T straight from the
+    // score registers (k-step ks = 2 kt + kk takes registers 8 kk .. 8 kk + 7
+    // of tile kt), V^T through ds_read_b64_tr_b16 in the same key order.
+    // Every K and V fragment feeds 32 queries.
+    const int lt = wave & 1, hh = wave >> 1;
+    const int l32 = lane & 31, g2 = lane >> 5;
+    const int q0 = qb_a * QB + 32 * lt;
+    // Q^T as the B operand: query l32, d = 16 s + 8 g2 + [0,8) (rows past
+    // q_len load the last row and are never stored)
+    u32x4 qr[8];
+    {
+      const int row = min(q0 + l32, q_len - 1);
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) p[kt][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][j], c, -mc_ref));
-      rs[kt] = (p[kt][0] + p[kt][1]) + (p[kt][2] + p[kt][3]);
+      for (int s = 0; s < 8; ++s) qr[s] = *(const u32x4 *)(Qp + (size_t)row * q_rs + s * 16 + g2 * 8);
     }
-    float rsum = (rs[0] + rs[1]) + (rs[2] + rs[3]);
-    if (__builtin_expect(__any(rsum > RESCALE_BOUND), 0)) {
-      float mx = -__builtin_inff();
+    // LDS byte offsets within a 16 KiB block:
+    //  K (d-step s, key tile kt): row 32 kt + l32, chunk 2 s + g2,
+    //    swz = 2 (l32 & 7)  ->  ko[s] + kt * 8192
+    //  V^T (d tile dt, k-step ks, half hi): in 16-lane group q16 = lane / 16
+    //    lane i reads row 16 ks + 8 hi + 4 g2 + i / 4, d 32 dt + 16 (q16 % 2)
+    //    + 4 (i % 4) and receives d 32 dt + l32 at keys 16 ks + 8 hi + 4 g2
+    //    + [0,4)  ->  vo[dt] + (16 ks + 8 hi) * 256
+    uint32_t ko[8], vo[4];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) ko[s] = (uint32_t)(l32 * 256 + (((2 * s + g2) ^ (2 * (l32 & 7))) << 4));
+    {
+      const int q16 = lane >> 4, i16 = lane & 15;
+      const int vrow = 4 * g2 + (i16 >> 2);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+        vo[dt] = (uint32_t)(vrow * 256 + (((4 * dt + 2 * (q16 & 1) + ((i16 >> 1) & 1)) ^ (2 * (vrow & 7))) << 4) +
+                            8 * (i16 & 1));
+    }
+    float mref = NOREF;  // scaled reference max of query l32 (shared with lane ^ 32)
+    float lsum = 0.0f;   // this lane's partial sum of P
+    f32x16 oacc[4];      // O^T d tile dt: d 32 dt + 8 (r / 4) + 4 g2 + r % 4, query l32
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.0f;
+
+    auto compute = [&](int kb, const char *sk, const char *sv, auto &&kdma, auto &&vdma)
+                       __attribute__((always_inline)) {
+      f32x16 sc[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[kt][r] = 0.0f;
+      // K fragments two d-steps ahead of their MFMAs; then the V fragments
+      // of k-steps 0 and 1, which land during the softmax
+      u32x4 kf[8][2];
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) kf[s][kt] = *(const u32x4 *)(sk + ko[s] + kt * 8192);
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) sc[kt] = mfma32<T>(kf[s][kt], qr[s], sc[kt]);
+      u32x4 vf[4][4];
+      auto read_v = [&](int ks) __attribute__((always_inline)) {
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)(sv + vo[dt] + (16 * ks) * 256));
+          const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)(sv + vo[dt] + (16 * ks + 8) * 256));
+          vf[ks][dt] = __builtin_bit_cast(u32x4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+      };
+      read_v(0);
+      read_v(1);
+      kdma();
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 4, 0);
+#pragma unroll
+      for (int s = 0; s < 6; ++s) {
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 16, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_VMEM, 4, 0);
+      // key kb*BK + 32 kt + 8 (r / 4) + 4 g2 + r % 4 is visible to query
+      // q0 + l32 iff it is below kv_len and (causal) not past the query
+      if ((CAUSAL && kb * BK + BK - 1 > q0) || kb * BK + BK > kv_len) {
+        const int lim = CAUSAL ? min(q0 + l32, kv_len - 1) : kv_len - 1;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (kb * BK + 32 * kt + 8 * (r >> 2) + 4 * g2 + (r & 3) > lim) sc[kt][r] = -__builtin_inff();
+      }
+      f32x16 p[2];
+      float rsum;
+      auto expo = [&]() __attribute__((always_inline)) {
+        float rs[8];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              p[kt][4 * r4 + j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][4 * r4 + j], c, -mref));
+            rs[4 * kt + r4] = (p[kt][4 * r4] + p[kt][4 * r4 + 1]) + (p[kt][4 * r4 + 2] + p[kt][4 * r4 + 3]);
+          }
+        rsum = ((rs[0] + rs[1]) + (rs[2] + rs[3])) + ((rs[4] + rs[5]) + (rs[6] + rs[7]));
+      };
+      expo();
+      if (__builtin_expect(__any(rsum > RESCALE_BOUND), 0)) {
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[kt][r]);
+        mx = xor32_max(mx);
+        const float mc_new = mx * c;
+        if (mx != -__builtin_inff() && mc_new > mref + RESCALE_LOG2) {
+          const float alpha = __builtin_amdgcn_exp2f(mref - mc_new);  // 0 from NOREF
+          lsum *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+          mref = mc_new;
+        }
+        expo();
+      }
+      lsum += rsum;
+      typedef T t8 __attribute__((ext_vector_type(8)));
+      u32x4 pb[4];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          t8 x;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) x[j] = (T)p[kt][8 * kk + j];
+          pb[2 * kt + kk] = __builtin_bit_cast(u32x4, x);
+        }
+      // V fragments of k-steps 2 and 3 while those of 0 and 1 feed the MFMAs
+      read_v(2);
+      read_v(3);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) oacc[dt] = mfma32<T>(vf[ks][dt], pb[ks], oacc[dt]);
+      vdma();
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 8, 1);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 4, 1);
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 8, 1);
+      __builtin_amdgcn_sched_group_barrier(SG_VMEM, 1, 1);
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 4, 1);
+        __builtin_amdgcn_sched_group_barrier(SG_VMEM, 1, 1);
+      }
+    };
+
+    run([&](int t, auto slot, auto &&kdma, auto &&vdma) __attribute__((always_inline)) {
+      constexpr int P = decltype(slot)::value;
+      const int kb = 2 * t + hh;
+      if (kb < nk_a) {
+        compute(kb, (const char *)sbuf[P][hh], (const char *)sbuf[P][2 + hh], kdma, vdma);
+      } else {
+        asm volatile("" ::: "memory");  // keeps the moves from being hoisted out of compute
+        kdma();
+        vdma();
+      }
+    });
+
+    // The two key halves of a query tile merge by a reduce-scatter through
+    // LDS (free after the loop's last barrier): half H keeps d tiles 2 H and
+    // 2 H + 1, hands the other two to its partner, merges the partner's two
+    // into its own, normalises and writes them.  Exchange layout: 16-byte
+    // vectors [lt][writer half][tile][r / 4][lane], then the (reference max,
+    // lane sum) pairs.  Each state is (acc, l) relative to its scaled
+    // reference max; a state that saw no visible key (NOREF) has l == 0 and
+    // acc == 0 (state merge of OnlineAttentionMaterialization.cpp:264-373,
+    // finalize :197-262).
+    auto merge_h = [&](auto half_c) __attribute__((always_inline)) {
+      constexpr int H = decltype(half_c)::value;  // == hh, so every tile index is static
+      f32x4 *xacc = (f32x4 *)&sbuf[0][0][0];      // 32 KiB
+      float *xml = (float *)(xacc + 2 * 2 * 2 * 4 * 64);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const f32x16 &a = oacc[2 * (1 - H) + i];
+          xacc[(((lt * 2 + H) * 2 + i) * 4 + rq) * 64 + lane] =
+              f32x4{a[4 * rq], a[4 * rq + 1], a[4 * rq + 2], a[4 * rq + 3]};
+        }
+      xml[((lt * 2 + H) * 2 + 0) * 64 + lane] = mref;
+      xml[((lt * 2 + H) * 2 + 1) * 64 + lane] = lsum;
+      lds_barrier();
+      const float m1 = xml[((lt * 2 + (1 - H)) * 2 + 0) * 64 + lane];
+      const float l1 = xml[((lt * 2 + (1 - H)) * 2 + 1) * 64 + lane];
+      const float e = fmaxf(mref, m1);
+      const float s0 = __builtin_amdgcn_exp2f(mref - e);
+      const float s1 = __builtin_amdgcn_exp2f(m1 - e);
+      const float l = xor32_sum(lsum * s0 + l1 * s1);
+      // finalize: coefficient = Recip(l) (0 for an empty row), out = T(acc * coef)
+      const float coef = (l == 0.0f) ? 0.0f : 1.0f / l;
+      uint16_t *orow = Op + (int64_t)(q0 + l32) * o_rs + 4 * g2;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int dt = 2 * H + i;
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const f32x4 o = xacc[(((lt * 2 + (1 - H)) * 2 + i) * 4 + rq) * 64 + lane];
+          f32x4 r;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) r[j] = (oacc[dt][4 * rq + j] * s0 + o[j] * s1) * coef;
+          u32x2 packed;
+          packed[0] = narrow_pair<T>(r[0], r[1]);
+          packed[1] = narrow_pair<T>(r[2], r[3]);
+          if (q0 + l32 < q_len) *(u32x2 *)(orow + dt * 32 + rq * 8) = packed;
+        }
+      }
+      // a distinct marker per half: keeps the two copies from being merged
+      // into one tail that would index oacc at run time (and spill it)
+      asm volatile("; fa merge tail %0" ::"n"(H));
+    };
+    if (hh == 0)  // wave-uniform
+      merge_h(std::integral_constant<int, 0>{});
+    else
+      merge_h(std::integral_constant<int, 1>{});
+  } else {
+    // ---- early block: wave 4 + e takes queries 16 e + [0,16) over every
+    // key block (both blocks of each stage), so it needs no merge.
+    // S^T = K.Q^T on v_mfma_f32_16x16x32 (A = 16 keys x 32 d from LDS,
+    // B = Q^T in VGPRs): each lane holds 16 scores of query l16, the 4 lanes
+    // of a query combine with permlane16/permlane32 swaps.  O^T = V^T.P^T
+    // with P^T from the score registers and V^T through ds_read_b64_tr_b16
+    // (within each 16-lane group, lane i receives element i%4 of the
+    // 4-element vectors at the addresses of lanes 4e + i/4, e = 0..3).
+    const int l16 = lane & 15, g = lane >> 4;
+    const int q0 = qb_b * QB + (wave - 4) * 16;
+    // Q^T as the MFMA B operand: lane holds query l16, d = 32 s + 8 g + [0,8)
+    u32x4 qreg[4];
+    {
+      const int row = min(q0 + l16, q_len - 1);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) qreg[s] = *(const u32x4 *)(Qp + (size_t)row * q_rs + s * 32 + g * 8);
+    }
+    // LDS read offsets (bytes within a 16 KiB block), per lane:
+    //  K (A operand, k-step s, key tile kt): row kt*16 + l16, chunk 4 s + g,
+    //    swz = 2 (l16 & 7)  ->  k_off[s] + kt * 4096
+    //  V^T (A operand via ds_read_b64_tr_b16, k-step s, key half hx, d tile
+    //    dt): lane reads row 32 s + 16 hx + 4 g + l16/4, d 16 dt + 4 (l16 % 4)
+    //    (chunk 2 dt + (l16/2) % 2, byte 8 (l16 % 2));
+    //    swz = 8 (g % 2) + 2 (l16 / 4)  ->  v_off[dt] + (32 s + 16 hx) * 256
+    uint32_t k_off[4], v_off[8];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) k_off[s] = (uint32_t)(l16 * 256 + (((4 * s + g) ^ (2 * (l16 & 7))) << 4));
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+      v_off[dt] = (uint32_t)((4 * g + (l16 >> 2)) * 256 +
+                             (((2 * dt + ((l16 >> 1) & 1)) ^ (8 * (g & 1) + 2 * (l16 >> 2))) << 4) + 8 * (l16 & 1));
+    float mc_ref = NOREF;  // scaled reference max of query l16 (shared by its 4 lanes)
+    float l_part = 0.0f;   // this lane's partial sum of P
+    f32x4 acc_o[8];        // O^T rows dt*16 + 4 g + [0,4), column query l16
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc_o[dt][j] = 0.0f;
+
+    auto compute = [&](int kb, const char *sk, const char *sv, auto &&kdma, auto &&vdma)
+                       __attribute__((always_inline)) {
+      f32x4 sacc[4];  // S^T rows kt*16 + 4 g + [0,4)
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
-        mx = fmaxf(mx, fmaxf(fmaxf(sacc[kt][0], sacc[kt][1]), fmaxf(sacc[kt][2], sacc[kt][3])));
-      mx = xor16_max(xor32_max(mx));
-      const float mc_new = mx * c;
-      if (mx != -__builtin_inff() && mc_new > mc_ref + RESCALE_LOG2) {
-        const float alpha = __builtin_amdgcn_exp2f(mc_ref - mc_new);  // 0 from NOREF
-        l_part *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
+        for (int j = 0; j < 4; ++j) sacc[kt][j] = 0.0f;
+      u32x4 kf[4][4], vf[2][8];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc_o[dt][j] *= alpha;
-        mc_ref = mc_new;
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) kf[s][kt] = *(const u32x4 *)(sk + k_off[s] + kt * 4096);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) sacc[kt] = mfma16<T>(kf[s][kt], qreg[s], sacc[kt]);
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)(sv + v_off[dt] + (32 * s) * 256));
+          const v4i16 hi =
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)(sv + v_off[dt] + (32 * s + 16) * 256));
+          vf[s][dt] = __builtin_bit_cast(u32x4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+      kdma();
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 16, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 16, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 32, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_VMEM, 4, 0);
+      // key kb*BK + kt*16 + 4 g + j is visible to query q0 + l16 iff it is
+      // below kv_len and (causal) not past the query
+      if ((CAUSAL && kb * BK + BK - 1 > q0) || kb * BK + BK > kv_len) {
+        const int lim = CAUSAL ? min(q0 + l16, kv_len - 1) : kv_len - 1;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (kb * BK + kt * 16 + 4 * g + j > lim) sacc[kt][j] = -__builtin_inff();
       }
+      f32x4 p[4];
+      float rs[4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) p[kt][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][j], c, -mc_ref));
         rs[kt] = (p[kt][0] + p[kt][1]) + (p[kt][2] + p[kt][3]);
       }
-      rsum = (rs[0] + rs[1]) + (rs[2] + rs[3]);
-    }
-    l_part += rsum;
-    // P^T operand of k-step s: slots 8 g + [0,4) are keys 32 s + 4 g + [0,4)
-    // (tile 2 s), slots 8 g + [4,8) keys 32 s + 16 + 4 g + [0,4) (tile 2 s + 1)
-    typedef T t8 __attribute__((ext_vector_type(8)));
-    u32x4 pb[2];
+      float rsum = (rs[0] + rs[1]) + (rs[2] + rs[3]);
+      if (__builtin_expect(__any(rsum > RESCALE_BOUND), 0)) {
+        float mx = -__builtin_inff();
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      t8 x;
+        for (int kt = 0; kt < 4; ++kt)
+          mx = fmaxf(mx, fmaxf(fmaxf(sacc[kt][0], sacc[kt][1]), fmaxf(sacc[kt][2], sacc[kt][3])));
+        mx = xor16_max(xor32_max(mx));
+        const float mc_new = mx * c;
+        if (mx != -__builtin_inff() && mc_new > mc_ref + RESCALE_LOG2) {
+          const float alpha = __builtin_amdgcn_exp2f(mc_ref - mc_new);  // 0 from NOREF
+          l_part *= alpha;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        x[j] = (T)p[2 * s][j];
-        x[4 + j] = (T)p[2 * s + 1][j];
+          for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc_o[dt][j] *= alpha;
+          mc_ref = mc_new;
+        }
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) p[kt][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][j], c, -mc_ref));
+          rs[kt] = (p[kt][0] + p[kt][1]) + (p[kt][2] + p[kt][3]);
+        }
+        rsum = (rs[0] + rs[1]) + (rs[2] + rs[3]);
       }
-      pb[s] = __builtin_bit_cast(u32x4, x);
-    }
+      l_part += rsum;
+      // P^T operand of k-step s: slots 8 g + [0,4) are keys 32 s + 4 g + [0,4)
+      // (tile 2 s), slots 8 g + [4,8) keys 32 s + 16 + 4 g + [0,4) (tile 2 s + 1)
+      typedef T t8 __attribute__((ext_vector_type(8)));
+      u32x4 pb[2];
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+      for (int s = 0; s < 2; ++s) {
+        t8 x;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-        acc_o[dt] = mfma16<T>(vf[s][dt], pb[s], acc_o[dt]);
-    vdma();
+        for (int j = 0; j < 4; ++j) {
+          x[j] = (T)p[2 * s][j];
+          x[4 + j] = (T)p[2 * s + 1][j];
+        }
+        pb[s] = __builtin_bit_cast(u32x4, x);
+      }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 4, 1);
-      __builtin_amdgcn_sched_group_barrier(SG_VMEM, 1, 1);
-    }
-  };
-
-  // The two key halves of one query tile merge by a reduce-scatter through
-  // LDS (`xr`, free at the call): half h keeps d tiles 4 h .. 4 h + 3,
-  // hands the other four to its partner, merges the partner's four into its
-  // own, normalises and writes them.  Exchange layout: 16-byte vectors,
-  // [qt][writer half][tile][lane] (1 KiB rows: b128 without conflicts), then
-  // the (reference max, lane sum) pairs.  Each state is (acc, l) relative to
-  // its scaled reference max; a state that never saw a visible key (NOREF)
-  // has l == 0 and acc == 0.
-  auto lds_barrier = [&]() __attribute__((always_inline)) {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // LDS only: stores stay in flight
-  };
-  auto finish_h = [&](float *xr, bool last, auto half_c) __attribute__((always_inline)) {
-    constexpr int H = decltype(half_c)::value;  // == half, so every tile index is static
-    f32x4 *xacc = (f32x4 *)xr;                  // [qt][half][4][lane]: 32 KiB
-    float *xml = xr + 4 * 2 * 4 * 64 * 4;       // [qt][half][2][lane]
+      for (int s = 0; s < 2; ++s)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xacc[((qt * 2 + H) * 4 + i) * 64 + lane] = acc_o[4 * (1 - H) + i];
-    xml[((qt * 2 + H) * 2 + 0) * 64 + lane] = mc_ref;
-    xml[((qt * 2 + H) * 2 + 1) * 64 + lane] = l_part;
-    lds_barrier();
-    const float m1 = xml[((qt * 2 + (1 - H)) * 2 + 0) * 64 + lane];
-    const float l1 = xml[((qt * 2 + (1 - H)) * 2 + 1) * 64 + lane];
-    const float e = fmaxf(mc_ref, m1);
-    const float s0 = __builtin_amdgcn_exp2f(mc_ref - e);
-    const float s1 = __builtin_amdgcn_exp2f(m1 - e);
-    const float l = xor16_sum(xor32_sum(l_part * s0 + l1 * s1));
-    // finalize: coefficient = Recip(l) (0 for an empty row), out = T(acc * coef)
-    const float coef = (l == 0.0f) ? 0.0f : 1.0f / l;
-    uint16_t *orow = (STRIDED ? O + b * st.o[0] + h * st.o[1] + (int64_t)(q0 + l16) * st.o[2]
-                              : O + ((size_t)bh * q_len + q0 + l16) * D) + 4 * g;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int dt = 4 * H + i;
-      const f32x4 o = xacc[((qt * 2 + (1 - H)) * 4 + i) * 64 + lane];
-      f32x4 r;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) r[j] = (acc_o[dt][j] * s0 + o[j] * s1) * coef;
-      u32x2 packed;
-      packed[0] = narrow_pair<T>(r[0], r[1]);
-      packed[1] = narrow_pair<T>(r[2], r[3]);
-      if (q0 + l16 < q_len) *(u32x2 *)(orow + dt * 16) = packed;
-    }
-    if (!last) lds_barrier();  // exchange reads done before the buffers are reused
-    // a distinct marker per half: keeps the two copies from being merged
-    // into one tail that would index acc_o at run time (and spill it)
-    asm volatile("; fa merge tail %0" ::"n"(H));
-  };
-  auto finish = [&](float *xr, bool last) __attribute__((always_inline)) {
-    if (half == 0)  // wave-uniform
-      finish_h(xr, last, std::integral_constant<int, 0>{});
-    else
-      finish_h(xr, last, std::integral_constant<int, 1>{});
-  };
-
-  // Pipeline (iteration t works on block_of(t) of each half): stage t%2
-  // holds iteration t's blocks.  Iteration t moves iteration t+1's blocks
-  // into stage (t+1)%2 (read last in iteration t-1, before the barrier that
-  // ended it) while it computes from stage t%2, waits for its own moves and
-  // meets the other waves at one barrier.  After the last iteration of
-  // phase A stage t%2 is free until the next DMA: the halves merge there and
-  // phase B starts with a fresh state.
-  dma_k(block_of(0), 0);
-  dma_v(block_of(0), 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // Q and the first blocks
-  __syncthreads();
-
-  auto step = [&](int t, auto slot) __attribute__((always_inline)) {
-    constexpr int P = decltype(slot)::value;  // == t % 2
-    // the next blocks' moves (after the last iteration a clamped, unused
-    // block: unconditional, so they can sit between the MFMAs)
-    auto kdma = [&]() __attribute__((always_inline)) { dma_k(block_of(t + 1), P ^ 1); };
-    auto vdma = [&]() __attribute__((always_inline)) { dma_v(block_of(t + 1), P ^ 1); };
-    const int kb = t < ta ? 2 * t + half : 2 * (t - ta) + half;
-    if (kb < (t < ta ? nk_a : nk_b)) {
-      compute(kb, (const char *)sbuf[P][half], (const char *)sbuf[P][2 + half], kdma, vdma);
-    } else {
-      asm volatile("" ::: "memory");  // keeps the moves from being hoisted out of compute
-      kdma();
+        for (int dt = 0; dt < 8; ++dt) acc_o[dt] = mfma16<T>(vf[s][dt], pb[s], acc_o[dt]);
       vdma();
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (t == ta - 1 && niter > ta) {
-      finish((float *)&sbuf[P][0][0], false);  // 64 KiB, free until the next DMA
-      q0 = qb_b * QB + qt * 16;
-      load_q();
-      mc_ref = NOREF;
-      l_part = 0.0f;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
+      for (int i = 0; i < 4; ++i) {
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 4, 1);
+        __builtin_amdgcn_sched_group_barrier(SG_VMEM, 1, 1);
+      }
+    };
+    auto nop = [&]() __attribute__((always_inline)) {};
+
+    run([&](int t, auto slot, auto &&kdma, auto &&vdma) __attribute__((always_inline)) {
+      constexpr int P = decltype(slot)::value;
+      if (t < nite) {
+        compute(2 * t, (const char *)sbuf[P][0], (const char *)sbuf[P][2], kdma, vdma);
+        if (2 * t + 1 < nk_b) compute(2 * t + 1, (const char *)sbuf[P][1], (const char *)sbuf[P][3], nop, nop);
+        if (t == nite - 1) {
+          // finalize: coefficient = Recip(l) (0 for an empty row), out = T(acc * coef)
+          const float l = xor16_sum(xor32_sum(l_part));
+          const float coef = (l == 0.0f) ? 0.0f : 1.0f / l;
+          uint16_t *orow = Op + (int64_t)(q0 + l16) * o_rs + 4 * g;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc_o[dt][j] = 0.0f;
-    }
-  };
-  for (int t = 0; t < niter; t += 2) {
-    step(t, std::integral_constant<int, 0>{});
-    if (t + 1 < niter) step(t + 1, std::integral_constant<int, 1>{});
+          for (int dt = 0; dt < 8; ++dt) {
+            u32x2 packed;
+            packed[0] = narrow_pair<T>(acc_o[dt][0] * coef, acc_o[dt][1] * coef);
+            packed[1] = narrow_pair<T>(acc_o[dt][2] * coef, acc_o[dt][3] * coef);
+            if (q0 + l16 < q_len) *(u32x2 *)(orow + dt * 16) = packed;
+          }
+        }
+      } else {
+        asm volatile("" ::: "memory");
+        kdma();
+        vdma();
+      }
+    });
+    lds_barrier();  // the late waves' merge barrier
   }
-  finish((float *)&sbuf[0][0][0], true);
 }
 
 // one launch of the kernel for the storage format (BF16 or F16)
