@@ -467,16 +467,18 @@ def test_mfma_gemm_vs_formal(hip, B, oracle, m, k, n, rt, fmt):
     assert rel <= 2e-3 and np.abs(gf - ref).max() <= 2e-2 * np.abs(ref).max()
 
 
-@pytest.mark.parametrize("rt,fmt,out", [(1, 3, 3), (0, 3, 5), (1, 2, 2)])
-def test_mfma_gemm_256_tiles_vs_formal(hip, B, oracle, rt, fmt, out):
-    """m = n = 4096, k = 1024: 256 tiles of 256x256, which takes the 256x256
-    instantiation (used only from 192 such tiles on).  Sampled rows against
+@pytest.mark.parametrize("rt,fmt,out,K", [(1, 3, 3, 1024), (0, 3, 5, 1024), (1, 2, 2, 1024), (1, 3, 3, 192),
+                                          (1, 2, 2, 64)])
+def test_mfma_gemm_256_tiles_vs_formal(hip, B, oracle, rt, fmt, out, K):
+    """m = n = 4096: 256 tiles of 256x256, which takes the 256x256
+    instantiation (used only from 192 such tiles on); k = 192 and 64 give an
+    odd number of 128-byte K stages and a single one.  Sampled rows against
     the formal lane run on the GPU (bit-exact k-order fma chains; itself
     pinned against the CPU oracle on two rows here), held to the MFMA GEMM
     tolerances: f32 out relL2 <= 1e-5, narrowed out relL2 <= 2e-3."""
-    say("mfma gemm 256x256 tiles", rt, fmt, out)
-    rng = np.random.default_rng(4096 + 10 * rt + fmt)
-    M, K, N = 4096, 1024, 4096
+    say("mfma gemm 256x256 tiles", rt, fmt, out, K)
+    rng = np.random.default_rng(4096 + 10 * rt + fmt + K)
+    M, N = 4096, 4096
     a = rng.standard_normal((M, K)).astype(np.float32)
     b = (rng.standard_normal((K, N)) / math.sqrt(K)).astype(np.float32)
     if fmt == B.BF16:
@@ -513,15 +515,16 @@ def test_mfma_gemm_256_tiles_vs_formal(hip, B, oracle, rt, fmt, out):
         assert int(np.count_nonzero(got_all.view(np.uint16) == 0x1234)) < 64
 
 
-@pytest.mark.parametrize("m,n,out", [(1024, 6144, 3), (1024, 6144, 5), (512, 12288, 3)])
-def test_mfma_gemm_192_tiles_vs_formal(hip, B, oracle, m, n, out):
+@pytest.mark.parametrize("m,n,out,K", [(1024, 6144, 3, 256), (1024, 6144, 5, 256), (512, 12288, 3, 256),
+                                       (1024, 6144, 3, 320), (1024, 6144, 5, 64)])
+def test_mfma_gemm_192_tiles_vs_formal(hip, B, oracle, m, n, out, K):
     """Shapes that take the 128x192 tiles (one round of 256 workgroups where
-    128x128 tiles need two: the decoder layer's QKV projection), k = 256.
+    128x128 tiles need two: the decoder layer's QKV projection); k = 320 and
+    64 give an odd number of 128-byte K stages and a single one.
     Sampled rows against the GPU formal lane (pinned to the CPU oracle on two
     rows), every output written; MFMA GEMM tolerances."""
-    say("mfma gemm 128x192 tiles", m, n, out)
-    rng = np.random.default_rng(m + n + out)
-    K = 256
+    say("mfma gemm 128x192 tiles", m, n, out, K)
+    rng = np.random.default_rng(m + n + out + K)
     a = oracle.f32_to_bf16(rng.standard_normal((m, K)).astype(np.float32)).reshape(m, K)
     bt = oracle.f32_to_bf16((rng.standard_normal((n, K)) / math.sqrt(K)).astype(np.float32)).reshape(n, K)
     ad, bd = u16(a), u16(bt)

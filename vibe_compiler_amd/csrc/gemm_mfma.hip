@@ -734,6 +734,171 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
 }
 
+// 4-wave tiles (one wave per SIMD, the accumulators in AGPRs) with the K
+// slices moved global -> LDS by buffer_load ... lds: no staging registers
+// and no LDS write instructions, which the register-staged kernel above
+// issues in bursts that fill the LDS data FIFO.  Stages of SB bytes of K per
+// row (SB / 32 MFMA k-steps) in a ring of 128 KiB (two stages of 256 + 256
+// rows at SB = 128, three of 128 + 192 rows).  One DMA instruction fills
+// 1024 / SB rows: lane l writes chunk position l % (SB / 16) of its row, so
+// it loads the global chunk that the swizzle maps there.  Chunk c of row r
+// sits at position c ^ swz(r), swz a function of r % 16 ((r >> 2) & 3 for
+// 64-byte rows, r & 7 for 128-byte rows): each fragment address is a
+// per-lane base per k-step plus an immediate per 32-row tile, and the rows
+// one fragment read touches hit distinct 16-byte bank groups.  One barrier
+// per stage, before its last k-step: it publishes stage kt+1 and frees
+// stage kt's slot.  Each stage's moves go out in two halves spread over the
+// MFMA slots of two k-steps (a burst of them fills the texture address
+// FIFO): the first half in the last k-step of the stage whose slot it
+// refills, the second in the next stage's first k-step.  K bytes a multiple
+// of SB; full tiles only.
+template <int KIND, int OUT, int BM, int BN, int SB = 64, int WM = 2, int WN = 2, bool SPLIT = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_nt_dma4_kernel(GemmArgs args) {
+  static_assert(WM * WN == 4, "four waves");
+  static_assert(SB == 64 || SB == 128, "64- or 128-byte stages");
+  constexpr int ROWB = SB, CH = SB / 16, KS = SB / 32;      // bytes per row, chunks per row, k-steps per stage
+  constexpr int STAGE_BYTES = (BM + BN) * ROWB;
+  constexpr int NS = (128 * 1024) / STAGE_BYTES;            // ring of 128 KiB
+  constexpr int RPI = 1024 / ROWB;                           // rows per 1 KiB DMA instruction
+  constexpr int WTM = BM / WM / 32, WTN = BN / WN / 32;
+  constexpr int INSTR = (BM + BN) / RPI, PER_WAVE = INSTR / 4;
+  static_assert(NS >= 2 && INSTR % 4 == 0, "two stages at least; DMA instructions split evenly over the waves");
+  constexpr int OC = OUT == OUT_SWIGLU ? BN / WN / 2 : BN / WN;
+  static_assert(4 * (BM / WM) * OC * 2 <= NS * STAGE_BYTES, "staging fits in the ring");
+  __shared__ __align__(1024) uint8_t lds[NS * STAGE_BYTES];
+  // split-K: workgroup ids [s tiles, (s + 1) tiles) take split s
+  const int tiles = args.tiles_m * args.tiles_n;
+  const int split = SPLIT ? (int)blockIdx.x / tiles : 0;
+  int tm, tn;
+  tile_coords(args, (int)blockIdx.x - split * tiles, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wv / WN, wn = wv % WN;
+  const int l32 = lane & 31, g = lane >> 5;
+
+  typename Acc<KIND>::T acc[WTM][WTN];
+#pragma unroll
+  for (int i = 0; i < WTM; ++i)
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  const int kb = args.kbytes;
+  const int kchunk = SPLIT ? kb / args.ksplit : kb;
+  const int k0 = split * kchunk, nkt = kchunk / SB;
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc((void *)(args.a + (size_t)m0 * kb + k0), 0, BM * kb - k0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb =
+      __builtin_amdgcn_make_buffer_rsrc((void *)(args.bt + (size_t)n0 * kb + k0), 0, BN * kb - k0, 0x00020000);
+  // the swizzle of row r: (r >> 2) & 3 for 64-byte rows, r & 7 for 128-byte
+  // rows (a function of r % 16 either way)
+  auto swz = [](int r) __attribute__((always_inline)) { return SB == 64 ? (r >> 2) & 3 : r & 7; };
+  // DMA lane offset: row lane / CH of the instruction's RPI, global chunk
+  // (lane % CH) ^ swz(row)
+  const int voff = (lane / CH) * kb + (((lane % CH) ^ swz(lane / CH)) << 4);
+  // instructions q0 .. q1-1 of this wave's PER_WAVE for stage kt into ring
+  // slot kt % NS (past the last stage a clamped copy into a free slot, never
+  // read)
+  auto issue = [&](int kt, int q0, int q1) __attribute__((always_inline)) {
+    const int koff = min(kt, nkt - 1) * SB;
+    uint8_t *slot = lds + (kt % NS) * STAGE_BYTES;
+#pragma unroll
+    for (int q = q0; q < q1; ++q) {
+      const int ins = wv * PER_WAVE + q;  // 0 .. INSTR - 1 (wave-uniform)
+      const bool is_a = ins < BM / RPI;
+      const int rel = is_a ? ins : ins - BM / RPI;
+      const int soff = __builtin_amdgcn_readfirstlane(rel * RPI * kb + koff);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(is_a ? ra : rb,
+                                               (__attribute__((address_space(3))) void *)(slot + ins * 1024), 16,
+                                               voff, soff, 0, 0);
+    }
+  };
+  // fragment offsets within a stage for k-step ks (chunk 2 ks + g):
+  // A row wm * (BM / WM) + 32 i + l32, Bt row BM + wn * (BN / WN) + 32 j + l32
+  // (32 i keeps the swizzle, so the tiles differ by immediates)
+  const int sw = swz(l32);
+  int fa_off[KS], fb_off[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    fa_off[ks] = (wm * (BM / WM) + l32) * ROWB + (((2 * ks + g) ^ sw) << 4);
+    fb_off[ks] = (BM + wn * (BN / WN) + l32) * ROWB + (((2 * ks + g) ^ sw) << 4);
+  }
+  u32x4 fa[2][WTM], fb[2][WTN];
+  constexpr int NM = WTM * WTN, NR = WTM + WTN;
+  // fragment read r of a k-step, in the order its MFMAs (row-major over i,
+  // j) consume them: A tile 0, the WTN Bt tiles, A tiles 1 ..
+  auto read_frag = [&](int kt, int ks, int f, int r) __attribute__((always_inline)) {
+    const uint8_t *base = lds + (kt % NS) * STAGE_BYTES;
+    if (r == 0)
+      fa[f][0] = *(const u32x4 *)(base + fa_off[ks]);
+    else if (r <= WTN)
+      fb[f][r - 1] = *(const u32x4 *)(base + fb_off[ks] + (r - 1) * 32 * ROWB);
+    else
+      fa[f][r - WTN] = *(const u32x4 *)(base + fa_off[ks] + (r - WTN) * 32 * ROWB);
+  };
+  auto read_frags = [&](int kt, int ks, int f) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) read_frag(kt, ks, f, r);
+  };
+  // One k-step in NR slots, each fenced: NM / NR MFMAs of fragment set f,
+  // one fragment read of the next k-step (set nf of stage nkt_, k-step nks)
+  // and, for `moves` > 0, DMA instructions q0 .. q0 + moves - 1 of stage
+  // `mkt` spread over the slots (a burst of DMA issues fills the texture
+  // address FIFO and stalls the wave).
+  auto kstep = [&](int f, int nkt_, int nks, int nf, int mkt, int q0, int moves) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+#pragma unroll
+      for (int t = (r * NM) / NR; t < ((r + 1) * NM) / NR; ++t)
+        acc[t / WTN][t % WTN] = mfma<KIND>(fa[f][t / WTN], fb[f][t % WTN], acc[t / WTN][t % WTN]);
+      read_frag(nkt_, nks, nf, r);
+      if (moves > 0) issue(mkt, q0 + (r * moves) / NR, q0 + ((r + 1) * moves) / NR);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // each stage's moves go out in two halves: the first in the last k-step
+  // of the stage whose slot it refills (after that stage's barrier), the
+  // second in the first k-step of the next stage
+  constexpr int H1 = PER_WAVE / 2, H2 = PER_WAVE - H1;
+
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) issue(s, 0, PER_WAVE);
+  issue(NS - 1, 0, H1);
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE + H1) : "memory");
+  read_frags(0, 0, 0);
+  for (int kt = 0; kt < nkt; ++kt) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int cur = ks & 1;
+      if (ks < KS - 1) {
+        // this k-step's MFMAs with the next one's fragment reads between
+        // them (and, in the first, the second half of stage kt+NS-1's moves)
+        kstep(cur, kt, ks + 1, cur ^ 1, kt + NS - 1, H1, ks == 0 ? H2 : 0);
+      } else {
+        // stage kt+1 has landed for this wave (later stages may still fly)
+        // and its reads of stage kt are done; after the barrier stage kt+1
+        // is visible to every wave and slot kt % NS is free for stage kt+NS
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE) : "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        // the last k-step's MFMAs with stage kt+1's first fragment reads and
+        // the first half of stage kt+NS's moves between them
+        kstep(cur, kt + 1, 0, cur ^ 1, kt + NS, 0, H1);
+      }
+    }
+  }
+  // the clamped tail loads are still in flight: drain before the LDS is reused
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if constexpr (SPLIT) {
+    GemmArgs pa = args;
+    pa.y = args.part + (size_t)split * args.m * args.n;
+    gemm_store<KIND, BM, BN, OUT_F32, false, WM, WN, false>(pa, acc, m0, n0, nullptr);
+  } else {
+    gemm_store<KIND, BM, BN, OUT, false, WM, WN, true>(args, acc, m0, n0, (char *)lds + wv * (BM / WM) * OC * 2);
+  }
+}
+
 // Split-K fold: y = epilogue(part[0] + part[1] + ... + part[S-1]) per
 // element, the partial tiles added in split order; OUT_NARROW narrows to
 // the input format, OUT_NARROW_RES adds the residual as the per-element
@@ -932,10 +1097,11 @@ int launch_gemm_tiles(hipStream_t st, GemmArgs args) {
     // register-staged (int8 keeps 8 waves: its 4-wave dequant epilogue
     // spills; a residual keeps the 8-wave kernel's staged epilogue)
     if constexpr (KIND != KIND_I8 && OUT != OUT_NARROW_RES) {
-      if (args.kbytes % 256 == 0) {
-        hipLaunchKernelGGL((gemm_nt_rs_kernel<KIND, OUT, 256, 256, 128, false>), dim3(args.tiles_m * args.tiles_n),
+      if (args.kbytes % 128 == 0) {
+        // LDS-DMA staging (4096^3: 107 against 111 us register-staged)
+        hipLaunchKernelGGL((gemm_nt_dma4_kernel<KIND, OUT, 256, 256, 128>), dim3(args.tiles_m * args.tiles_n),
                            dim3(256), 0, st, args);
-        return launch_status("gemm_nt_rs_kernel");
+        return launch_status("gemm_nt_dma4_kernel");
       }
     }
     hipLaunchKernelGGL((gemm_nt_kernel<KIND, 256, 256, OUT, false, SB>), dim3(args.tiles_m * args.tiles_n),
@@ -957,10 +1123,12 @@ int launch_gemm_tiles(hipStream_t st, GemmArgs args) {
         // 53.3 against 55.4 us); a residual keeps the 8-wave kernel's staged
         // epilogue
         if constexpr (KIND != KIND_I8 && OUT != OUT_NARROW_RES) {
-          if (args.kbytes % 256 == 0) {
-            hipLaunchKernelGGL((gemm_nt_rs_kernel<KIND, OUT, 128, 192, 128, false>), dim3(args.tiles_m * args.tiles_n),
+          if (args.kbytes % 128 == 0) {
+            // LDS-DMA staging, three stages (QKV at M = 1024 in the decoder
+            // layer: 52.5 against 59.4 us register-staged)
+            hipLaunchKernelGGL((gemm_nt_dma4_kernel<KIND, OUT, 128, 192, 128>), dim3(args.tiles_m * args.tiles_n),
                                dim3(256), 0, st, args);
-            return launch_status("gemm_nt_rs_kernel");
+            return launch_status("gemm_nt_dma4_kernel");
           }
         }
         hipLaunchKernelGGL((gemm_nt_kernel<KIND, 128, 192, OUT, false, SB, 4, 2>),
