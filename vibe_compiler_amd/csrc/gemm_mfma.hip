@@ -761,8 +761,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   constexpr int NS = (128 * 1024) / STAGE_BYTES;            // ring of 128 KiB
   constexpr int RPI = 1024 / ROWB;                           // rows per 1 KiB DMA instruction
   constexpr int WTM = BM / WM / 32, WTN = BN / WN / 32;
-  constexpr int INSTR = (BM + BN) / RPI, PER_WAVE = INSTR / 4;
-  static_assert(NS >= 2 && INSTR % 4 == 0, "two stages at least; DMA instructions split evenly over the waves");
+  // each wave issues a quarter of the A instructions, then a quarter of the
+  // Bt ones, so which operand an issue slot moves is known at compile time
+  constexpr int A_INSTR = BM / RPI, B_INSTR = BN / RPI;
+  constexpr int PA = A_INSTR / 4, PB = B_INSTR / 4, PER_WAVE = PA + PB;
+  static_assert(NS >= 2 && A_INSTR % 4 == 0 && B_INSTR % 4 == 0,
+                "two stages at least; DMA instructions split evenly over the waves");
   constexpr int OC = OUT == OUT_SWIGLU ? BN / WN / 2 : BN / WN;
   static_assert(4 * (BM / WM) * OC * 2 <= NS * STAGE_BYTES, "staging fits in the ring");
   __shared__ __align__(1024) uint8_t lds[NS * STAGE_BYTES];
@@ -806,9 +810,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     uint8_t *slot = lds + (kt % NS) * STAGE_BYTES;
 #pragma unroll
     for (int q = q0; q < q1; ++q) {
-      const int ins = wv * PER_WAVE + q;  // 0 .. INSTR - 1 (wave-uniform)
-      const bool is_a = ins < BM / RPI;
-      const int rel = is_a ? ins : ins - BM / RPI;
+      const bool is_a = q < PA;                                 // compile-time
+      const int rel = is_a ? wv * PA + q : wv * PB + (q - PA);  // instruction within the operand
+      const int ins = is_a ? rel : A_INSTR + rel;
       const int soff = __builtin_amdgcn_readfirstlane(rel * RPI * kb + koff);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(is_a ? ra : rb,
                                                (__attribute__((address_space(3))) void *)(slot + ins * 1024), 16,
