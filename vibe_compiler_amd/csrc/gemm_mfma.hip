@@ -22,11 +22,11 @@
 // or walk that XCD's own column strip in 4-row groups (other grids whose tile
 // rows divide by 4 and tile columns by 8), bounding the XCD's L2 working set.
 // Tiles are 256x256 when they fill the chip, 128x192 where that saves a round
-// of workgroups, else 128x128.  For 16-bit operands the 256x256 and 128x192
-// tiles run on a 4-wave kernel instead (one wave per SIMD, K slices staged
-// through VGPRs into padded LDS rows), and long-K grids of at most one round
-// of 128x128 tiles split K over 4 workgroups of 256x256 tiles with a fold
-// launch.
+// of workgroups, else 128x128.  For 16-bit operands the 256x256, 256x224
+// (SwiGLU) and 128x192 tiles run on a 4-wave kernel instead (one wave per
+// SIMD, K slices moved by LDS DMA into a ring of 128 KiB), and long-K grids
+// of at most one round of 128x128 tiles split K over 4 workgroups of
+// 256x256 tiles with a fold launch.
 //
 // int8 semantics (no reference implementation exists; the closed form on the
 // reference's conversion routes): acc = sum_k int32(a)*int32(b) exactly
@@ -1047,19 +1047,20 @@ int launch_gemm_sb(hipStream_t st, GemmArgs args) {
   if constexpr (OUT != OUT_SWIGLU) {
     return launch_gemm_tiles<KIND, OUT, SB>(st, args);
   } else {
-    // 256x224 tiles (4 x 1 waves of 64 x 224) where their rounds of 256
-    // workgroups take less time than those of 256x256 tiles (gate/up at
-    // n 28672: 512 tiles in two rounds of 7/8 the work, against 448 tiles
-    // whose second round is three quarters full)
+    // 256x224 tiles (4 x 1 waves of 64 x 224, LDS-DMA staging) where their
+    // rounds of 256 workgroups take less time than those of 256x256 tiles
+    // (gate/up at n 28672: 512 tiles in two rounds of 7/8 the work, against
+    // 448 tiles whose second round is three quarters full; 211 against
+    // 217 us register-staged in the decoder layer)
     if constexpr (SB == 128) {
       if (args.m % 256 == 0 && args.n % 224 == 0 && args.kbytes % 256 == 0) {
         const long t224 = (long)(args.m / 256) * (args.n / 224), t256 = (long)(args.m / 256) * ((args.n + 255) / 256);
         if (7 * ((t224 + 255) / 256) < 8 * ((t256 + 255) / 256)) {
           args.tiles_m = args.m / 256;
           args.tiles_n = args.n / 224;
-          hipLaunchKernelGGL((gemm_nt_rs_kernel<KIND, OUT, 256, 224, 128, false, 4, 1>),
+          hipLaunchKernelGGL((gemm_nt_dma4_kernel<KIND, OUT, 256, 224, 128, 4, 1>),
                              dim3(args.tiles_m * args.tiles_n), dim3(256), 0, st, args);
-          return launch_status("gemm_nt_rs_kernel");
+          return launch_status("gemm_nt_dma4_kernel");
         }
       }
     }
@@ -1078,14 +1079,16 @@ int launch_gemm_sb(hipStream_t st, GemmArgs args) {
 
 template <int KIND, int OUT, int SB>
 int launch_gemm_tiles(hipStream_t st, GemmArgs args) {
-  // split-K planned by the entry (plan_split, partial area in args.part)
+  // split-K planned by the entry (plan_split, partial area in args.part), on
+  // the LDS-DMA kernel (the decoder layer's down projection: 106 against
+  // 115 us register-staged)
   if constexpr (KIND != KIND_I8 && SB == 128) {
     if (args.ksplit > 1) {
       args.tiles_m = args.m / 256;
       args.tiles_n = args.n / 256;
-      hipLaunchKernelGGL((gemm_nt_rs_kernel<KIND, OUT_F32, 256, 256, 128, false, 2, 2, true>),
+      hipLaunchKernelGGL((gemm_nt_dma4_kernel<KIND, OUT_F32, 256, 256, 128, 2, 2, true>),
                          dim3(args.tiles_m * args.tiles_n * args.ksplit), dim3(256), 0, st, args);
-      WAFER_TRY(launch_status("gemm_nt_rs_kernel"));
+      WAFER_TRY(launch_status("gemm_nt_dma4_kernel"));
       const int64_t count = (int64_t)args.m * args.n;
       const unsigned grid = (unsigned)std::min<int64_t>((count / 8 + 255) / 256, 8192);
       hipLaunchKernelGGL((gemm_fold_kernel<KIND, OUT>), dim3(grid), dim3(256), 0, st, args.part, args.ksplit,
