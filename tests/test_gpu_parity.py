@@ -515,6 +515,55 @@ def test_mfma_gemm_256_tiles_vs_formal(hip, B, oracle, rt, fmt, out, K):
         assert int(np.count_nonzero(got_all.view(np.uint16) == 0x1234)) < 64
 
 
+def _narrowing_cases(oracle, rng, n):
+    """bf16 pairs (x, y) whose exact f32 sum x + y lands on the cases RNE
+    narrowing has to get right: ties to even (y = half an ulp of x, x with
+    even and odd mantissa), just below and above a tie, carries into the
+    exponent, the overflow edge (rounds to inf), infinities and NaNs."""
+    e = rng.integers(-100, 120, n)
+    mant = rng.integers(0, 128, n)
+    sign = rng.choice([-1.0, 1.0], n)
+    x = sign * (1.0 + mant / 128.0) * np.exp2(e.astype(np.float64))
+    half = np.exp2(e - 8.0)
+    kind = rng.integers(0, 5, n)
+    y = np.select([kind == 0, kind == 1, kind == 2, kind == 3], [half, 0.75 * half, 1.5 * half, -half], 0.375 * half)
+    y = y * sign
+    x[:64] = sign[:64] * (2.0 - 1 / 128.0) * 2.0 ** 127   # largest finite bf16 ...
+    y[:32] = sign[:32] * 2.0 ** 119                     # ... plus half an ulp: ties to inf
+    y[32:64] = sign[32:64] * 2.0 ** 118                 # ... plus a quarter: stays finite
+    # every x and y is a bf16 value, so these conversions are exact
+    xb = oracle.f32_to_bf16(x.astype(np.float32)).reshape(n)
+    yb = oracle.f32_to_bf16(y.astype(np.float32)).reshape(n)
+    xb[64:72] = [0x7f80, 0xff80, 0x7fc0, 0x7fa1, 0xffd3, 0x7f81, 0x0000, 0x8000]  # inf, NaN payloads, zeros
+    return xb, yb
+
+
+@pytest.mark.parametrize("m,n", [(4096, 4096), (1024, 6144)])
+def test_mfma_gemm_bf16_narrowing_bit_exact(hip, B, oracle, m, n):
+    """The staged epilogues narrow f32 to bf16 with v_cvt_pk_bf16_f32 and set
+    NaNs to the codec's 0x7fc0.  Here every output is an exact f32 sum
+    x + y (A rows [1, 1, 0 ...], Bt rows [x, y, 0 ...], k = 64) chosen on
+    RNE's edge cases, so the narrowed output must equal the oracle's
+    f32_to_bf16 of x + y bit for bit (256x256 tiles at 4096 x 4096, 128x192
+    at 1024 x 6144)."""
+    say("mfma gemm bf16 narrowing", m, n)
+    rng = np.random.default_rng(m + n)
+    K = 64
+    xb, yb = _narrowing_cases(oracle, rng, n)
+    a = np.zeros((m, K), dtype=np.uint16)
+    a[:, 0] = a[:, 1] = 0x3F80
+    bt = np.zeros((n, K), dtype=np.uint16)
+    bt[:, 0], bt[:, 1] = xb, yb
+    dst = torch.full((m, n), 0x1234, dtype=torch.int16, device="cuda")
+    hip.gemm_mfma(u16(a), u16(bt), dst, m, K, n, in_fmt=B.BF16, out_fmt=B.BF16, rhs_t=True)
+    got = host(dst).view(np.uint16)
+    exact = (oracle.to_float(B.BF16, xb).astype(np.float64) + oracle.to_float(B.BF16, yb).astype(np.float64))
+    assert np.all(np.isnan(exact) | np.isinf(exact) | (exact.astype(np.float32).astype(np.float64) == exact))
+    want = oracle.f32_to_bf16(exact.astype(np.float32)).reshape(n)
+    assert np.array_equal(got[0], want), np.nonzero(got[0] != want)[0][:8]
+    assert np.array_equal(got, np.broadcast_to(want, got.shape))
+
+
 @pytest.mark.parametrize("m,n,out,K", [(1024, 6144, 3, 256), (1024, 6144, 5, 256), (512, 12288, 3, 256),
                                        (1024, 6144, 3, 320), (1024, 6144, 5, 64)])
 def test_mfma_gemm_192_tiles_vs_formal(hip, B, oracle, m, n, out, K):

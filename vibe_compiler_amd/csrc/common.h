@@ -114,6 +114,19 @@ __host__ __device__ inline uint16_t f32_to_bf16(float v) {
   return (uint16_t)(u >> 16);
 }
 __host__ __device__ inline float bf16_to_f32(uint16_t b) { return u2f((uint32_t)b << 16); }
+// Two f32 -> packed bf16 (lo in bits 0..15) by v_cvt_pk_bf16_f32: RNE with
+// gradual underflow and overflow to inf, the bits of f32_to_bf16 for every
+// non-NaN input (checked over halfway cases, denormals and the overflow
+// edge); the instruction keeps a NaN's sign and payload, so NaNs are set to
+// the codec's canonical 0x7fc0 afterwards.
+__device__ inline uint32_t bf16x2_rne(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  uint32_t r = __builtin_bit_cast(uint32_t, v);
+  r = lo != lo ? (r & 0xffff0000u) | 0x7fc0u : r;
+  r = hi != hi ? (r & 0x0000ffffu) | 0x7fc00000u : r;
+  return r;
+}
 
 __host__ __device__ inline float f16_to_f32(uint16_t bits) {
   uint32_t sign = (uint32_t)(bits & 0x8000u) << 16;

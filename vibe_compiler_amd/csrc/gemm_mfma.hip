@@ -110,9 +110,10 @@ __device__ inline uint16_t swiglu_pair(float a, float b) {
     const float uv = widen_f16(narrow_f16(__uint_as_float(t[1])));
     return narrow_f16(silu_mul_1(gv, uv));
   } else {
-    const float gv = bf16_to_f32(f32_to_bf16(__uint_as_float(t[0])));
-    const float uv = bf16_to_f32(f32_to_bf16(__uint_as_float(t[1])));
-    return f32_to_bf16(silu_mul_1(gv, uv));
+    const uint32_t gu = bf16x2_rne(__uint_as_float(t[0]), __uint_as_float(t[1]));
+    const float gv = __uint_as_float(gu << 16), uv = __uint_as_float(gu & 0xffff0000u);
+    const float y = silu_mul_1(gv, uv);
+    return (uint16_t)bf16x2_rne(y, y);
   }
 }
 
@@ -236,13 +237,20 @@ __device__ __attribute__((always_inline)) inline void gemm_store(
 #pragma unroll
           for (int i = 0; i < WTM; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              uint16_t v;
-              if (OUT == OUT_NARROW || OUT == OUT_NARROW_RES)
-                v = KIND == KIND_F16 ? narrow_f16((float)acc[i][j][r]) : f32_to_bf16((float)acc[i][j][r]);
-              else
-                v = f32_to_bf16((float)(int32_t)acc[i][j][r] * sc);
-              put(i * 32 + 8 * (r >> 2) + 4 * g + (r & 3), j * 32 + l32, v);
+            for (int r = 0; r < 16; r += 2) {
+              // rows r and r + 1 of the lane's column, narrowed as a pair
+              uint32_t v2;
+              if constexpr (OUT == OUT_NARROW || OUT == OUT_NARROW_RES) {
+                if constexpr (KIND == KIND_F16)
+                  v2 = (uint32_t)narrow_f16((float)acc[i][j][r]) | ((uint32_t)narrow_f16((float)acc[i][j][r + 1]) << 16);
+                else
+                  v2 = bf16x2_rne((float)acc[i][j][r], (float)acc[i][j][r + 1]);
+              } else {
+                v2 = bf16x2_rne((float)(int32_t)acc[i][j][r] * sc, (float)(int32_t)acc[i][j][r + 1] * sc);
+              }
+              const int row = i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+              put(row, j * 32 + l32, (uint16_t)v2);
+              put(row + 1, j * 32 + l32, (uint16_t)(v2 >> 16));
             }
           // 128-row sub-tiles: bound the accumulators read out at once
           if constexpr (WTM * WTN > 8) __builtin_amdgcn_sched_barrier(0);
@@ -265,7 +273,7 @@ __device__ __attribute__((always_inline)) inline void gemm_store(
             const float hi = KIND == KIND_F16 ? widen_f16((uint16_t)(a >> 16)) + widen_f16((uint16_t)(b >> 16))
                                               : bf16_to_f32((uint16_t)(a >> 16)) + bf16_to_f32((uint16_t)(b >> 16));
             v[e] = KIND == KIND_F16 ? ((uint32_t)narrow_f16(lo) | ((uint32_t)narrow_f16(hi) << 16))
-                                    : ((uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16));
+                                    : bf16x2_rne(lo, hi);
           }
         }
         *(u32x4 *)(ybase + (size_t)row * ldy + c * 8) = v;
@@ -929,20 +937,22 @@ __global__ __launch_bounds__(256) void gemm_fold_kernel(const float *__restrict_
       u32x4 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        uint32_t h[2];
+        if constexpr (KIND == KIND_F16) {
+          uint32_t h[2];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const float a = v[2 * e + t];
-          uint16_t n = KIND == KIND_F16 ? narrow_f16(a) : f32_to_bf16(a);
-          if constexpr (OUT == OUT_NARROW_RES) {
-            const uint16_t r = (uint16_t)(rv[e] >> (16 * t));
-            const float nv = KIND == KIND_F16 ? widen_f16(n) : bf16_to_f32(n);
-            const float rf = KIND == KIND_F16 ? widen_f16(r) : bf16_to_f32(r);
-            n = KIND == KIND_F16 ? narrow_f16(nv + rf) : f32_to_bf16(nv + rf);
+          for (int t = 0; t < 2; ++t) {
+            uint16_t n = narrow_f16(v[2 * e + t]);
+            if constexpr (OUT == OUT_NARROW_RES) n = narrow_f16(widen_f16(n) + widen_f16((uint16_t)(rv[e] >> (16 * t))));
+            h[t] = n;
           }
-          h[t] = n;
+          o[e] = h[0] | (h[1] << 16);
+        } else {
+          uint32_t n = bf16x2_rne(v[2 * e], v[2 * e + 1]);
+          if constexpr (OUT == OUT_NARROW_RES)
+            n = bf16x2_rne(__uint_as_float(n << 16) + __uint_as_float(rv[e] << 16),
+                           __uint_as_float(n & 0xffff0000u) + __uint_as_float(rv[e] & 0xffff0000u));
+          o[e] = n;
         }
-        o[e] = h[0] | (h[1] << 16);
       }
       *(u32x4 *)((uint16_t *)y + 8 * q) = o;
     }
