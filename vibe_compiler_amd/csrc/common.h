@@ -185,6 +185,16 @@ __device__ inline float f32_rounded(float x) {
   asm("" : "+v"(x));
   return x;
 }
+// f32 -> f16 by v_cvt_f16_f32: RNE with gradual underflow and overflow to
+// inf, the bits of f32_to_f16 for every non-NaN input (checked on the GPU
+// over tie remainders at every exponent of f16's range, the overflow edge
+// and half the smallest subnormal); a NaN is set to the codec's 0x7e00 (the
+// instruction keeps sign and payload).  The pin keeps the compiler from
+// fusing a preceding multiply into v_fma_mix (one rounding instead of two).
+__device__ inline uint32_t f16_rne(float x) {
+  x = f32_rounded(x);
+  return x != x ? 0x7e00u : (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+}
 
 // ExpLp (ManagedReferenceTargetModel.cpp:265-270): exp2f(x * log2(e))
 __device__ inline float explp_acc(float x) { return exp2f(x * 0x1.715476p+0f); }
@@ -227,10 +237,10 @@ template <> __device__ inline void store_from_f32<WAFER_FMT_F32>(void *b, int64_
   ((float *)b)[i] = v;
 }
 template <> __device__ inline void store_from_f32<WAFER_FMT_BF16>(void *b, int64_t i, float v) {
-  ((uint16_t *)b)[i] = f32_to_bf16(v);
+  ((uint16_t *)b)[i] = (uint16_t)bf16x2_rne(v, v);
 }
 template <> __device__ inline void store_from_f32<WAFER_FMT_F16>(void *b, int64_t i, float v) {
-  ((uint16_t *)b)[i] = f32_to_f16(v);
+  ((uint16_t *)b)[i] = (uint16_t)f16_rne(v);
 }
 
 // ExpLp: one RNE multiply by log2(e) = 0x1.715476p+0, then exp2
@@ -257,8 +267,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // v rounded to the storage format F and widened back (what a store then a
 // load of v gives)
 template <uint32_t F> __device__ inline float round_to(float v) {
-  if constexpr (F == WAFER_FMT_BF16) return bf16_to_f32(f32_to_bf16(v));
-  else if constexpr (F == WAFER_FMT_F16) return f16_to_f32(f32_to_f16(v));
+  if constexpr (F == WAFER_FMT_BF16) return u2f(bf16x2_rne(v, v) << 16);
+  else if constexpr (F == WAFER_FMT_F16) return f16_to_f32((uint16_t)f16_rne(v));
   else return v;
 }
 template <uint32_t F> __device__ inline void load8(const void *b, int64_t i, float (&v)[8]) {
@@ -292,11 +302,8 @@ template <uint32_t F> __device__ inline void store8(void *b, int64_t i, const fl
   } else {
     u32x4 w;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t l = F == WAFER_FMT_BF16 ? f32_to_bf16(v[2 * e]) : f32_to_f16(v[2 * e]);
-      const uint32_t h = F == WAFER_FMT_BF16 ? f32_to_bf16(v[2 * e + 1]) : f32_to_f16(v[2 * e + 1]);
-      w[e] = l | (h << 16);
-    }
+    for (int e = 0; e < 4; ++e)
+      w[e] = F == WAFER_FMT_BF16 ? bf16x2_rne(v[2 * e], v[2 * e + 1]) : f16_rne(v[2 * e]) | (f16_rne(v[2 * e + 1]) << 16);
     ((u32x4 *)b)[i / 8] = w;
   }
 }
