@@ -1027,15 +1027,16 @@ def test_softmax_shapes(hip, B, oracle, rows, cols, fmt):
                    oracle.to_float(fmt, oracle.softmax(xb, fmt=fmt)).reshape(x.shape), what="softmax")
 
 
-@pytest.mark.parametrize("rows,cols", [(1, 8), (67, 520), (1024, 4096), (3, 4104), (9, 33), (4096, 8), (4097, 520),
-                                       (4099, 1024), (4098, 2056), (4096, 4096)])
+@pytest.mark.parametrize("rows,cols", [(1, 8), (67, 520), (1024, 4096), (3, 4104), (5, 6152), (2, 8192), (2, 8200),
+                                       (9, 33), (4096, 8), (4097, 520), (4099, 1024), (4098, 2056), (4096, 4096)])
 @pytest.mark.parametrize("fmt", [3, 5, 2])
 def test_rmsnorm_shapes(hip, B, oracle, rows, cols, fmt):
-    """The workgroup RMSNorm below 4096 rows and beyond 4096 columns, the
-    scalar kernel (33 columns), and from 4096 rows the wave-per-row kernel at
-    1, 2, 4 and 8 chunks per lane (partial last chunks, row counts that leave
-    a workgroup's last waves idle); all three float formats against the
-    oracle."""
+    """Below 4096 rows the register-resident row kernel at 1, 2 and 4 chunks
+    per thread (up to 8192 columns, partial last chunks) and the two-pass
+    workgroup kernel beyond 8192 columns, the scalar kernel (33 columns), and
+    from 4096 rows the wave-per-row kernel at 1, 2, 4 and 8 chunks per lane
+    (row counts that leave a workgroup's last waves idle); all three float
+    formats against the oracle."""
     say("rmsnorm", rows, cols, fmt)
     rng = np.random.default_rng(rows * cols + fmt)
     x = (rng.standard_normal((rows, cols)) * 2).astype(np.float32)
@@ -1055,14 +1056,15 @@ def test_rmsnorm_shapes(hip, B, oracle, rows, cols, fmt):
                    oracle.to_float(fmt, oracle.rmsnorm(xb, wb, 1e-5, fmt=fmt)).reshape(x.shape), what="rmsnorm")
 
 
-@pytest.mark.parametrize("rows,cols", [(1024, 4096), (67, 520), (5, 2056), (3, 4104), (9, 33), (4097, 520),
-                                       (4096, 4096)])
+@pytest.mark.parametrize("rows,cols", [(1024, 4096), (67, 520), (5, 2056), (3, 4104), (5, 6152), (2, 8200), (9, 33),
+                                       (4097, 520), (4096, 4096)])
 @pytest.mark.parametrize("fmt", [3, 5, 2])
 def test_add_rmsnorm_equals_add_then_rmsnorm(hip, B, rows, cols, fmt):
     """The fused residual Add + RMSNorm gives the bits of the Add command
-    followed by the RMSNorm region, for both outputs: the workgroup kernel
-    (below 4096 rows or above 4096 columns), the wave-per-row kernel (from
-    4096 rows), and the two-launch path for columns not a multiple of 8."""
+    followed by the RMSNorm region, for both outputs: the row kernels (below
+    4096 rows or above 4096 columns: register-resident up to 8192 columns,
+    two-pass beyond), the wave-per-row kernel (from 4096 rows), and the
+    two-launch path for columns not a multiple of 8."""
     say("add_rmsnorm", rows, cols, fmt)
     dt = {3: torch.bfloat16, 5: torch.float32, 2: torch.float16}[fmt]
     iv = torch.int32 if fmt == 5 else torch.int16

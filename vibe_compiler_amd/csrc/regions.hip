@@ -99,6 +99,62 @@ __global__ __launch_bounds__(RT) void rmsnorm_kernel(const void *__restrict__ x,
   }
 }
 
+// The row workgroup kernel above with the row held in registers between the
+// sum and the scaling (rows of at most 8 * RT * NCH columns, cols % 8 == 0,
+// 16-byte aligned): x (for ADD, x and r) is read once and w is loaded before
+// the reduction; the sums and products are the same, in the same order.
+template <uint32_t F, int NCH, bool ADD>
+__global__ __launch_bounds__(RT) void rmsnorm_row_kernel(const void *__restrict__ x, const void *__restrict__ r,
+                                                         const void *__restrict__ w, void *__restrict__ sum,
+                                                         void *__restrict__ y, int64_t cols, float inv_n,
+                                                         float eps) {
+  __shared__ float red[RT / 64];
+  const int64_t base = (int64_t)blockIdx.x * cols;
+  float v[NCH][8], wv[NCH][8];
+#pragma unroll
+  for (int q = 0; q < NCH; ++q) {
+    const int64_t c = 8 * ((int64_t)threadIdx.x + RT * q);
+    if (c < cols) {
+      load8<F>(x, base + c, v[q]);
+      load8<F>(w, c, wv[q]);
+    }
+  }
+  if constexpr (ADD) {
+#pragma unroll
+    for (int q = 0; q < NCH; ++q) {
+      const int64_t c = 8 * ((int64_t)threadIdx.x + RT * q);
+      if (c < cols) {
+        float rv[8];
+        load8<F>(r, base + c, rv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[q][e] += rv[e];
+        store8<F>(sum, base + c, v[q]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[q][e] = round_to<F>(v[q][e]);
+      }
+    }
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int q = 0; q < NCH; ++q)
+    if (8 * ((int64_t)threadIdx.x + RT * q) < cols) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += v[q][e] * v[q][e];
+    }
+  s = block_sum(s, red);
+  const float rs = 1.0f / sqrtf(s * inv_n + eps);
+#pragma unroll
+  for (int q = 0; q < NCH; ++q) {
+    const int64_t c = 8 * ((int64_t)threadIdx.x + RT * q);
+    if (c < cols) {
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = v[q][e] * rs * wv[q][e];
+      store8<F>(y, base + c, o);
+    }
+  }
+}
+
 // Row counts from which the wave-per-row kernel below is used: it keeps one
 // wave per row in flight (4 per CU at 1024 rows, where the workgroup kernel's
 // 16 hide the latency chain better: 9.1 against 6.2 us at 1024 x 4096), and
@@ -574,6 +630,36 @@ int prologue(wafer_hip_context *ctx, uint32_t format, const char *what) {
 }  // namespace
 }  // namespace wafer
 
+namespace wafer {
+namespace {
+// the register-resident row kernel for rows of at most 8 * RT * 4 columns
+template <bool ADD>
+bool launch_rmsnorm_row(hipStream_t st, uint32_t format, uint64_t rows, uint64_t cols, const void *x, const void *r,
+                        const void *w, void *sum, void *y, float inv_n, float eps) {
+  if (cols > 8 * RT * 4) return false;
+  const int nch = cols <= 8 * RT ? 1 : cols <= 16 * RT ? 2 : 4;
+  const dim3 grid((unsigned)rows);
+  const int64_t c = (int64_t)cols;
+#define RMS_ROW(FMT, N) hipLaunchKernelGGL((rmsnorm_row_kernel<FMT, N, ADD>), grid, dim3(RT), 0, st, x, r, w, sum, y, c, inv_n, eps)
+#define RMS_ROW_N(FMT)      \
+  do {                       \
+    if (nch == 1)            \
+      RMS_ROW(FMT, 1);       \
+    else if (nch == 2)       \
+      RMS_ROW(FMT, 2);       \
+    else                     \
+      RMS_ROW(FMT, 4);       \
+  } while (0)
+  if (format == WAFER_FMT_F32) RMS_ROW_N(WAFER_FMT_F32);
+  else if (format == WAFER_FMT_BF16) RMS_ROW_N(WAFER_FMT_BF16);
+  else RMS_ROW_N(WAFER_FMT_F16);
+#undef RMS_ROW_N
+#undef RMS_ROW
+  return true;
+}
+}  // namespace
+}  // namespace wafer
+
 using namespace wafer;
 
 extern "C" int wafer_hip_rmsnorm(wafer_hip_context *ctx, uint32_t format, const void *x,
@@ -591,6 +677,8 @@ extern "C" int wafer_hip_rmsnorm(wafer_hip_context *ctx, uint32_t format, const 
     launch_rmsnorm_wave_f<false>(ctx->stream, format, nch, grid, x, nullptr, w, nullptr, y, r, c, inv_n, eps);
     return launch_status("rmsnorm_wave_kernel");
   }
+  if (vec && launch_rmsnorm_row<false>(ctx->stream, format, rows, cols, x, nullptr, w, nullptr, y, inv_n, eps))
+    return launch_status("rmsnorm_row_kernel");
   DISPATCH_FB(format, vec, rmsnorm_kernel, dim3((unsigned)rows), dim3(RT), x, w, y, (int64_t)cols, inv_n, eps);
   return launch_status("rmsnorm_kernel");
 }
@@ -615,6 +703,8 @@ extern "C" int wafer_hip_add_rmsnorm(wafer_hip_context *ctx, uint32_t format, co
                                 inv_n, eps);
     return launch_status("rmsnorm_wave_kernel");
   }
+  if (launch_rmsnorm_row<true>(ctx->stream, format, rows, cols, x, r, w, sum, y, inv_n, eps))
+    return launch_status("rmsnorm_row_kernel");
   const dim3 grid((unsigned)rows);
   if (format == WAFER_FMT_F32)
     hipLaunchKernelGGL((rmsnorm_kernel<WAFER_FMT_F32, true, true>), grid, dim3(RT), 0, ctx->stream, x, w, y,
