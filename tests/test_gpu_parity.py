@@ -515,6 +515,48 @@ def test_mfma_gemm_256_tiles_vs_formal(hip, B, oracle, rt, fmt, out, K):
         assert int(np.count_nonzero(got_all.view(np.uint16) == 0x1234)) < 64
 
 
+@pytest.mark.parametrize("m,n,fmt,out,K", [(1024, 4096, 3, 3, 512), (1024, 4096, 3, 5, 320), (384, 640, 2, 2, 64),
+                                           (128, 128, 3, 3, 192), (256, 1024, 2, 5, 1024)])
+def test_mfma_gemm_128_tiles_vs_formal(hip, B, oracle, m, n, fmt, out, K):
+    """Full 128x128 tiles where neither 256x256 nor 128x192 tiles are taken
+    (the decoder layer's O projection, 1024 x 4096): the four-wave LDS-DMA
+    kernel; k = 320, 192 and 64 give odd numbers of 128-byte K stages and a
+    single one.  Sampled rows against the GPU formal lane (pinned to the CPU
+    oracle on two rows), every output written; MFMA GEMM tolerances."""
+    say("mfma gemm 128x128 tiles", m, n, fmt, out, K)
+    rng = np.random.default_rng(m + n + fmt + out + K)
+    a = rng.standard_normal((m, K)).astype(np.float32)
+    b = (rng.standard_normal((n, K)) / math.sqrt(K)).astype(np.float32)
+    if fmt == B.BF16:
+        a, bt = oracle.f32_to_bf16(a).reshape(m, K), oracle.f32_to_bf16(b).reshape(n, K)
+    else:
+        a, bt = a.astype(np.float16).view(np.uint16), b.astype(np.float16).view(np.uint16)
+    ad, bd = u16(a), u16(bt)
+    if out == B.F32:
+        dst = torch.full((m, n), 7.5, dtype=torch.float32, device="cuda")
+    else:
+        dst = torch.full((m, n), 0x1234, dtype=torch.int16, device="cuda")
+    hip.gemm_mfma(ad, bd, dst, m, K, n, in_fmt=fmt, out_fmt=out, rhs_t=True)
+    got_all = host(dst)
+    rows = np.concatenate([[0, 1, 127, m - 1], rng.choice(m, 28, replace=False)])
+    sub = np.ascontiguousarray(a[rows])
+    ref_d = torch.zeros((len(rows), n), dtype=torch.float32, device="cuda")
+    hip.gemm(u16(sub), bd, ref_d, len(rows), K, n, in_fmt=fmt, out_fmt=B.F32, rhs_t=True)
+    ref = host(ref_d)
+    cpu = oracle.gemm_formal(fmt, oracle.F32, np.ascontiguousarray(sub[:2]), bt, 2, K, n, rhs_t=True)
+    assert np.array_equal(cpu.reshape(2, n).view(np.uint32), ref[:2].view(np.uint32))
+    if out == B.F32:
+        got = got_all[rows]
+        tol_rel, tol_max = 1e-5, 1e-4
+        assert not np.any(got_all == 7.5)
+    else:
+        got = oracle.to_float(fmt, got_all[rows].view(np.uint16)).reshape(len(rows), n)
+        tol_rel, tol_max = 2e-3, 2e-2
+        assert int(np.count_nonzero(got_all.view(np.uint16) == 0x1234)) < 64
+    rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert rel <= tol_rel and np.abs(got - ref).max() <= tol_max * np.abs(ref).max(), (rel,)
+
+
 def _narrowing_cases(oracle, rng, n):
     """bf16 pairs (x, y) whose exact f32 sum x + y lands on the cases RNE
     narrowing has to get right: ties to even (y = half an ulp of x, x with
@@ -538,14 +580,14 @@ def _narrowing_cases(oracle, rng, n):
     return xb, yb
 
 
-@pytest.mark.parametrize("m,n", [(4096, 4096), (1024, 6144)])
+@pytest.mark.parametrize("m,n", [(4096, 4096), (1024, 6144), (1024, 4096)])
 def test_mfma_gemm_bf16_narrowing_bit_exact(hip, B, oracle, m, n):
     """The staged epilogues narrow f32 to bf16 with v_cvt_pk_bf16_f32 and set
     NaNs to the codec's 0x7fc0.  Here every output is an exact f32 sum
     x + y (A rows [1, 1, 0 ...], Bt rows [x, y, 0 ...], k = 64) chosen on
     RNE's edge cases, so the narrowed output must equal the oracle's
     f32_to_bf16 of x + y bit for bit (256x256 tiles at 4096 x 4096, 128x192
-    at 1024 x 6144)."""
+    at 1024 x 6144, 128x128 at 1024 x 4096)."""
     say("mfma gemm bf16 narrowing", m, n)
     rng = np.random.default_rng(m + n)
     K = 64

@@ -1157,7 +1157,17 @@ int launch_gemm_tiles(hipStream_t st, GemmArgs args) {
   args.tiles_m = (args.m + 127) / 128;
   args.tiles_n = (args.n + 127) / 128;
   const dim3 grid(args.tiles_m * args.tiles_n);
-  // 4 x 2 waves (each 32 x 64) measured 2-3 % faster than 2 x 4 on 128x128 tiles
+  // full 16-bit tiles with plain outputs: the 4-wave LDS-DMA kernel, each
+  // wave 64x64 (the decoder layer's O projection, 1024 x 4096 x 4096: 36.0
+  // against 41.4 us on the 8-wave register-staged kernel)
+  if constexpr (KIND != KIND_I8 && OUT != OUT_NARROW_RES && SB == 128) {
+    if (args.m % 128 == 0 && args.n % 128 == 0) {
+      hipLaunchKernelGGL((gemm_nt_dma4_kernel<KIND, OUT, 128, 128, 128>), grid, dim3(256), 0, st, args);
+      return launch_status("gemm_nt_dma4_kernel");
+    }
+  }
+  // ragged, int8, residual or 64-byte-stage GEMMs: 4 x 2 waves (each 32 x 64)
+  // measured 2-3 % faster than 2 x 4 on 128x128 tiles
   if (args.m % 128 == 0 && args.n % 128 == 0)
     hipLaunchKernelGGL((gemm_nt_kernel<KIND, 128, 128, OUT, false, SB, 4, 2>), grid, dim3(512), 0, st, args);
   else
