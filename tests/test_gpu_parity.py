@@ -1047,6 +1047,27 @@ def test_regions_vs_oracle(hip, B, oracle):
     assert np.array_equal(host(yb), oracle.bias_add(x, bias))
 
 
+def test_bias_add_past_one_grid_stride(hip, B, oracle):
+    """bias_add over more 8-element chunks than its grid has threads (65536
+    workgroups of 256: 134,217,728 elements), so threads take a second chunk
+    whose column comes from the stride's remainder; 4104 columns make that
+    remainder wrap rows.  Bit-exact against torch's float32 add, which is the
+    oracle's one IEEE binary32 Add per element (pinned against the oracle on
+    the first and last rows)."""
+    rows, cols = 32800, 4104
+    say("bias_add past one grid stride", rows, cols)
+    gen = torch.Generator(device="cuda").manual_seed(4104)
+    x = torch.randn(rows, cols, generator=gen, device="cuda")
+    bias = torch.randn(cols, generator=gen, device="cuda")
+    y = torch.full_like(x, 7.5)
+    hip.bias_add(x, bias, y, fmt=B.F32)
+    torch.cuda.synchronize()
+    assert torch.equal(y, x + bias)
+    for r in (0, rows - 1):
+        assert np.array_equal(host(y[r:r + 1]), oracle.bias_add(host(x[r:r + 1]), host(bias)))
+    del x, y
+
+
 @pytest.mark.parametrize("rows,cols,fmt", [(7, 8, 3), (33, 2048, 3), (5, 2056, 3), (9, 6000, 2), (3, 8192, 5),
                                            (4, 9000, 3), (2, 24, 5)])
 def test_softmax_shapes(hip, B, oracle, rows, cols, fmt):

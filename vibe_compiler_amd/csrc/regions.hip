@@ -545,14 +545,20 @@ __global__ __launch_bounds__(256) void bias_add_kernel(const void *__restrict__ 
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if constexpr (VEC) {
+    // the column of this thread's chunk advances by the stride's remainder
+    // (one 64-bit division per thread, not one per chunk)
+    const int64_t step = (8 * stride) % cols;
+    int64_t c0 = (8 * gid) % cols;
     for (int64_t q = gid; q < count / 8; q += stride) {
-      const int64_t e0 = 8 * q, c0 = e0 % cols;
+      const int64_t e0 = 8 * q;
       float v[8], b[8], r[8];
       load8<F>(x, e0, v);
       load8<WAFER_FMT_F32>(bias, c0, b);
 #pragma unroll
       for (int e = 0; e < 8; ++e) r[e] = v[e] + b[e];
       store8<F>(y, e0, r);
+      c0 += step;
+      if (c0 >= cols) c0 -= cols;
     }
   } else {
     for (int64_t e = gid; e < count; e += stride) store_from_f32<F>(y, e, load_as_f32<F>(x, e) + bias[e % cols]);
