@@ -804,12 +804,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       __builtin_amdgcn_make_buffer_rsrc((void *)(args.a + (size_t)m0 * kb + k0), 0, BM * kb - k0, 0x00020000);
   const __amdgpu_buffer_rsrc_t rb =
       __builtin_amdgcn_make_buffer_rsrc((void *)(args.bt + (size_t)n0 * kb + k0), 0, BN * kb - k0, 0x00020000);
-  // the swizzle of row r: (r >> 2) & 3 for 64-byte rows, r & 7 for 128-byte
-  // rows (a function of r % 16 either way)
-  auto swz = [](int r) __attribute__((always_inline)) { return SB == 64 ? (r >> 2) & 3 : r & 7; };
-  // DMA lane offset: row lane / CH of the instruction's RPI, global chunk
-  // (lane % CH) ^ swz(row)
-  const int voff = (lane / CH) * kb + (((lane % CH) ^ swz(lane / CH)) << 4);
+  // the swizzle of row r: (r >> 2) & 3 for 64-byte rows, (r >> 1) & 7 for
+  // 128-byte rows, a function of r % 16 either way.  The LDS serves a
+  // fragment read 16 lanes (16 rows r0 .. r0 + 15, r0 % 16 == 0) at a time
+  // over 64 banks, so a 16-byte chunk's bank group is (r * ROWB / 16 + chunk)
+  // % 16; with these swizzles the 16 rows hit 16 distinct groups.  (r & 7
+  // for 128-byte rows puts rows r and r + 8 on one group: every read took
+  // two passes, half the LDS cycles counted as bank conflicts.)
+  auto swz = [](int r) __attribute__((always_inline)) { return SB == 64 ? (r >> 2) & 3 : (r >> 1) & 7; };
+  // DMA lane offset: row lane / CH of the instruction's RPI rows, global
+  // chunk (lane % CH) ^ swz(row); at 128-byte rows an instruction covers 8
+  // rows, so odd instructions (rows 8 .. 15 of a 16-row group) take voff1
+  const int voff0 = (lane / CH) * kb + (((lane % CH) ^ swz(lane / CH)) << 4);
+  const int voff1 = (lane / CH) * kb + (((lane % CH) ^ swz((RPI % 16) + lane / CH)) << 4);
   // instructions q0 .. q1-1 of this wave's PER_WAVE for stage kt into ring
   // slot kt % NS (past the last stage a clamped copy into a free slot, never
   // read)
@@ -822,6 +829,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       const int rel = is_a ? wv * PA + q : wv * PB + (q - PA);  // instruction within the operand
       const int ins = is_a ? rel : A_INSTR + rel;
       const int soff = __builtin_amdgcn_readfirstlane(rel * RPI * kb + koff);
+      // (ins & 1 is known at compile time where the wave's share of the
+      // operand's instructions is even)
+      const int voff = RPI < 16 && (ins & 1) ? voff1 : voff0;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(is_a ? ra : rb,
                                                (__attribute__((address_space(3))) void *)(slot + ins * 1024), 16,
                                                voff, soff, 0, 0);
