@@ -45,10 +45,11 @@
 //    addresses of lanes 4e + i/4, e = 0..3);
 //  * K and V blocks move global -> LDS by buffer_load ... lds (no staging
 //    registers): two stages, the next blocks' DMA overlapping the current
-//    blocks' compute.  Rows are 256 bytes with 16-byte chunks XOR-swizzled
-//    by 2 (row & 7), which keeps the ds_read_b128 K reads and the
-//    transposed V reads free of bank conflicts (measured: 128 banks per
-//    half-wave for b128 reads, 64 for b64 reads);
+//    blocks' compute.  Rows are 256 bytes (one line of the 64 LDS banks)
+//    with 16-byte chunks XOR-swizzled: K by row & 15, so the 16 rows one
+//    LDS pass of a ds_read_b128 fragment read serves hit 16 distinct bank
+//    groups (measured: no conflicts on K), V by 2 (row & 7) for the
+//    transposed ds_read_b64_tr_b16 reads;
 //  * lazy rescale: the exponentials are taken against a per-query reference
 //    max that moves only when a score exceeds it by more than 2^8 in the
 //    log2 domain; the common path computes no block max at all (a lane sum
@@ -196,9 +197,10 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_d128(
   // 16 (w >> 1) + 4 j + lane / 16 (j = 0..3) of the K and V blocks of key
   // half w & 1 (block 2t + (w & 1)), 4 + 4 instructions of 1 KiB per wave
   // and iteration.  Lane l writes chunk position l % 16, so it loads global
-  // chunk (l % 16) ^ swz(row), swz(row) = 2 (row & 7) = 8 (j & 1) + 2 (l >> 4),
-  // which keeps the K fragment reads (ds_read_b128) and the transposed V
-  // reads (ds_read_b64_tr_b16) free of bank conflicts.  One buffer resource
+  // chunk (l % 16) ^ swz(row): for K swz(row) = row & 15 = 4 j + (l >> 4),
+  // which keeps the K fragment reads (ds_read_b128, 16 rows per LDS pass)
+  // free of bank conflicts; for V swz(row) = 2 (row & 7) = 8 (j & 1) +
+  // 2 (l >> 4), for the transposed reads (ds_read_b64_tr_b16).  One buffer resource
   // per block, based at the block and sized to its rows (the hardware range
   // check covers the lane offset, not the scalar one), so rows of a partial
   // last block past kv_len read as zero.
@@ -212,9 +214,10 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_d128(
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int row = 16 * dq + 4 * j + (lane >> 4);
-    const uint32_t chunk = (uint32_t)(((lane & 15) ^ (8 * (j & 1) + 2 * (lane >> 4))) << 4);
-    dma_off_k[j] = (uint32_t)(row * k_rs * 2) + chunk;
-    dma_off_v[j] = (uint32_t)(row * v_rs * 2) + chunk;
+    const uint32_t chunk_k = (uint32_t)(((lane & 15) ^ (4 * j + (lane >> 4))) << 4);  // row & 15
+    const uint32_t chunk_v = (uint32_t)(((lane & 15) ^ (8 * (j & 1) + 2 * (lane >> 4))) << 4);  // 2 (row & 7)
+    dma_off_k[j] = (uint32_t)(row * k_rs * 2) + chunk_k;
+    dma_off_v[j] = (uint32_t)(row * v_rs * 2) + chunk_v;
   }
   // this wave's share of iteration t's blocks (t clamped to the last
   // iteration, the block to the late block's last: loads past the end are
@@ -290,14 +293,14 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_d128(
     }
     // LDS byte offsets within a 16 KiB block:
     //  K (d-step s, key tile kt): row 32 kt + l32, chunk 2 s + g2,
-    //    swz = 2 (l32 & 7)  ->  ko[s] + kt * 8192
+    //    swz = l32 & 15  ->  ko[s] + kt * 8192
     //  V^T (d tile dt, k-step ks, half hi): in 16-lane group q16 = lane / 16
     //    lane i reads row 16 ks + 8 hi + 4 g2 + i / 4, d 32 dt + 16 (q16 % 2)
     //    + 4 (i % 4) and receives d 32 dt + l32 at keys 16 ks + 8 hi + 4 g2
     //    + [0,4)  ->  vo[dt] + (16 ks + 8 hi) * 256
     uint32_t ko[8], vo[4];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) ko[s] = (uint32_t)(l32 * 256 + (((2 * s + g2) ^ (2 * (l32 & 7))) << 4));
+    for (int s = 0; s < 8; ++s) ko[s] = (uint32_t)(l32 * 256 + (((2 * s + g2) ^ (l32 & 15)) << 4));
     {
       const int q16 = lane >> 4, i16 = lane & 15;
       const int vrow = 4 * g2 + (i16 >> 2);
@@ -517,14 +520,14 @@ __global__ __launch_bounds__(THREADS) void fa_prefill_d128(
     }
     // LDS read offsets (bytes within a 16 KiB block), per lane:
     //  K (A operand, k-step s, key tile kt): row kt*16 + l16, chunk 4 s + g,
-    //    swz = 2 (l16 & 7)  ->  k_off[s] + kt * 4096
+    //    swz = l16  ->  k_off[s] + kt * 4096
     //  V^T (A operand via ds_read_b64_tr_b16, k-step s, key half hx, d tile
     //    dt): lane reads row 32 s + 16 hx + 4 g + l16/4, d 16 dt + 4 (l16 % 4)
     //    (chunk 2 dt + (l16/2) % 2, byte 8 (l16 % 2));
     //    swz = 8 (g % 2) + 2 (l16 / 4)  ->  v_off[dt] + (32 s + 16 hx) * 256
     uint32_t k_off[4], v_off[8];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) k_off[s] = (uint32_t)(l16 * 256 + (((4 * s + g) ^ (2 * (l16 & 7))) << 4));
+    for (int s = 0; s < 4; ++s) k_off[s] = (uint32_t)(l16 * 256 + (((4 * s + g) ^ l16) << 4));
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
       v_off[dt] = (uint32_t)((4 * g + (l16 >> 2)) * 256 +
