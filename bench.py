@@ -171,7 +171,7 @@ def causal_flops(heads, s, d):
 TX81_28x2048_MS = 3.649  # docs/attention-optimization-retrospective.md:9 (TX81, 16 tiles)
 
 
-def bench_fa_cases(torch, hip, steps, warmup):
+def bench_fa_cases(torch, hip, steps, warmup, with_cpu=True):
     """FA on the shapes and formats the reference's own attention cases use:
     config 1 in F16 through the plain entry (the dedicated head_dim-128
     kernel), config 1 through the masked entry in F16 and BF16 (the fa_fwd
@@ -204,6 +204,21 @@ def bench_fa_cases(torch, hip, steps, warmup):
         if ref_ms is not None:
             e["reference_published_ms"] = ref_ms
             e["speedup_vs_reference_published"] = ref_ms / ms
+        if with_cpu:
+            # the oracle of the same entry (masked: the masked-attention
+            # restatement) on a bounded sample of the heads
+            from oracle import oracle as orc
+            heads = min(shape[1], 4)
+            qs, ks, vs = (t[:, :heads].contiguous().cpu().view(torch.int16).numpy().view("uint16") for t in (q, k, v))
+            t0 = time.perf_counter()
+            if masked:
+                orc.attention_prefill_ex(qs, ks, vs, scale, causal=True, fmt=fmt, nthreads=cores())
+            else:
+                orc.attention_prefill(qs, ks, vs, scale, causal=True, block_k=64, fmt=fmt, nthreads=cores())
+            cdt = time.perf_counter() - t0
+            e["cpu_baseline"] = {"value": fl * heads / shape[1] / cdt / 1e12, "unit": "TFLOP/s", "cores": cores(),
+                                 "kind": "port",
+                                 "sample": f"{heads} of {shape[1]} heads of the same shape, {cdt:.2f} s wall"}
         legs.append(e)
 
     leg("fa_prefill_f16_config1", "fa_prefill_d128<_Float16, true, false>", FA_SHAPE, F16, False)
@@ -611,14 +626,14 @@ def main() -> int:
     if "fa" in only:
         fa = bench_fa(torch, hip, args.steps, args.warmup, with_cpu)
     if "fa_cases" in only:
-        secondary.append(dict(name="fa_cases", **bench_fa_cases(torch, hip, args.steps, args.warmup)))
+        secondary.append(dict(name="fa_cases", **bench_fa_cases(torch, hip, args.steps, args.warmup, with_cpu)))
     if "fd" in only:
         secondary.append(dict(name="fd_decode", **bench_fd(torch, hip, args.steps, args.warmup, with_cpu)))
     if "i8" in only:
         secondary.append(dict(name="gemm_i8", **bench_i8(torch, hip, args.steps, args.warmup, with_cpu)))
     if "mlp" in only:
         secondary.append(dict(name="mlp_fp32", **bench_mlp(torch, hip, B, args.steps, args.warmup, with_cpu)))
-        secondary.append(dict(name="mlp_fp32_formal", **bench_mlp(torch, hip, B, args.steps, args.warmup, False,
+        secondary.append(dict(name="mlp_fp32_formal", **bench_mlp(torch, hip, B, args.steps, args.warmup, with_cpu,
                                                                   lane="formal")))
     if "llama" in only:
         secondary.append(dict(name="llama_layer", **bench_llama(torch, hip, args.steps, args.warmup, with_cpu)))
