@@ -289,6 +289,27 @@ template <uint32_t F> __device__ inline void load8(const void *b, int64_t i, flo
     }
   }
 }
+// load8 with non-temporal loads, for streams read exactly once (no L2
+// allocation for data nothing reads again)
+template <uint32_t F> __device__ inline void load8_nt(const void *b, int64_t i, float (&v)[8]) {
+  if constexpr (F == WAFER_FMT_F32) {
+    const u32x4 lo = __builtin_nontemporal_load((const u32x4 *)b + i / 4);
+    const u32x4 hi = __builtin_nontemporal_load((const u32x4 *)b + i / 4 + 1);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = u2f(lo[e]);
+      v[4 + e] = u2f(hi[e]);
+    }
+  } else {
+    const u32x4 w = __builtin_nontemporal_load((const u32x4 *)b + i / 8);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint16_t l = (uint16_t)(w[e] & 0xffffu), h = (uint16_t)(w[e] >> 16);
+      v[2 * e] = F == WAFER_FMT_BF16 ? bf16_to_f32(l) : f16_to_f32(l);
+      v[2 * e + 1] = F == WAFER_FMT_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+    }
+  }
+}
 template <uint32_t F> __device__ inline void store8(void *b, int64_t i, const float (&v)[8]) {
   if constexpr (F == WAFER_FMT_F32) {
     u32x4 lo, hi;

@@ -79,8 +79,8 @@ __global__ __launch_bounds__(256) void ew_kernel(const void *__restrict__ in0,
     const uint64_t groups = count / 8;
     for (uint64_t q = gid; q < groups; q += stride) {
       float a[8], b[8], r[8];
-      load8<F>(in0, (int64_t)(8 * q), a);
-      if (in1) load8<F>(in1, (int64_t)(8 * q), b);
+      load8_nt<F>(in0, (int64_t)(8 * q), a);
+      if (in1) load8_nt<F>(in1, (int64_t)(8 * q), b);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         r[e] = ew_eval<OP>(a[e], in1 ? b[e] : 0.0f);
