@@ -751,9 +751,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 // 1024 / SB rows: lane l writes chunk position l % (SB / 16) of its row, so
 // it loads the global chunk that the swizzle maps there.  Chunk c of row r
 // sits at position c ^ swz(r), swz a function of r % 16 ((r >> 2) & 3 for
-// 64-byte rows, r & 7 for 128-byte rows): each fragment address is a
-// per-lane base per k-step plus an immediate per 32-row tile, and the rows
-// one fragment read touches hit distinct 16-byte bank groups.  One barrier
+// 64-byte rows, (r >> 1) & 7 for 128-byte rows): each fragment address is a
+// per-lane base per k-step plus an immediate per 32-row tile, and the 16
+// rows one LDS pass of a fragment read serves hit distinct 16-byte bank
+// groups.  One barrier
 // per stage, before its last k-step: it publishes stage kt+1 and frees
 // stage kt's slot.  Each stage's moves go out in two halves spread over the
 // MFMA slots of two k-steps (a burst of them fills the texture address
