@@ -114,6 +114,18 @@ def f32_to_bf16(x: np.ndarray) -> np.ndarray:
     return r
 
 
+def f32_to_f16(x: np.ndarray) -> np.ndarray:
+    """Float32 -> f16 bits through oracle_f32_to_f16 (RNE, overflow to inf,
+    gradual underflow), a NaN set to the codec's 0x7e00 as store_float does."""
+    src = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.empty(src.size, dtype=np.uint16)
+    h = ctypes.c_uint16()
+    f = lib().oracle_f32_to_f16
+    for i, v in enumerate(src.tolist()):
+        out[i] = h.value if f(v, ctypes.byref(h)) == 0 else 0x7E00
+    return out
+
+
 def bf16_to_f32(b: np.ndarray) -> np.ndarray:
     return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 

@@ -606,6 +606,68 @@ def test_mfma_gemm_bf16_narrowing_bit_exact(hip, B, oracle, m, n):
     assert np.array_equal(got, np.broadcast_to(want, got.shape))
 
 
+def _f16_narrowing_cases(rng, n):
+    """f16 triples (x, y, z) whose exact f32 sum x + y + z * 2^-14 lands on
+    the cases f16 RNE narrowing has to get right: ties to even, just below
+    and above a tie, carries into the exponent, 65504 + 16 (ties to inf) and
+    65504 + 8 (stays finite), subnormal results that tie, round up or
+    underflow to a signed zero (x a subnormal input, z * 2^-14 a fraction of
+    the smallest subnormal), infinities and NaNs."""
+    e = rng.integers(-10, 16, n)
+    mant = rng.integers(0, 1024, n)
+    sign = rng.choice([-1.0, 1.0], n)
+    x = sign * (1.0 + mant / 1024.0) * np.exp2(e.astype(np.float64))
+    half = np.exp2(e - 11.0)
+    kind = rng.integers(0, 5, n)
+    y = sign * np.select([kind == 0, kind == 1, kind == 2, kind == 3], [half, 0.75 * half, 1.5 * half, -half],
+                         0.375 * half)
+    z = np.zeros(n)
+    x[:64] = sign[:64] * 65504.0
+    y[:32] = sign[:32] * 16.0
+    y[32:64] = sign[32:64] * 8.0
+    sub = slice(72, 200)
+    x[sub] = sign[sub] * rng.integers(0, 1024, 128) * 2.0 ** -24
+    x[72:80] = sign[72:80] * 0.0                                   # the sum alone: underflow to a signed zero
+    y[sub] = 0.0
+    z[sub] = sign[sub] * rng.choice([2.0 ** -11, 1.5 * 2.0 ** -11, 2.0 ** -12, 0.75 * 2.0 ** -11], 128)
+    bits = [v.astype(np.float16).view(np.uint16) for v in (x, y, z)]
+    for v, b in zip((x, y, z), bits):
+        assert np.array_equal(b.view(np.float16).astype(np.float64), v)  # every operand is an f16 value
+    bits[0][64:72] = [0x7C00, 0xFC00, 0x7E00, 0x7D01, 0xFE13, 0x7C01, 0x0000, 0x8000]  # inf, NaN payloads, zeros
+    return bits
+
+
+@pytest.mark.parametrize("m,n", [(4096, 4096), (1024, 6144), (1024, 4096)])
+def test_mfma_gemm_f16_narrowing_bit_exact(hip, B, oracle, m, n):
+    """The staged epilogues narrow f32 to f16 with the hardware conversion
+    (RNE, overflow to inf, gradual underflow) and set NaNs to the codec's
+    0x7e00.  Every output is an exact f32 sum x + y + z * 2^-14 (A rows
+    [1, 1, 2^-14, 0 ...], Bt rows [x, y, z, 0 ...], k = 64) chosen on RNE's
+    edge cases, so the narrowed output must equal the oracle's f16 narrowing
+    of that sum bit for bit; the subnormal x also pin that the f16 MFMA keeps
+    subnormal inputs (256x256 tiles at 4096 x 4096, 128x192 at 1024 x 6144,
+    128x128 at 1024 x 4096)."""
+    say("mfma gemm f16 narrowing", m, n)
+    rng = np.random.default_rng(m + 3 * n)
+    K = 64
+    xb, yb, zb = _f16_narrowing_cases(rng, n)
+    a = np.zeros((m, K), dtype=np.uint16)
+    a[:, 0] = a[:, 1] = 0x3C00
+    a[:, 2] = 0x0400
+    bt = np.zeros((n, K), dtype=np.uint16)
+    bt[:, 0], bt[:, 1], bt[:, 2] = xb, yb, zb
+    dst = torch.full((m, n), 0x1234, dtype=torch.int16, device="cuda")
+    hip.gemm_mfma(u16(a), u16(bt), dst, m, K, n, in_fmt=B.F16, out_fmt=B.F16, rhs_t=True)
+    got = host(dst).view(np.uint16)
+    f = [oracle.to_float(B.F16, v).astype(np.float64) for v in (xb, yb, zb)]
+    with np.errstate(invalid="ignore"):
+        exact = f[0] + f[1] + f[2] * 2.0 ** -14
+    assert np.all(np.isnan(exact) | np.isinf(exact) | (exact.astype(np.float32).astype(np.float64) == exact))
+    want = oracle.f32_to_f16(exact.astype(np.float32))
+    assert np.array_equal(got[0], want), np.nonzero(got[0] != want)[0][:8]
+    assert np.array_equal(got, np.broadcast_to(want, got.shape))
+
+
 @pytest.mark.parametrize("m,n,out,K", [(1024, 6144, 3, 256), (1024, 6144, 5, 256), (512, 12288, 3, 256),
                                        (1024, 6144, 3, 320), (1024, 6144, 5, 64)])
 def test_mfma_gemm_192_tiles_vs_formal(hip, B, oracle, m, n, out, K):

@@ -329,3 +329,30 @@ def test_pool_single_element_window_copies_bits():
     assert list(got.ravel()) == list(src.ravel())  # no combine: raw NaN payloads survive
     got = o.pool(116, F32, src, (2, 2), (1, 1, 1, 1))
     assert list(got.ravel()) == [NAN[F32], 0, 0x3F800000, NAN[F32]]  # +0 + -0 = +0
+
+
+def test_f32_to_f16_matches_ieee_rne():
+    """oracle.f32_to_f16 (the narrowing of every F16 store) against numpy's
+    IEEE round-to-nearest-even cast on the values that decide it: ties with
+    even and odd mantissas, just off a tie, carries into the exponent, the
+    overflow edge 65504 + 16 (ties to inf) and 65504 + 8 (stays finite),
+    subnormal ties and underflow, plus random bit patterns over the range."""
+    rng = np.random.default_rng(7)
+    h = rng.integers(0, 0x7C00, 4096).astype(np.uint16)      # finite f16, both signs below
+    base = h.view(np.float16).astype(np.float32)
+    ulp = np.spacing(h.view(np.float16)).astype(np.float32)
+    frac = rng.choice(np.array([0.5, 0.5 - 2.0 ** -12, 0.5 + 2.0 ** -12, 0.25, 0.75], np.float32), h.size)
+    x = np.concatenate([base + frac * ulp, -(base + frac * ulp),
+                        rng.integers(0, 2 ** 32, 4096, dtype=np.uint64).astype(np.uint32).view(np.float32),
+                        np.array([65504 + 16, 65504 + 8, 65504 + 15.99, -65520, 2.0 ** -25, 1.5 * 2.0 ** -25,
+                                  2.0 ** -26, 1023 * 2.0 ** -24 + 2.0 ** -25, 3 * 2.0 ** -25, np.inf, -np.inf,
+                                  0.0, -0.0, 1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11], np.float32)])
+    got = o.f32_to_f16(x)
+    nan = np.isnan(x)
+    assert (got[nan] == NAN[F16]).all()
+    with np.errstate(over="ignore"):
+        want = x[~nan].astype(np.float16).view(np.uint16)
+    assert np.array_equal(got[~nan], want), np.nonzero(got[~nan] != want)[0][:8]
+    assert list(got[-15:-10]) == [0x7C00, 0x7BFF, 0x7BFF, 0xFC00, 0x0000]
+    assert list(got[-10:-4]) == [0x0001, 0x0000, 0x0400, 0x0002, 0x7C00, 0xFC00]
+    assert list(got[-2:]) == [0x3C00, 0x3C02]
