@@ -378,12 +378,17 @@ gemm_nt_kernel(GemmArgs args) {
   constexpr int CH = SB / 16, KS = SB / 32;
   constexpr int NS = (128 * 1024) / ((BM + BN) * SB) < 4 ? (128 * 1024) / ((BM + BN) * SB) : 4;
   static_assert(NS >= 2, "at least two stages");
-  __shared__ __align__(16) u32x4 sA[NS][BM * CH];
-  __shared__ __align__(16) u32x4 sB[NS][BN * CH];
+  // one LDS object holding the A stages, then the B stages
+  __shared__ __align__(1024) uint8_t lds[NS * (BM + BN) * SB];
+  u32x4 (*const sA)[BM * CH] = (u32x4 (*)[BM * CH])lds;
+  u32x4 (*const sB)[BN * CH] = (u32x4 (*)[BN * CH])(lds + NS * BM * SB);
   // 16-byte chunk c of row r sits at position swz(r, c) (an involution in c):
   // 16 consecutive rows read at one chunk hit 16 distinct 16-byte bank
   // groups, and so do 32 consecutive rows for 128-byte rows
+  // (BKN: chunk ^ ((row >> 1) & 7), a function of row % 16, so the DMA's
+  // per-lane offsets take two forms, by instruction parity)
   auto swz = [](int row, int chunk) __attribute__((always_inline)) {
+    if constexpr (BKN) return chunk ^ ((row >> 1) & 7);
     return SB == 64 ? chunk ^ ((row >> 2) & 3) : chunk ^ (((row >> 1) ^ (row >> 4)) & 7);
   };
 
@@ -422,10 +427,53 @@ gemm_nt_kernel(GemmArgs args) {
   // last row of the tile that exists in A / Bt (BM - 1 / BN - 1 unless TAIL)
   const int last_a = TAIL ? min(BM, args.m - m0) - 1 : BM - 1;
   const int last_b = TAIL ? min(BN, args.n - n0) - 1 : BN - 1;
+  // BKN: buffer-resource DMA with a scalar offset per instruction.  Each
+  // wave moves PA instructions of A, then PB of B, so the operand of an
+  // issue slot is known at compile time; the per-lane offsets are set up
+  // once, two forms each by instruction parity (the A swizzle and the B
+  // k-row swizzle repeat every 16 rows / 8 k-rows).  The offsets are 32-bit:
+  // the entry keeps K * N below 2^31 on this path.
+  constexpr int PA = BKN ? A_INSTR / NW : 0, PB = BKN ? B_INSTR / NW : 0;
+  static_assert(!BKN || (SB == 128 && A_INSTR % NW == 0 && B_INSTR % NW == 0 && PA + PB == PER_WAVE &&
+                         PA % 2 == 0 && PB % 2 == 0), "BKN DMA: whole, even instruction shares per wave");
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc((void *)abase, 0, BKN ? BM * (int)kb32 : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb =
+      __builtin_amdgcn_make_buffer_rsrc((void *)bbase, 0, BKN ? (int)(kb32 * npitch - (uint32_t)n0) : 0, 0x00020000);
+  int voa[2] = {0, 0}, vob[2] = {0, 0};
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  if constexpr (BKN) {
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+      const int r16 = par * RPI + lane / CH;           // A row within its 16-row group
+      voa[par] = (lane / CH) * (int)kb32 + (((lane % CH) ^ ((r16 >> 1) & 7)) << 4);
+      const int kr8 = par * (1024 / BN) + lane / 16;  // B k-row within its 8-row group
+      vob[par] = (lane / 16) * (int)npitch + (((lane & 15) ^ (2 * kr8)) << 4);
+    }
+  }
   // instructions q0 .. q1-1 of this wave's PER_WAVE for stage kt
   auto issue = [&](int kt, int q0, int q1) __attribute__((always_inline)) {
     const int st = kt % NS;
     const uint32_t koff = (uint32_t)min(kt, nkt - 1) * SB;
+    if constexpr (BKN) {
+#pragma unroll
+      for (int q = q0; q < q1; ++q) {
+        if (q < PA) {
+          const int rel = wv * PA + q;
+          const int soff = __builtin_amdgcn_readfirstlane(rel * RPI * (int)kb32 + (int)koff);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              ra, (__attribute__((address_space(3))) void *)((char *)&sA[st][0] + rel * 1024), 16, voa[q & 1],
+              soff, 0, 0);
+        } else {
+          const int rel = wv * PB + (q - PA);
+          const int soff = __builtin_amdgcn_readfirstlane(((int)koff + rel * (1024 / BN)) * (int)npitch);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rb, (__attribute__((address_space(3))) void *)((char *)&sB[st][0] + rel * 1024), 16,
+              vob[(q - PA) & 1], soff, 0, 0);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int q = q0; q < q1; ++q) {
       const int ins = wave * PER_WAVE + q;  // 0 .. A_INSTR + B_INSTR - 1
@@ -433,15 +481,7 @@ gemm_nt_kernel(GemmArgs args) {
       const int row = (is_a ? ins : ins - A_INSTR) * RPI + dma_row;
       const int chunk = swz(row, dma_pos);
       const int src_row = TAIL ? min(row, is_a ? last_a : last_b) : row;
-      const uint8_t *src;
-      if constexpr (BKN) {
-        // B: k-row koff + kr, 16-byte chunks of a 256-byte row
-        const int kr = (ins - A_INSTR) * (1024 / BN) + lane / 16;
-        const uint32_t loff = is_a ? src_row * kb32 + chunk * 16 : kr * npitch + (((lane & 15) ^ (2 * (kr & 7))) * 16);
-        src = (is_a ? abase + koff : bbase + (size_t)koff * npitch) + loff;
-      } else {
-        src = (is_a ? abase : bbase) + (src_row * kb32 + koff + chunk * 16);
-      }
+      const uint8_t *src = (is_a ? abase : bbase) + (src_row * kb32 + koff + chunk * 16);
       u32x4 *dst = is_a ? &sA[st][(ins * RPI) * CH] : &sB[st][((ins - A_INSTR) * RPI) * CH];
       __builtin_amdgcn_global_load_lds((const void *)src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
     }
@@ -455,26 +495,10 @@ gemm_nt_kernel(GemmArgs args) {
       const int row = wm * (BM / WM) + i * 32 + l32;
       fa[f][i] = sA[buf][row * CH + swz(row, chunk)];
     }
-    if constexpr (BKN) {
-      // k-rows 32 ks + 16 g + 8 h + lane % 16 / 2 (h = 0, 1), chunk of
-      // columns wn * BN / WN + 32 j + 16 (lane / 16 % 2); the row's swizzle
-      // is 2 (row & 7) = 2 (lane % 16 / 2)
-      const char *sb = (const char *)&sB[buf][0];
-      const int l16 = lane & 15;
 #pragma unroll
-      for (int j = 0; j < WTN; ++j) {
-        const int c = (wn * (BN / WN) + j * 32) / 16 + ((lane >> 4) & 1);
-        const int off = (ks * 32 + 16 * g + (l16 >> 1)) * BN + ((c ^ (2 * (l16 >> 1))) * 16) + 8 * (l16 & 1);
-        const v2i32 lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i32 *)(sb + off));
-        const v2i32 hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i32 *)(sb + off + 8 * BN));
-        fb[f][j] = __builtin_bit_cast(u32x4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3));
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < WTN; ++j) {
-        const int row = wn * (BN / WN) + j * 32 + l32;
-        fb[f][j] = sB[buf][row * CH + swz(row, chunk)];
-      }
+    for (int j = 0; j < WTN; ++j) {
+      const int row = wn * (BN / WN) + j * 32 + l32;
+      fb[f][j] = sB[buf][row * CH + swz(row, chunk)];
     }
   };
   auto mfmas = [&](int f) __attribute__((always_inline)) {
@@ -491,56 +515,153 @@ gemm_nt_kernel(GemmArgs args) {
   // keep the compiler from moving MFMAs across the barrier; sched_group_barrier
   // pins the interleave (masks: 0x008 MFMA, 0x100 LDS read, 0x010 VMEM,
   // which covers the DMA issues).
-  constexpr int NR = WTM + (BKN ? 2 : 1) * WTN;  // fragment reads per k-step
-  constexpr int DKS = KS > 2 ? KS - 2 : 1;       // k-steps that carry DMA issues
-  constexpr int NV = (PER_WAVE + DKS - 1) / DKS;  // DMA issues per such k-step
+  if constexpr (BKN) {
+    // [K,N] rhs: every B fragment of a stage is read right after the
+    // barrier that makes the stage visible (k-steps 0 .. KS-2, k-step KS-1's
+    // at the start of k-step 0), and the next stage's DMA moves go out only
+    // after them.  ds_read_b64_tr_b8 carries no LDS alias information, so the
+    // compiler puts an s_waitcnt vmcnt(0) before each one issued while an LDS
+    // DMA may be in flight; read this way, every such wait falls where the
+    // stage barrier has already drained the DMA.  A fragments (plain LDS
+    // loads) keep the per-k-step pipeline.
+    u32x4 fbs[KS][WTN];
+    const char *sbb = (const char *)&sB[0][0];
+    const int l16 = lane & 15;
+    // k-rows 32 ks + 16 g + 8 h + lane % 16 / 2 (h = 0, 1), chunk of
+    // columns wn * BN / WN + 32 j + 16 (lane / 16 % 2); the row's swizzle
+    // is 2 (row & 7) = 2 (lane % 16 / 2)
+    auto read_b = [&](int buf, int ks) __attribute__((always_inline)) {
 #pragma unroll
-  for (int s = 0; s < NS - 1; ++s) issue(s, 0, PER_WAVE);
-  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE) : "memory");
-  read_frags(0, 0, 0);
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int buf = kt % NS;
+      for (int j = 0; j < WTN; ++j) {
+        const int c = (wn * (BN / WN) + j * 32) / 16 + ((lane >> 4) & 1);
+        const int off = buf * (SB * BN) + (ks * 32 + 16 * g + (l16 >> 1)) * BN + ((c ^ (2 * (l16 >> 1))) * 16) +
+                        8 * (l16 & 1);
+        const v2i32 lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i32 *)(sbb + off));
+        const v2i32 hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i32 *)(sbb + off + 8 * BN));
+        fbs[ks][j] = __builtin_bit_cast(u32x4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3));
+      }
+    };
+    auto read_a = [&](int buf, int ks, int f) __attribute__((always_inline)) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int cur = ks & 1;
-      if (ks < KS - 1) {
-        read_frags(buf, ks + 1, cur ^ 1);
-        mfmas(cur);
-        // into buffer (kt - 1) % NS, which every wave finished reading
-        // before the last barrier
-        if (ks < DKS) issue(kt + NS - 1, min(ks * NV, PER_WAVE), min((ks + 1) * NV, PER_WAVE));
+      for (int i = 0; i < WTM; ++i) {
+        const int row = wm * (BM / WM) + i * 32 + l32;
+        fa[f][i] = sA[buf][row * CH + swz(row, ks * 2 + g)];
+      }
+    };
+    auto mfmas_b = [&](int f, int ks) __attribute__((always_inline)) {
 #pragma unroll
-        for (int r = 0; r < NR; ++r) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          if (ks < DKS && r < NV) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
-        }
-        if (ks < DKS && NV > NR) {
+      for (int i = 0; i < WTM; ++i)
 #pragma unroll
-          for (int v = NR; v < NV; ++v) {
+        for (int j = 0; j < WTN; ++j) acc[i][j] = mfma<KIND>(fa[f][i], fbs[ks][j], acc[i][j]);
+    };
+    constexpr int NM = WTM * WTN;
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) issue(s, 0, PER_WAVE);
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE) : "memory");
+    read_a(0, 0, 0);
+#pragma unroll
+    for (int ks = 0; ks < KS - 1; ++ks) read_b(0, ks);
+    for (int kt = 0; kt < nkt; ++kt) {
+      const int buf = kt % NS;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int cur = ks & 1;
+        if (ks == 0) {
+          // the stage's last B fragments, then stage kt+NS-1's moves into
+          // slot (kt-1) % NS, which every wave finished reading before the
+          // last barrier
+          read_b(buf, KS - 1);
+          read_a(buf, 1, cur ^ 1);
+          mfmas_b(cur, 0);
+          issue(kt + NS - 1, 0, PER_WAVE);
+          __builtin_amdgcn_sched_group_barrier(0x100, 2 * WTN, 0);
+#pragma unroll
+          for (int t = 0; t < NM; ++t) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+            if (t < WTM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (t < PER_WAVE) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
           }
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
-        __builtin_amdgcn_sched_barrier(0);
-      } else {
-        // this wave's stage-(kt+1) loads have landed (the NS-2 later stages
-        // may stay in flight) and its reads of stage kt are complete; after
-        // the barrier stage kt+1 is visible to every wave and buffer kt % NS
-        // is free
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE) : "memory");
-        __builtin_amdgcn_sched_barrier(0);
-        // stage kt+1's first fragments (past the last stage a clamped copy, unused)
-        read_frags((kt + 1) % NS, 0, cur ^ 1);
-        mfmas(cur);
+          __builtin_amdgcn_sched_barrier(0);
+        } else if (ks < KS - 1) {
+          read_a(buf, ks + 1, cur ^ 1);
+          mfmas_b(cur, ks);
 #pragma unroll
-        for (int r = 0; r < NR; ++r) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          for (int t = 0; t < NM; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (t < WTM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        } else {
+          // stage kt+1 has landed for this wave and its reads of stage kt
+          // are complete; after the barrier stage kt+1 is visible to every
+          // wave (past the last stage a clamped copy, read but unused)
+          asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE) : "memory");
+          __builtin_amdgcn_sched_barrier(0);
+          read_a((kt + 1) % NS, 0, cur ^ 1);
+#pragma unroll
+          for (int k2 = 0; k2 < KS - 1; ++k2) read_b((kt + 1) % NS, k2);
+          mfmas_b(cur, KS - 1);
+#pragma unroll
+          for (int t = 0; t < NM; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, (WTM + 2 * WTN * (KS - 1) + NM - 1) / NM, 0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
-        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  } else {
+    constexpr int NR = WTM + WTN;                  // fragment reads per k-step
+    constexpr int DKS = KS > 2 ? KS - 2 : 1;       // k-steps that carry DMA issues
+    constexpr int NV = (PER_WAVE + DKS - 1) / DKS;  // DMA issues per such k-step
+  #pragma unroll
+    for (int s = 0; s < NS - 1; ++s) issue(s, 0, PER_WAVE);
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE) : "memory");
+    read_frags(0, 0, 0);
+    for (int kt = 0; kt < nkt; ++kt) {
+      const int buf = kt % NS;
+  #pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int cur = ks & 1;
+        if (ks < KS - 1) {
+          read_frags(buf, ks + 1, cur ^ 1);
+          mfmas(cur);
+          // into buffer (kt - 1) % NS, which every wave finished reading
+          // before the last barrier
+          if (ks < DKS) issue(kt + NS - 1, min(ks * NV, PER_WAVE), min((ks + 1) * NV, PER_WAVE));
+  #pragma unroll
+          for (int r = 0; r < NR; ++r) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (ks < DKS && r < NV) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+          }
+          if (ks < DKS && NV > NR) {
+  #pragma unroll
+            for (int v = NR; v < NV; ++v) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+              __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+            }
+          }
+          __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        } else {
+          // this wave's stage-(kt+1) loads have landed (the NS-2 later stages
+          // may stay in flight) and its reads of stage kt are complete; after
+          // the barrier stage kt+1 is visible to every wave and buffer kt % NS
+          // is free
+          asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE) : "memory");
+          __builtin_amdgcn_sched_barrier(0);
+          // stage kt+1's first fragments (past the last stage a clamped copy, unused)
+          read_frags((kt + 1) % NS, 0, cur ^ 1);
+          mfmas(cur);
+  #pragma unroll
+          for (int r = 0; r < NR; ++r) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
+          __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     }
   }
@@ -1343,8 +1464,9 @@ extern "C" int wafer_hip_gemm_i8(wafer_hip_context *ctx, const int8_t *a, const 
   WAFER_TRY(check_hip(hipSetDevice(ctx->device), "hipSetDevice"));
   const uint8_t *bt = (const uint8_t *)b;
   // a [K, N] rhs on whole 256x256 tiles that fill the chip: read in place
+  // (K * N below 2^31: the kernel's buffer offsets are 32-bit)
   if (rhs_orientation == WAFER_GEMM_NORMAL && m % 256 == 0 && n % 256 == 0 && k % 128 == 0 &&
-      (m / 256) * (n / 256) >= 192) {
+      (m / 256) * (n / 256) >= 192 && (uint64_t)k * n < (1ull << 31)) {
     GemmArgs args{(const uint8_t *)a, bt, y, acc_out, scale, (int)m, (int)n, (int)k, 0, 0};
     args.tiles_m = (int)(m / 256);
     args.tiles_n = (int)(n / 256);
