@@ -382,13 +382,13 @@ def test_i8_gemm_baseline_size_y_only(hip, B, oracle, rt):
     assert np.array_equal(host(acc).astype(np.int64).sum(0), colsum)
 
 
-@pytest.mark.parametrize("m,k,n", [(3072, 128, 4096), (4096, 384, 3072), (4096, 1152, 4096)])
+@pytest.mark.parametrize("m,k,n", [(3072, 128, 4096), (4096, 256, 3072), (4096, 384, 3072), (4096, 1152, 4096)])
 def test_i8_gemm_kn_rhs_in_place(hip, B, oracle, m, k, n):
     """A [K, N] rhs on >= 192 whole 256x256 tiles is read in place (the
     transposing LDS reads, no re-layout pass): y and the accumulator over
     the whole output equal the run on the same rhs stored [N, K], and the
-    int64 closed form on sampled rows; one, three and nine 128-byte K
-    stages."""
+    int64 closed form on sampled rows; one, two, three and nine 128-byte K
+    stages (the two-slot ring's first, even and odd stage counts)."""
     say("i8 gemm [K,N] in place", m, k, n)
     rng = np.random.default_rng(m * 7 + k + n)
     a = rng.integers(-128, 128, size=(m, k), dtype=np.int64).astype(np.int8)
