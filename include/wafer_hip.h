@@ -202,9 +202,10 @@ int wafer_hip_gemm_f32_mfma(wafer_hip_context *ctx, const float *lhs,
  * a [m,k] i8, b [k,n] i8 (Transpose: [n,k]), scale [n] f32, y [m,n] bf16;
  * acc_out [m,n] i32 may be NULL.  Any m, n; k a multiple of 64 and at most
  * 131071 (|acc| <= k*128*128 < 2^31); other k are rejected.  A [k,n] b with
- * m and n multiples of 256, k of 128 and at least 192 tiles of 256x256 is
- * read in place (no workspace, so such calls may be captured); other [k,n]
- * shapes are re-laid out to [n,k] in the context's workspace first. */
+ * m and n multiples of 256, k of 128, at least 192 tiles of 256x256 and
+ * k*n below 2^31 is read in place (no workspace, so such calls may be
+ * captured); other [k,n] shapes are re-laid out to [n,k] in the context's
+ * workspace first. */
 int wafer_hip_gemm_i8(wafer_hip_context *ctx, const int8_t *a, const int8_t *b,
                       const float *scale, int32_t *acc_out, uint16_t *y,
                       uint32_t m, uint32_t k, uint32_t n,
