@@ -384,7 +384,9 @@ gemm_nt_kernel(GemmArgs args) {
   constexpr int CH = SB / 16, KS = SB / 32;
   constexpr int NS = (128 * 1024) / ((BM + BN) * SB) < 4 ? (128 * 1024) / ((BM + BN) * SB) : 4;
   static_assert(NS >= 2, "at least two stages");
-  // one LDS object holding the A stages, then the B stages
+  // one LDS object holding the A stages, then the B stages (with A and B in
+  // two objects the compiler put an s_waitcnt vmcnt before the A fragment
+  // reads for the A moves in flight)
   __shared__ __align__(1024) uint8_t lds[NS * (BM + BN) * SB];
   u32x4 (*const sA)[BM * CH] = (u32x4 (*)[BM * CH])lds;
   u32x4 (*const sB)[BN * CH] = (u32x4 (*)[BN * CH])(lds + NS * BM * SB);
